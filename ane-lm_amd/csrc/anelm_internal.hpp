@@ -1,0 +1,138 @@
+// Internal helpers shared by the libanelm HIP translation units: status and
+// error text, the per-device workspace, and wavefront (64-lane) primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/anelm.h"
+
+namespace anelm {
+
+// Records a thread-local error message and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Converts a HIP status into ANELM_EHIP with the failing call named.
+int hip_fail(hipError_t e, const char* what);
+
+#define ANELM_HIP(call)                                        \
+    do {                                                       \
+        hipError_t e_ = (call);                                \
+        if (e_ != hipSuccess) return ::anelm::hip_fail(e_, #call); \
+    } while (0)
+
+#define ANELM_REQUIRE(cond, ...)                                         \
+    do {                                                                 \
+        if (!(cond)) return ::anelm::set_error(ANELM_EINVAL, __VA_ARGS__); \
+    } while (0)
+
+#define ANELM_NONNULL(p)                                                      \
+    do {                                                                      \
+        if ((p) == nullptr) return ::anelm::set_error(ANELM_ENULL, "%s is NULL", #p); \
+    } while (0)
+
+// Launch check: reports the first launch error, if any.
+#define ANELM_LAUNCHED(name)                                      \
+    do {                                                          \
+        hipError_t e_ = hipGetLastError();                        \
+        if (e_ != hipSuccess) return ::anelm::hip_fail(e_, name); \
+    } while (0)
+
+// Per-device state.  `ws` is a growable scratch buffer (contents undefined
+// between calls); `counters` is a zeroed uint32 array that kernels use for
+// last-block-done reductions and always leave zeroed again.
+struct Device {
+    int id = -1;
+    int num_cus = 0;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    uint32_t* counters = nullptr;
+    size_t n_counters = 0;
+};
+
+// Current device's state (lazily initialised).  nullptr on failure with the
+// error recorded.
+Device* device();
+
+// Workspace of at least `bytes` on the current device (grows with a stream
+// sync + free + malloc).  Returns nullptr on failure with the error recorded.
+void* workspace(size_t bytes, hipStream_t stream);
+
+// `n` zeroed counters on the current device; nullptr if n exceeds the pool.
+uint32_t* counters(size_t n);
+
+constexpr size_t kCounterPool = 1 << 16;
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Host-side cos/sin for RoPE pair j at dim 2j, exactly the reference formula
+// (core/cpu_ops.cpp:51-55, models/llm/qwen3_5.cpp:311-321).
+void rope_row(float* cos_out, float* sin_out, int rot_dim, int pos, float theta);
+
+constexpr int kMaxRotPairs = 128;
+
+// ------------------------------------------------------------- device code
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+// RoPE pair rotation with separately rounded products, as the reference's
+// expression v0*c - v1*s evaluates without fused multiply-add
+// (core/cpu_ops.cpp:57-60).
+__device__ __forceinline__ void rotate_pair(float& o0, float& o1, float v0, float v1, float c,
+                                            float s) {
+#pragma clang fp contract(off)
+    o0 = v0 * c - v1 * s;
+    o1 = v0 * s + v1 * c;
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+// Full-wave (64-lane) sum; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64); `red` holds NT/64
+// floats of shared memory.  All threads receive the total.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i++) t += red[i];
+    return t;
+}
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+}  // namespace anelm

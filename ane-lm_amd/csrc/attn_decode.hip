@@ -1,0 +1,641 @@
+// Decode attention over a ring KV cache (fp16 or fp32), optionally fused with
+// the q/k RMSNorm + RoPE + ring append prologue and the sigmoid output gate.
+//
+// Reference semantics: core/cpu_ops.cpp:148-204 (gqa_attention) composed as in
+// models/llm/qwen3_5.cpp:944-1002.  The reference walks q heads one at a time
+// and re-reads K/V per q head; here one workgroup owns (kv head, key split) and
+// scores all G = Hq/Hkv query heads of that kv head against each K/V row read
+// once.  Splits are merged with the standard (max, sum, unnormalised output)
+// log-sum-exp combine, done by the last workgroup of each split group (two
+// levels), so the whole step is one launch.
+#include "anelm_internal.hpp"
+
+#include <algorithm>
+#include <math.h>
+
+namespace anelm {
+
+namespace {
+
+constexpr int kNT = 256;      // threads per workgroup
+constexpr int kNW = kNT / 64;  // waves per workgroup
+constexpr int kMaxKps = 512;  // keys per split held in LDS
+
+struct DecodeParams {
+    float* out;
+    const float* q;
+    int q_stride;
+    const void* k_cache;
+    const void* v_cache;
+    int n_kv_heads;
+    int start, len, cap;       // ring mode
+    float scale;
+    int kps, max_splits, cg, max_groups;
+    float* part;       // level-1 partials [seq][Hkv][max_splits][G][D+2]
+    float* part2;      // level-2 partials [seq][Hkv][max_groups][G][D+2]
+    uint32_t* cnt;     // [seq][Hkv][max_groups] level-1, then [seq][Hkv] level-2
+    // paged mode: pages [page][Hkv][page_size][D]; key t of sequence s is
+    // row t % page_size of page page_table[s*max_pages + t/page_size]
+    int paged;
+    const int32_t* page_table;
+    const int32_t* seq_lens;
+    int max_pages, page_size, n_pages, n_seqs;
+    // fused prologue (ring mode only)
+    int fused;
+    const float* q_norm_w;
+    const float* k_norm_w;
+    const float* k_new;
+    const float* v_new;
+    void* k_cache_w;
+    void* v_cache_w;
+    int new_slot;
+    float eps;
+    int rot_pairs, rope_mode, gate;
+    float cs[kMaxRotPairs];
+    float sn[kMaxRotPairs];
+};
+
+// Per-workgroup view of its sequence.
+struct SeqView {
+    const float* q;
+    float* out;
+    int len, n_splits, n_groups;
+    float* part;
+    float* part2;
+    uint32_t* cnt1;
+    uint32_t* cnt2;
+};
+
+template <typename KV> struct Raw8;
+template <> struct Raw8<uint16_t> { uint4 a; };
+template <> struct Raw8<float> { float4 a, b; };
+
+__device__ __forceinline__ Raw8<uint16_t> load_raw(const uint16_t* p) {
+    Raw8<uint16_t> r;
+    r.a = *reinterpret_cast<const uint4*>(p);
+    return r;
+}
+__device__ __forceinline__ Raw8<float> load_raw(const float* p) {
+    Raw8<float> r;
+    r.a = reinterpret_cast<const float4*>(p)[0];
+    r.b = reinterpret_cast<const float4*>(p)[1];
+    return r;
+}
+__device__ __forceinline__ void to_f32(const Raw8<uint16_t>& r, float (&f)[8]) {
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = h2f((uint16_t)(w[i] & 0xffffu));
+        f[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+    }
+}
+__device__ __forceinline__ void to_f32(const Raw8<float>& r, float (&f)[8]) {
+    f[0] = r.a.x; f[1] = r.a.y; f[2] = r.a.z; f[3] = r.a.w;
+    f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
+}
+
+__device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f2h(v); }
+__device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
+
+// Reduces R partial values held by each of L consecutive lanes so that lane
+// `li` (0..L-1) ends with the totals of value indices (R/L)*li + j in v[j].
+template <int L, int R>
+__device__ __forceinline__ void transpose_reduce(float (&v)[R], int li) {
+    static_assert(R >= L, "transpose_reduce needs R >= L");
+    int n = R;
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) {
+        const bool up = (li & m) != 0;
+#pragma unroll
+        for (int i = 0; i < R / 2; i++) {
+            if (i < n / 2) {
+                float send = up ? v[i] : v[i + n / 2];
+                float keep = up ? v[i + n / 2] : v[i];
+                v[i] = keep + shfl_xor(send, m);
+            }
+        }
+        n >>= 1;
+    }
+}
+
+// RMSNorm (cpu_ops.cpp:24-30) + RoPE (cpu_ops.cpp:40-63) of one D-vector held
+// in shared memory, in place.  All threads participate.
+template <int D>
+__device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p, float* red) {
+    float ss = 0.f;
+    for (int d = threadIdx.x; d < D; d += kNT) ss += row[d] * row[d];
+    ss = block_sum<kNT>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+    for (int d = threadIdx.x; d < D; d += kNT) row[d] = (row[d] * inv) * w[d];
+    __syncthreads();
+    for (int j = threadIdx.x; j < p.rot_pairs; j += kNT) {
+        const int i0 = p.rope_mode == 0 ? 2 * j : j;
+        const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
+        const float c = p.cs[j], s = p.sn[j];
+        const float v0 = row[i0], v1 = row[i1];
+        rotate_pair(row[i0], row[i1], v0, v1, c, s);
+    }
+    __syncthreads();
+}
+
+// Merges `n` partial records (m, l, o[D]) for G heads at src (record stride
+// G*(D+2) floats) into one record at dst, or, when `final_out` is set, into
+// the normalised (and optionally gated) output rows.
+template <int D, int G>
+__device__ void combine(const float* src, int n, float* dst, bool final_out, int kvh,
+                        const DecodeParams& p, const SeqView& sv) {
+    constexpr int REC = D + 2;
+    for (int e = threadIdx.x; e < G * D; e += kNT) {
+        const int g = e / D, d = e % D;
+        float M = -INFINITY;
+        for (int s = 0; s < n; s++) M = fmaxf(M, src[(size_t)(s * G + g) * REC]);
+        float L = 0.f, O = 0.f;
+        for (int s = 0; s < n; s++) {
+            const float* r = src + (size_t)(s * G + g) * REC;
+            const float f = __expf(r[0] - M);
+            L += r[1] * f;
+            O += r[2 + d] * f;
+        }
+        if (final_out) {
+            const int h = kvh * G + g;
+            float y = O / L;
+            if (p.gate) y = y / (1.0f + expf(-sv.q[(size_t)h * p.q_stride + D + d]));
+            sv.out[(size_t)h * D + d] = y;
+        } else {
+            float* r = dst + (size_t)g * REC;
+            if (d == 0) { r[0] = M; r[1] = L; }
+            r[2 + d] = O;
+        }
+    }
+}
+
+template <typename KV, int D, int G>
+__global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) {
+    constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
+    constexpr int KPI = 64 / LPK;     // key rows per wave instruction
+    constexpr int KPB = kNW * KPI;    // key rows per workgroup instruction
+    constexpr int KB = LPK / G;       // instructions batched per reduction
+    constexpr int REC = D + 2;
+    static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
+
+    __shared__ float q_s[G][D];
+    __shared__ float kn_s[D];
+    __shared__ float sc[G][kMaxKps];
+    __shared__ float red_o[kNW][G][D];
+    __shared__ float red[kNW];
+    __shared__ int flag;
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int seq = blockIdx.z;
+    const int Hkv = p.n_kv_heads;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int sub = lane / LPK, dl = lane % LPK;
+
+    SeqView sv;
+    sv.len = p.paged ? min(p.seq_lens[seq], p.len) : p.len;
+    if (sv.len <= 0) {  // empty sequence: zeros, as cpu_ops.cpp:152-155
+        if (split == 0)
+            for (int e = tid; e < G * D; e += kNT)
+                p.out[(size_t)seq * Hkv * G * D + (size_t)kvh * G * D + e] = 0.f;
+        return;
+    }
+    sv.n_splits = (sv.len + p.kps - 1) / p.kps;
+    if (split >= sv.n_splits) return;
+    sv.n_groups = (sv.n_splits + p.cg - 1) / p.cg;
+    sv.q = p.q + (size_t)seq * Hkv * G * p.q_stride;
+    sv.out = p.out + (size_t)seq * Hkv * G * D;
+    sv.part = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * G * REC;
+    sv.part2 = p.part2 + ((size_t)seq * Hkv + kvh) * p.max_groups * G * REC;
+    sv.cnt1 = p.cnt + ((size_t)seq * Hkv + kvh) * p.max_groups;
+    sv.cnt2 = p.cnt + (size_t)p.n_seqs * Hkv * p.max_groups + (size_t)seq * Hkv + kvh;
+
+    const int t0 = split * p.kps;
+    const int nk = min(p.kps, sv.len - t0);
+    const size_t tok_stride = (size_t)Hkv * D;
+    const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
+    const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
+
+    // ---- q rows (and, for the split holding the newest key, the append)
+    for (int g = 0; g < G; g++) {
+        const float* src = sv.q + (size_t)(kvh * G + g) * p.q_stride;
+        for (int d = tid; d < D; d += kNT) q_s[g][d] = src[d];
+    }
+    __syncthreads();
+    if (p.fused) {
+        for (int g = 0; g < G; g++) norm_rope_row<D>(q_s[g], p.q_norm_w, p, red);
+        if (split == sv.n_splits - 1) {
+            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
+            __syncthreads();
+            norm_rope_row<D>(kn_s, p.k_norm_w, p, red);
+            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
+            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
+            for (int d = tid; d < D; d += kNT) {
+                store_kv(kw + d, kn_s[d]);
+                store_kv(vw + d, p.v_new[(size_t)kvh * D + d]);
+            }
+            __threadfence();
+            __syncthreads();
+        }
+    }
+
+    float qr[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
+
+    const int32_t* ptab = p.paged ? p.page_table + (size_t)seq * p.max_pages : nullptr;
+    auto row_ptr = [&](const KV* base, int t) -> const KV* {
+        const int lt = t0 + t;
+        if (p.paged) {
+            const int page = min(max(ptab[lt / p.page_size], 0), p.n_pages - 1);
+            const int row = lt % p.page_size;
+            return base + (((size_t)page * Hkv + kvh) * p.page_size + row) * D + dl * 8;
+        }
+        int phys = p.start + lt;
+        if (phys >= p.cap) phys -= p.cap;
+        return base + (size_t)phys * tok_stride + (size_t)kvh * D + dl * 8;
+    };
+
+    // ---- scores: KB instructions of key rows per batch, one transpose reduce
+    for (int it = 0; it < nk; it += KPB * KB) {
+        Raw8<KV> raw[KB];
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int t = it + b * KPB + w * KPI + sub;
+            if (t < nk) raw[b] = load_raw(row_ptr(kc, t));
+        }
+        float part[KB * G];
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int t = it + b * KPB + w * KPI + sub;
+            float kf[8];
+            to_f32(raw[b], kf);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float s = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) s = fmaf(qr[g][i], kf[i], s);
+                part[b * G + g] = (t < nk) ? s : 0.f;
+            }
+        }
+        transpose_reduce<LPK, KB * G>(part, dl);
+        const int b = dl / G, g = dl % G;
+        const int t = it + b * KPB + w * KPI + sub;
+        if (t < nk) sc[g][t] = part[0] * p.scale;
+    }
+    __syncthreads();
+
+    // ---- softmax statistics per head over this split
+    float mloc[G], lloc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float m = -INFINITY;
+        for (int t = tid; t < nk; t += kNT) m = fmaxf(m, sc[g][t]);
+        mloc[g] = block_max<kNT>(m, red);
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float l = 0.f;
+        for (int t = tid; t < nk; t += kNT) {
+            const float e = __expf(sc[g][t] - mloc[g]);
+            sc[g][t] = e;
+            l += e;
+        }
+        lloc[g] = block_sum<kNT>(l, red);
+    }
+    __syncthreads();
+
+    // ---- P V
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
+    for (int it = 0; it < nk; it += KPB * KB) {
+        Raw8<KV> raw[KB];
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int t = it + b * KPB + w * KPI + sub;
+            if (t < nk) raw[b] = load_raw(row_ptr(vc, t));
+        }
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int t = it + b * KPB + w * KPI + sub;
+            if (t < nk) {
+                float vf[8];
+                to_f32(raw[b], vf);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float pg = sc[g][t];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pg, vf[i], acc[g][i]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = LPK; m < 64; m <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[g][i] += shfl_xor(acc[g][i], m);
+    if (sub == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) red_o[w][g][dl * 8 + i] = acc[g][i];
+    }
+    __syncthreads();
+
+    // ---- output: direct when there is one split, else partial + combine
+    if (sv.n_splits == 1) {
+        for (int e = tid; e < G * D; e += kNT) {
+            const int g = e / D, d = e % D;
+            float o = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+            const int h = kvh * G + g;
+            float y = o / lloc[g];
+            if (p.gate) y = y / (1.0f + expf(-sv.q[(size_t)h * p.q_stride + D + d]));
+            sv.out[(size_t)h * D + d] = y;
+        }
+        return;
+    }
+    float* rec = sv.part + (size_t)split * G * REC;
+    for (int e = tid; e < G * D; e += kNT) {
+        const int g = e / D, d = e % D;
+        float o = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+        rec[(size_t)g * REC + 2 + d] = o;
+        if (d == 0) { rec[(size_t)g * REC] = mloc[g]; rec[(size_t)g * REC + 1] = lloc[g]; }
+    }
+    __threadfence();
+    __syncthreads();
+    const int grp = split / p.cg;
+    const int gsize = min(p.cg, sv.n_splits - grp * p.cg);
+    if (tid == 0) {
+        uint32_t* c = sv.cnt1 + grp;
+        const uint32_t old = atomicAdd(c, 1u);
+        flag = (old == (uint32_t)gsize - 1);
+        if (flag) atomicExch(c, 0u);
+    }
+    __syncthreads();
+    if (!flag) return;
+    __threadfence();
+    const float* src = sv.part + (size_t)grp * p.cg * G * REC;
+    if (sv.n_groups == 1) {
+        combine<D, G>(src, gsize, nullptr, true, kvh, p, sv);
+        return;
+    }
+    combine<D, G>(src, gsize, sv.part2 + (size_t)grp * G * REC, false, kvh, p, sv);
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = atomicAdd(sv.cnt2, 1u);
+        flag = (old == (uint32_t)sv.n_groups - 1);
+        if (flag) atomicExch(sv.cnt2, 0u);
+    }
+    __syncthreads();
+    if (!flag) return;
+    __threadfence();
+    combine<D, G>(sv.part2, sv.n_groups, nullptr, true, kvh, p, sv);
+}
+
+template <typename KV, int D>
+int launch_d(DecodeParams& p, int G, dim3 grid, hipStream_t st) {
+    switch (G) {
+        case 1: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1>), grid, dim3(kNT), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 2>), grid, dim3(kNT), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 4>), grid, dim3(kNT), 0, st, p); break;
+        case 8: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 8>), grid, dim3(kNT), 0, st, p); break;
+        default: return set_error(ANELM_EINVAL, "n_heads/n_kv_heads = %d unsupported (1,2,4,8)", G);
+    }
+    ANELM_LAUNCHED("attn_decode_kernel");
+    return ANELM_OK;
+}
+
+template <typename KV>
+int launch_kv(DecodeParams& p, int D, int G, dim3 grid, hipStream_t st) {
+    switch (D) {
+        case 64: return (G <= 8) ? launch_d<KV, 64>(p, G, grid, st) : ANELM_EINVAL;
+        case 128: return launch_d<KV, 128>(p, G, grid, st);
+        case 256: return launch_d<KV, 256>(p, G, grid, st);
+        default: return set_error(ANELM_EINVAL, "head_dim %d unsupported (64,128,256)", D);
+    }
+}
+
+// Chooses the split layout and workspace for one decode call, then launches.
+// `max_len` bounds every sequence's key count; `n_seqs` sequences (1 in ring
+// mode).  Splits aim at about two workgroups per compute unit.
+int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, int max_len,
+               hipStream_t st) {
+    const int Hkv = p.n_kv_heads;
+    const int G = n_heads / Hkv;
+    Device* dev = device();
+    if (!dev) return ANELM_EHIP;
+    const int target = 2 * dev->num_cus;
+    int per_seq = std::max(1, target / (Hkv * n_seqs));
+    if (n_seqs > 1) per_seq = std::max(1, 2 * per_seq);  // ragged: average length ~ max/2
+    int splits = std::min(per_seq, (max_len + 63) / 64);
+    int kps = (max_len + splits - 1) / splits;
+    kps = (kps + 15) & ~15;
+    kps = std::min(std::max(kps, 16), kMaxKps);
+    const int max_splits = (max_len + kps - 1) / kps;
+    int cg = 1;
+    while (cg * cg < max_splits) cg++;
+    const int max_groups = (max_splits + cg - 1) / cg;
+    p.kps = kps;
+    p.max_splits = max_splits;
+    p.cg = cg;
+    p.max_groups = max_groups;
+    p.n_seqs = n_seqs;
+    const size_t rec = (size_t)G * (D + 2);
+    if (max_splits > 1) {
+        const size_t pairs = (size_t)n_seqs * Hkv;
+        const size_t need = pairs * ((size_t)max_splits + max_groups) * rec * sizeof(float);
+        float* ws = static_cast<float*>(workspace(need, st));
+        if (!ws) return ANELM_ENOMEM;
+        p.part = ws;
+        p.part2 = ws + pairs * max_splits * rec;
+        p.cnt = counters(pairs * max_groups + pairs);
+        if (!p.cnt) return ANELM_ERANGE;
+    } else {
+        p.part = p.part2 = nullptr;
+        p.cnt = nullptr;
+    }
+    dim3 grid(max_splits, Hkv, n_seqs);
+    return kv_dtype == ANELM_F16 ? launch_kv<uint16_t>(p, D, G, grid, st)
+                                 : launch_kv<float>(p, D, G, grid, st);
+}
+
+int check_heads(int n_heads, int n_kv_heads, int head_dim) {
+    ANELM_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                  "n_heads %d must be a positive multiple of n_kv_heads %d", n_heads, n_kv_heads);
+    const int G = n_heads / n_kv_heads;
+    ANELM_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "n_heads/n_kv_heads = %d unsupported", G);
+    ANELM_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                  "head_dim %d unsupported (64,128,256)", head_dim);
+    ANELM_REQUIRE(!(head_dim == 64 && G > 8), "head_dim 64 supports G <= 8");
+    return ANELM_OK;
+}
+
+}  // namespace
+
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" int anelm_gqa_attention(float* out, const float* q, const void* k_cache,
+                                   const void* v_cache, int kv_dtype, int n_heads, int n_kv_heads,
+                                   int head_dim, int q_head_stride, int cache_start, int cache_len,
+                                   int cache_capacity, void* stream) {
+    ANELM_NONNULL(out);
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(kv_dtype == ANELM_F16 || kv_dtype == ANELM_F32, "kv_dtype %d unknown", kv_dtype);
+    hipStream_t st = as_stream(stream);
+    if (cache_len <= 0) {
+        ANELM_HIP(hipMemsetAsync(out, 0, (size_t)n_heads * head_dim * sizeof(float), st));
+        return ANELM_OK;
+    }
+    ANELM_NONNULL(q);
+    ANELM_NONNULL(k_cache);
+    ANELM_NONNULL(v_cache);
+    ANELM_REQUIRE(q_head_stride >= head_dim, "q_head_stride %d < head_dim", q_head_stride);
+    ANELM_REQUIRE(cache_capacity > 0 && cache_len <= cache_capacity && cache_start >= 0 &&
+                      cache_start < cache_capacity,
+                  "ring (start %d, len %d, capacity %d) inconsistent", cache_start, cache_len,
+                  cache_capacity);
+    DecodeParams p{};
+    p.out = out;
+    p.q = q;
+    p.q_stride = q_head_stride;
+    p.k_cache = k_cache;
+    p.v_cache = v_cache;
+    p.n_kv_heads = n_kv_heads;
+    p.start = cache_start;
+    p.len = cache_len;
+    p.cap = cache_capacity;
+    p.scale = 1.0f / sqrtf((float)head_dim);
+    p.fused = 0;
+    p.gate = 0;
+    return run_decode(p, kv_dtype, n_heads, head_dim, 1, cache_len, st);
+}
+
+extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const float* k,
+                                      const float* v, uint16_t* k_cache, uint16_t* v_cache,
+                                      const float* q_norm_w, const float* k_norm_w, int n_heads,
+                                      int n_kv_heads, int head_dim, int rot_dim, int pos,
+                                      float theta, float eps, int rope_mode, int gate,
+                                      const float* cos_row, const float* sin_row,
+                                      int* cache_start, int* cache_len, int cache_capacity,
+                                      void* stream) {
+    ANELM_NONNULL(out);
+    ANELM_NONNULL(q_gate);
+    ANELM_NONNULL(k);
+    ANELM_NONNULL(v);
+    ANELM_NONNULL(k_cache);
+    ANELM_NONNULL(v_cache);
+    ANELM_NONNULL(q_norm_w);
+    ANELM_NONNULL(k_norm_w);
+    ANELM_NONNULL(cache_start);
+    ANELM_NONNULL(cache_len);
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(rot_dim >= 0 && rot_dim % 2 == 0 && rot_dim <= head_dim &&
+                      rot_dim / 2 <= kMaxRotPairs,
+                  "rot_dim %d must be even and <= head_dim", rot_dim);
+    ANELM_REQUIRE(rope_mode == ANELM_ROPE_INTERLEAVED || rope_mode == ANELM_ROPE_HALF_SPLIT,
+                  "rope_mode %d unknown", rope_mode);
+    ANELM_REQUIRE(cache_capacity > 0 && *cache_len >= 0 && *cache_len <= cache_capacity &&
+                      *cache_start >= 0 && *cache_start < cache_capacity,
+                  "ring (start %d, len %d, capacity %d) inconsistent", *cache_start, *cache_len,
+                  cache_capacity);
+    // Ring bookkeeping, models/llm/qwen3_5.cpp:973-983.
+    int start = *cache_start, len = *cache_len, slot;
+    if (len < cache_capacity) {
+        slot = start + len;
+        if (slot >= cache_capacity) slot -= cache_capacity;
+        len++;
+    } else {
+        slot = start;
+        start++;
+        if (start >= cache_capacity) start = 0;
+    }
+    DecodeParams p{};
+    p.out = out;
+    p.q = q_gate;
+    p.q_stride = 2 * head_dim;
+    p.k_cache = k_cache;
+    p.v_cache = v_cache;
+    p.n_kv_heads = n_kv_heads;
+    p.start = start;
+    p.len = len;
+    p.cap = cache_capacity;
+    p.scale = 1.0f / sqrtf((float)head_dim);
+    p.fused = 1;
+    p.q_norm_w = q_norm_w;
+    p.k_norm_w = k_norm_w;
+    p.k_new = k;
+    p.v_new = v;
+    p.k_cache_w = k_cache;
+    p.v_cache_w = v_cache;
+    p.new_slot = slot;
+    p.eps = eps;
+    p.rot_pairs = rot_dim / 2;
+    p.rope_mode = rope_mode;
+    p.gate = gate ? 1 : 0;
+    if (cos_row && sin_row) {
+        for (int j = 0; j < rot_dim / 2; j++) { p.cs[j] = cos_row[j]; p.sn[j] = sin_row[j]; }
+    } else {
+        rope_row(p.cs, p.sn, rot_dim, pos, theta);
+    }
+    rc = run_decode(p, ANELM_F16, n_heads, head_dim, 1, len, as_stream(stream));
+    if (rc == ANELM_OK) {
+        *cache_start = start;
+        *cache_len = len;
+    }
+    return rc;
+}
+
+extern "C" int anelm_attn_decode_paged(float* out, const float* q, int q_head_stride,
+                                       const uint16_t* k_pages, const uint16_t* v_pages,
+                                       const int32_t* page_table, const int32_t* seq_lens,
+                                       int n_seqs, int max_pages, int page_size, int n_pages,
+                                       int max_seq_len,
+                                       int n_heads, int n_kv_heads, int head_dim, void* stream) {
+    ANELM_NONNULL(out);
+    ANELM_NONNULL(q);
+    ANELM_NONNULL(k_pages);
+    ANELM_NONNULL(v_pages);
+    ANELM_NONNULL(page_table);
+    ANELM_NONNULL(seq_lens);
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(n_seqs > 0 && n_seqs <= 65535, "paged: n_seqs %d", n_seqs);
+    ANELM_REQUIRE(page_size > 0 && max_pages > 0 && n_pages > 0,
+                  "paged: page_size %d max_pages %d n_pages %d", page_size, max_pages, n_pages);
+    ANELM_REQUIRE(max_seq_len > 0 && max_seq_len <= max_pages * page_size,
+                  "paged: max_seq_len %d beyond max_pages*page_size", max_seq_len);
+    ANELM_REQUIRE(q_head_stride >= head_dim, "paged: q_head_stride %d < head_dim", q_head_stride);
+    DecodeParams p{};
+    p.out = out;
+    p.q = q;
+    p.q_stride = q_head_stride;
+    p.k_cache = k_pages;
+    p.v_cache = v_pages;
+    p.n_kv_heads = n_kv_heads;
+    p.scale = 1.0f / sqrtf((float)head_dim);
+    p.paged = 1;
+    p.page_table = page_table;
+    p.seq_lens = seq_lens;
+    p.max_pages = max_pages;
+    p.page_size = page_size;
+    p.n_pages = n_pages;
+    p.len = max_seq_len;
+    return run_decode(p, ANELM_F16, n_heads, head_dim, n_seqs, max_seq_len, as_stream(stream));
+}

@@ -1,0 +1,125 @@
+// Hybrid decode step executor: the per-layer core + FFN launch sequence of
+// Qwen35Model::forward (models/llm/qwen3_5.cpp:1278-1356), issued from C++ and
+// optionally captured once into a HIP graph so a step costs one graph launch
+// instead of ~3 host launches per layer.
+#include "anelm_internal.hpp"
+
+#include <vector>
+
+struct anelm_hybrid_step {
+    anelm_hybrid_dims dims;
+    std::vector<anelm_hybrid_layer> layers;
+    float* x = nullptr;
+    float* h = nullptr;
+    bool use_graph = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace anelm {
+namespace {
+
+// One eager pass over all layers; `advance` moves every attention ring one
+// token forward (the host-side KVCache bookkeeping of qwen3_5.cpp:973-983).
+int launch_all(anelm_hybrid_step* s, hipStream_t st, bool advance) {
+    const anelm_hybrid_dims& d = s->dims;
+    for (auto& L : s->layers) {
+        int rc;
+        if (L.kind == ANELM_LAYER_ATTENTION) {
+            int start = L.cache_start, len = L.cache_len;
+            rc = anelm_full_attn_decode(L.core_out, L.q_gate, L.k, L.v, L.k_cache, L.v_cache,
+                                        L.q_norm_w, L.k_norm_w, d.n_heads, d.n_kv_heads,
+                                        d.head_dim, d.rot_dim, L.pos, d.theta, d.eps, d.rope_mode,
+                                        1, nullptr, nullptr, &start, &len, L.cache_capacity, st);
+            if (rc) return rc;
+            if (advance) {
+                L.cache_start = start;
+                L.cache_len = len;
+                L.pos++;
+            }
+        } else {
+            rc = anelm_deltanet_decode(L.core_out, L.state, L.dn_q, L.dn_k, L.dn_v, L.dn_a, L.dn_b,
+                                       L.dn_A, L.dn_dt_bias, L.dn_z, L.dn_norm_w, d.lin_k_heads,
+                                       d.lin_v_heads, d.lin_dim, d.lin_dim, L.dn_flags, st);
+            if (rc) return rc;
+        }
+        rc = anelm_lut6_ffn(s->x, s->h, L.ffn_norm_w, d.eps, L.gate_w, L.gate_lut, L.up_w, L.up_lut,
+                            L.down_w, L.down_lut, d.hidden, d.inter, st);
+        if (rc) return rc;
+    }
+    return ANELM_OK;
+}
+
+}  // namespace
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hybrid_dims* dims,
+                                        const anelm_hybrid_layer* layers, int n_layers, float* x,
+                                        float* h_scratch, int use_graph, void* stream) {
+    ANELM_NONNULL(out);
+    ANELM_NONNULL(dims);
+    ANELM_NONNULL(layers);
+    ANELM_NONNULL(x);
+    ANELM_NONNULL(h_scratch);
+    ANELM_REQUIRE(n_layers > 0, "hybrid_step: n_layers %d", n_layers);
+    ANELM_REQUIRE(!use_graph || stream != nullptr, "hybrid_step: graph capture needs a non-null stream");
+    for (int i = 0; i < n_layers; i++)
+        ANELM_REQUIRE(layers[i].kind == ANELM_LAYER_ATTENTION || layers[i].kind == ANELM_LAYER_DELTANET,
+                      "hybrid_step: layer %d kind %d", i, layers[i].kind);
+    auto* s = new anelm_hybrid_step();
+    s->dims = *dims;
+    s->layers.assign(layers, layers + n_layers);
+    s->x = x;
+    s->h = h_scratch;
+    s->use_graph = use_graph != 0;
+    hipStream_t st = as_stream(stream);
+    if (s->use_graph) {
+        // Warm-up: grows the workspace outside the capture.
+        int rc = launch_all(s, st, false);
+        if (rc == ANELM_OK) {
+            hipError_t e = hipStreamSynchronize(st);
+            if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+        }
+        if (rc == ANELM_OK) {
+            hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+            if (e != hipSuccess) rc = hip_fail(e, "hipStreamBeginCapture");
+            else {
+                rc = launch_all(s, st, false);
+                hipGraph_t g = nullptr;
+                e = hipStreamEndCapture(st, &g);
+                if (rc == ANELM_OK && e != hipSuccess) rc = hip_fail(e, "hipStreamEndCapture");
+                s->graph = g;
+                if (rc == ANELM_OK) {
+                    e = hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0);
+                    if (e != hipSuccess) rc = hip_fail(e, "hipGraphInstantiate");
+                }
+            }
+        }
+        if (rc != ANELM_OK) {
+            anelm_hybrid_step_destroy(s);
+            return rc;
+        }
+    }
+    *out = s;
+    return ANELM_OK;
+}
+
+extern "C" int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream) {
+    ANELM_NONNULL(step);
+    hipStream_t st = as_stream(stream);
+    if (step->use_graph) {
+        ANELM_HIP(hipGraphLaunch(step->exec, st));
+        return ANELM_OK;
+    }
+    return launch_all(step, st, true);
+}
+
+extern "C" int anelm_hybrid_step_destroy(anelm_hybrid_step* step) {
+    if (!step) return ANELM_OK;
+    if (step->exec) (void)hipGraphExecDestroy(step->exec);
+    if (step->graph) (void)hipGraphDestroy(step->graph);
+    delete step;
+    return ANELM_OK;
+}

@@ -1,0 +1,225 @@
+"""Torch-tensor wrappers over the libanelm C ABI.
+
+Every function takes device tensors, launches on torch's current HIP stream
+and returns the output tensor(s).  Names and argument meaning follow the
+reference's core/cpu_ops.h (rmsnorm, apply_rope_cached, gqa_attention,
+ssm_step, ...) and the caller glue in models/llm/qwen3_5.cpp.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import (ANELM_F16, ANELM_F32, ROPE_INTERLEAVED, call)
+
+_F32 = torch.float32
+_F16 = torch.float16
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _s():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t, dtype, name):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _floats(vals):
+    if vals is None:
+        return None
+    arr = (ctypes.c_float * len(vals))(*[float(v) for v in vals])
+    return ctypes.cast(arr, ctypes.POINTER(ctypes.c_float)), arr
+
+
+class KVRing:
+    """Host-side ring bookkeeping of one KV cache (qwen3_5.h:165-171)."""
+
+    def __init__(self, capacity: int, start: int = 0, length: int = 0):
+        self.capacity = capacity
+        self.start = ctypes.c_int(start)
+        self.len = ctypes.c_int(length)
+
+
+# ------------------------------------------------------------------ norms
+def rmsnorm(x, w, eps=1e-6, out=None):
+    """cpu_ops.cpp:24-30 per row of the last dimension."""
+    _need(x, _F32, "x")
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    out = torch.empty_like(x) if out is None else out
+    call("anelm_rmsnorm", _p(out), _p(x), _p(w), dim, rows, dim, dim, eps, _s())
+    return out
+
+
+def rmsnorm_gated(x, z, w):
+    """cpu_ops.cpp:32-38 per row."""
+    dim = x.shape[-1]
+    out = torch.empty_like(x)
+    call("anelm_rmsnorm_gated", _p(out), _p(x), _p(z), _p(w), dim, x.numel() // dim, _s())
+    return out
+
+
+def l2_normalize_(x):
+    """cpu_ops.cpp:82-87 in place per row."""
+    dim = x.shape[-1]
+    call("anelm_l2_normalize", _p(x), dim, x.numel() // dim, _s())
+    return x
+
+
+def apply_rope_(q, k, n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim,
+                pos, theta, rope_mode=ROPE_INTERLEAVED, cos_row=None, sin_row=None):
+    """cpu_ops.cpp:40-63 in place; cos_row/sin_row are host sequences or None."""
+    c = _floats(cos_row)
+    s = _floats(sin_row)
+    call("anelm_apply_rope", _p(q), _p(k), n_q_heads, n_kv_heads, head_dim, q_head_stride,
+         k_head_stride, rot_dim, pos, theta, c[0] if c else None, s[0] if s else None,
+         rope_mode, _s())
+
+
+def silu_(x):
+    call("anelm_silu_inplace", _p(x), x.numel(), _s())
+    return x
+
+
+def mul_sigmoid_(y, z):
+    call("anelm_mul_sigmoid_inplace", _p(y), _p(z), y.numel(), _s())
+    return y
+
+
+def softmax_(x):
+    n = x.shape[-1]
+    call("anelm_softmax", _p(x), n, x.numel() // n, _s())
+    return x
+
+
+def matvec(W, x):
+    out = torch.empty(W.shape[0], device=x.device, dtype=_F32)
+    call("anelm_matvec", _p(out), _p(W), _p(x), W.shape[0], W.shape[1], _s())
+    return out
+
+
+def conv1d_update(conv_state, state_pos: ctypes.c_int, x, w, kernel_size):
+    channels = x.numel()
+    y = torch.empty_like(x)
+    call("anelm_conv1d_update", _p(y), _p(conv_state), ctypes.byref(state_pos), _p(x), _p(w),
+         channels, kernel_size, _s())
+    return y
+
+
+# -------------------------------------------------------------- attention
+def gqa_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, q_head_stride,
+                  cache_start, cache_len, cache_capacity, out=None):
+    """cpu_ops.cpp:148-204; caches fp32 or fp16 [cap][Hkv][D]."""
+    kv = ANELM_F16 if k_cache.dtype == _F16 else ANELM_F32
+    out = torch.empty(n_heads, head_dim, device=q.device, dtype=_F32) if out is None else out
+    call("anelm_gqa_attention", _p(out), _p(q), _p(k_cache), _p(v_cache), kv, n_heads,
+         n_kv_heads, head_dim, q_head_stride, cache_start, cache_len, cache_capacity, _s())
+    return out
+
+
+def full_attn_decode(q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, ring: KVRing,
+                     n_heads, n_kv_heads, head_dim, rot_dim, pos, theta=1e7, eps=1e-6,
+                     rope_mode=ROPE_INTERLEAVED, gate=True, cos_row=None, sin_row=None,
+                     out=None):
+    """qwen3_5.cpp:944-1002 fused: norms, RoPE, fp16 ring append, attention, gate."""
+    _need(k_cache, _F16, "k_cache")
+    out = torch.empty(n_heads, head_dim, device=q_gate.device, dtype=_F32) if out is None else out
+    c = _floats(cos_row)
+    s = _floats(sin_row)
+    call("anelm_full_attn_decode", _p(out), _p(q_gate), _p(k), _p(v), _p(k_cache), _p(v_cache),
+         _p(q_norm_w), _p(k_norm_w), n_heads, n_kv_heads, head_dim, rot_dim, pos, theta, eps,
+         rope_mode, 1 if gate else 0, c[0] if c else None, s[0] if s else None,
+         ctypes.byref(ring.start), ctypes.byref(ring.len), ring.capacity, _s())
+    return out
+
+
+def attn_decode_paged(q, k_pages, v_pages, page_table, seq_lens, max_seq_len, n_heads,
+                      n_kv_heads, head_dim, page_size, q_head_stride=None, out=None):
+    n_seqs = seq_lens.numel()
+    max_pages = page_table.shape[-1]
+    q_head_stride = head_dim if q_head_stride is None else q_head_stride
+    out = (torch.empty(n_seqs, n_heads, head_dim, device=q.device, dtype=_F32)
+           if out is None else out)
+    n_pages = k_pages.shape[0]
+    call("anelm_attn_decode_paged", _p(out), _p(q), q_head_stride, _p(k_pages), _p(v_pages),
+         _p(page_table), _p(seq_lens), n_seqs, max_pages, page_size, n_pages, max_seq_len,
+         n_heads, n_kv_heads, head_dim, _s())
+    return out
+
+
+def attn_prefill(q, k, v, out_dtype=_F32):
+    """Causal GQA prefill; q [S][Hq][D], k/v [S][Hkv][D] fp16."""
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    out = torch.empty(S, Hq, D, device=q.device, dtype=out_dtype)
+    call("anelm_attn_prefill", _p(out), ANELM_F16 if out_dtype == _F16 else ANELM_F32, _p(q),
+         _p(k), _p(v), S, Hq, Hkv, D, _s())
+    return out
+
+
+# --------------------------------------------------------------- DeltaNet
+def ssm_step(state, q, k, v, decay, beta, flags=0):
+    """cpu_ops.cpp:131-146 on one head; state [dk][dv] updated in place."""
+    y = torch.empty(state.shape[1], device=state.device, dtype=_F32)
+    call("anelm_ssm_step", _p(y), _p(state), _p(q), _p(k), _p(v), decay, beta, state.shape[0],
+         state.shape[1], flags, _s())
+    return y
+
+
+def deltanet_decode(state, q, k, v, a, b, A, dt_bias, flags, z=None, norm_w=None, out=None):
+    """qwen3_5.cpp:879-908; state [Hv][dk][dv] updated in place."""
+    Hv, dk, dv = state.shape
+    Hk = q.shape[0]
+    out = torch.empty(Hv, dv, device=state.device, dtype=_F32) if out is None else out
+    call("anelm_deltanet_decode", _p(out), _p(state), _p(q), _p(k), _p(v), _p(a), _p(b), _p(A),
+         _p(dt_bias), _p(z), _p(norm_w), Hk, Hv, dk, dv, flags, _s())
+    return out
+
+
+def deltanet_prefill(state, q, k, v, a, b, A, dt_bias, flags, chunk=64):
+    """Chunked prefill; q,k [S][Hk][dk], v [S][Hv][dv], a,b [S][Hv]."""
+    S, Hk, dk = q.shape
+    Hv, _, dv = state.shape
+    y = torch.empty(S, Hv, dv, device=state.device, dtype=_F32)
+    call("anelm_deltanet_prefill", _p(y), _p(state), _p(q), _p(k), _p(v), _p(a), _p(b), _p(A),
+         _p(dt_bias), S, Hk, Hv, dk, dv, chunk, flags, _s())
+    return y
+
+
+# ------------------------------------------------------------------- LUT6
+def lut6_unpack(packed, n):
+    idx = torch.empty(n, device=packed.device, dtype=torch.uint8)
+    call("anelm_lut6_unpack", _p(idx), _p(packed), n, _s())
+    return idx
+
+
+def lut6_gemv(w, lut, x, out_dim, in_dim, out=None):
+    out = torch.empty(out_dim, device=x.device, dtype=_F32) if out is None else out
+    call("anelm_lut6_gemv", _p(out), _p(w), _p(lut), _p(x), out_dim, in_dim, _s())
+    return out
+
+
+def lut6_ffn_(x, h_scratch, norm_w, eps, gate, up, down, hidden, inter):
+    """x += down(silu(gate n) * (up n)), n = rmsnorm(x, norm_w); gate/up/down = (w, lut)."""
+    call("anelm_lut6_ffn", _p(x), _p(h_scratch), _p(norm_w), eps, _p(gate[0]), _p(gate[1]),
+         _p(up[0]), _p(up[1]), _p(down[0]), _p(down[1]), hidden, inter, _s())
+    return x
+
+
+def lut6_topk(w, lut, x, out_dim, in_dim, k):
+    batch = x.shape[0] if x.dim() == 2 else 1
+    idx = torch.empty(batch, k, device=x.device, dtype=torch.int32)
+    val = torch.empty(batch, k, device=x.device, dtype=_F32)
+    call("anelm_lut6_topk", _p(idx), _p(val), _p(w), _p(lut), _p(x), batch, out_dim, in_dim, k,
+         _s())
+    return idx, val

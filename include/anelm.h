@@ -1,0 +1,286 @@
+/*
+ * anelm.h -- C ABI of libanelm.so, the MI355X (gfx950) implementation of the
+ * ANE-LM core/cpu_ops hot path.
+ *
+ * Native tier: every pointer argument is a DEVICE pointer unless marked
+ * "host"; `stream` is a hipStream_t passed as void* (NULL = null stream).
+ * Calls are asynchronous on `stream` and return an int status:
+ *   0 = ANELM_OK, < 0 = error (see anelm_last_error(), thread-local text).
+ * Nothing throws across the ABI.  The library keeps one device workspace and
+ * one zeroed counter array per device; calls that use them must be issued
+ * from one host thread / one stream at a time per device (the reference's
+ * callers are serial: main.cpp:276-371, scripts/serve_hybrid.py:699).
+ *
+ * Each declaration names the reference interface it replaces.
+ */
+#ifndef ANELM_H
+#define ANELM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ANELM_OK = 0,
+    ANELM_EINVAL = -1,   /* bad shape, stride or flag */
+    ANELM_ENULL = -2,    /* required pointer is NULL */
+    ANELM_EHIP = -3,     /* HIP runtime error */
+    ANELM_ERANGE = -4,   /* size beyond a supported maximum */
+    ANELM_ENOMEM = -5    /* workspace allocation failed */
+};
+
+/* RoPE pairing: core/cpu_ops.cpp:40-63 rotates interleaved pairs (v[i], v[i+1]);
+ * scripts/serve_hybrid.py:94-103 rotates (v[j], v[j + rot/2]). */
+#define ANELM_ROPE_INTERLEAVED 0
+#define ANELM_ROPE_HALF_SPLIT 1
+
+/* DeltaNet flags. */
+#define ANELM_DN_L2NORM 1              /* l2-normalise q,k per key head (qwen3_5.cpp:882-887) */
+#define ANELM_DN_ORDER_TRANSFORMERS 2  /* decay-first rule (export_hybrid_chunks.py:137-147) */
+#define ANELM_DN_GATED_NORM 4          /* rmsnorm_gated epilogue (qwen3_5.cpp:902-908) */
+
+/* Cache element types. */
+#define ANELM_F32 0
+#define ANELM_F16 1
+
+const char* anelm_last_error(void);
+int anelm_version(void);
+/* Number of compute units of the current device (0 on error). */
+int anelm_device_cus(void);
+
+/* ---------------------------------------------------------------- norms */
+
+/* rmsnorm, core/cpu_ops.h:21 / cpu_ops.cpp:24-30, over n_rows rows of `dim`
+ * (row r of x at x + r*x_stride, of out at out + r*out_stride).  In place is
+ * allowed (out == x with equal strides). */
+int anelm_rmsnorm(float* out, const float* x, const float* weight, int dim, int n_rows,
+                  int x_stride, int out_stride, float eps, void* stream);
+
+/* rmsnorm_gated, cpu_ops.h:22 / cpu_ops.cpp:32-38, per row:
+ * out = rmsnorm(x, w, 1e-6) * sigmoid(z) * z. */
+int anelm_rmsnorm_gated(float* out, const float* x, const float* z, const float* weight,
+                        int dim, int n_rows, void* stream);
+
+/* l2_normalize, cpu_ops.h:41 / cpu_ops.cpp:82-87, in place per row. */
+int anelm_l2_normalize(float* x, int dim, int n_rows, void* stream);
+
+/* ----------------------------------------------------------------- RoPE */
+
+/* apply_rope_cached, cpu_ops.h:26-29 / cpu_ops.cpp:40-63.  cos_row/sin_row
+ * are HOST pointers to rot_dim/2 floats (the qwen3_5.cpp:308-324 table row)
+ * or NULL, in which case cosf/sinf(pos * theta^(-i/rot_dim)) are evaluated on
+ * the host exactly as cpu_ops.cpp:51-55 does.  rot_dim <= 256, even. */
+int anelm_apply_rope(float* q, float* k, int n_q_heads, int n_kv_heads, int head_dim,
+                     int q_head_stride, int k_head_stride, int rot_dim, int pos, float theta,
+                     const float* cos_row, const float* sin_row, int rope_mode, void* stream);
+
+/* ------------------------------------------------------------ activations */
+
+/* silu_vec_inplace (cpu_ops.cpp:6-13) and mul_sigmoid_inplace (:15-22); the
+ * reference's caller-provided tmp scratch is not needed. */
+int anelm_silu_inplace(float* x, int n, void* stream);
+int anelm_mul_sigmoid_inplace(float* y, const float* z, int n, void* stream);
+
+/* softmax, cpu_ops.h:33 / cpu_ops.cpp:65-75, in place over n_rows rows of n. */
+int anelm_softmax(float* x, int n, int n_rows, void* stream);
+
+/* matvec, cpu_ops.h:37 / cpu_ops.cpp:77-80: y = W x, W row-major fp32. */
+int anelm_matvec(float* y, const float* W, const float* x, int out_dim, int in_dim, void* stream);
+
+/* conv1d_update, cpu_ops.h:45-46 / cpu_ops.cpp:89-129.  conv_state is a device
+ * array [channels][kernel_size-1]; *state_pos is a HOST int advanced here. */
+int anelm_conv1d_update(float* y, float* conv_state, int* state_pos, const float* x,
+                        const float* w, int channels, int kernel_size, void* stream);
+
+/* ------------------------------------------------------------ attention */
+
+/* gqa_attention, cpu_ops.h:55-58 / cpu_ops.cpp:148-204, over a ring cache
+ * [cache_capacity][n_kv_heads][head_dim] of fp32 (kv_dtype ANELM_F32, the
+ * reference layout) or fp16 (ANELM_F16).  Keys are taken oldest to newest from
+ * cache_start; cache_len <= 0 writes zeros (cpu_ops.cpp:152-155).
+ * head_dim in {64, 128, 256}; n_heads / n_kv_heads in {1, 2, 4, 8}. */
+int anelm_gqa_attention(float* out, const float* q, const void* k_cache, const void* v_cache,
+                        int kv_dtype, int n_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                        int cache_start, int cache_len, int cache_capacity, void* stream);
+
+/* One full-attention decode step, the composition at
+ * models/llm/qwen3_5.cpp:944-1002, fused into one launch:
+ *   per-head RMSNorm of q (rows of q_gate, stride 2*head_dim) and k with
+ *   q_norm_w / k_norm_w (:952-959); RoPE (:961-971); fp16 ring append of k, v
+ *   (:973-986); gqa_attention (:989-991); sigmoid output gate when `gate`
+ *   (:993-1000).
+ * q_gate [n_heads][2*head_dim], k/v [n_kv_heads][head_dim] are read only.
+ * *cache_start / *cache_len are HOST ints advanced as the KVCache ring does.
+ * cos_row/sin_row: HOST, as for anelm_apply_rope. */
+int anelm_full_attn_decode(float* out, const float* q_gate, const float* k, const float* v,
+                           uint16_t* k_cache, uint16_t* v_cache,
+                           const float* q_norm_w, const float* k_norm_w,
+                           int n_heads, int n_kv_heads, int head_dim, int rot_dim,
+                           int pos, float theta, float eps, int rope_mode, int gate,
+                           const float* cos_row, const float* sin_row,
+                           int* cache_start, int* cache_len, int cache_capacity, void* stream);
+
+/* Batched decode over paged fp16 caches (no reference kernel: per sequence it
+ * is gqa_attention, cpu_ops.cpp:148-204, over that sequence's keys).
+ * n_pages pages hold page_size tokens each as [page][n_kv_heads][page_size][head_dim].
+ * Sequence s attends keys 0..min(seq_lens[s], max_seq_len)-1 (an empty
+ * sequence yields zeros); key t lives in page page_table[s*max_pages + t/page_size]
+ * (clamped to [0, n_pages)) at row t%page_size.
+ * q [n_seqs][n_heads][q_head_stride]; out [n_seqs][n_heads][head_dim].
+ * seq_lens, page_table: device int32. */
+int anelm_attn_decode_paged(float* out, const float* q, int q_head_stride,
+                            const uint16_t* k_pages, const uint16_t* v_pages,
+                            const int32_t* page_table, const int32_t* seq_lens,
+                            int n_seqs, int max_pages, int page_size, int n_pages, int max_seq_len,
+                            int n_heads, int n_kv_heads, int head_dim, void* stream);
+
+/* Causal GQA prefill (no reference kernel: generate.cpp:76-84 runs the
+ * decode core per token, so row t attends keys 0..t).  q [S][Hq][D],
+ * k/v [S][Hkv][D] fp16; out [S][Hq][D] fp32 (out_dtype ANELM_F32) or fp16.
+ * head_dim 256 or 128; Hq % Hkv == 0. */
+int anelm_attn_prefill(void* out, int out_dtype, const uint16_t* q, const uint16_t* k,
+                       const uint16_t* v, int S, int n_heads, int n_kv_heads, int head_dim,
+                       void* stream);
+
+/* ------------------------------------------------------------- DeltaNet */
+
+/* ssm_step, cpu_ops.h:50-51 / cpu_ops.cpp:131-146, for one head:
+ * state [key_dim][value_dim] fp32 updated in place, y [value_dim].
+ * decay and beta are scalars (HOST floats), order as ANELM_DN_ORDER_*. */
+int anelm_ssm_step(float* y, float* state, const float* q, const float* k, const float* v,
+                   float decay, float beta, int key_dim, int value_dim, int flags, void* stream);
+
+/* One Gated-DeltaNet decode step for all heads, the composition at
+ * models/llm/qwen3_5.cpp:879-908 after conv/SiLU:
+ *   q,k [Hk][dk] (read only), v [Hv][dv], a,b [Hv] projections,
+ *   A [Hv] = exp(A_log) (qwen3_5.cpp:417-421), dt_bias [Hv];
+ *   beta = sigmoid(b), decay = exp(-A*softplus(a+dt_bias)) (:896-898);
+ *   value head h uses key head h/(Hv/Hk) (:890);
+ *   state [Hv][dk][dv] fp32 updated in place; y [Hv][dv];
+ *   with ANELM_DN_GATED_NORM, y = rmsnorm_gated(y, z [Hv][dv], norm_w [dv]).
+ * dk, dv = 128. */
+int anelm_deltanet_decode(float* y, float* state, const float* q, const float* k, const float* v,
+                          const float* a, const float* b, const float* A, const float* dt_bias,
+                          const float* z, const float* norm_w,
+                          int Hk, int Hv, int dk, int dv, int flags, void* stream);
+
+/* Chunked DeltaNet prefill over S tokens (no reference kernel: the reference
+ * runs ssm_step per token, qwen3_5.cpp:1204-1217).  q,k [S][Hk][dk],
+ * v [S][Hv][dv], a,b [S][Hv]; y [S][Hv][dv]; state [Hv][dk][dv] updated to the
+ * state after token S-1.  chunk = 64.  Flags as anelm_deltanet_decode minus
+ * GATED_NORM.  dk, dv = 128. */
+int anelm_deltanet_prefill(float* y, float* state, const float* q, const float* k, const float* v,
+                           const float* a, const float* b, const float* A, const float* dt_bias,
+                           int S, int Hk, int Hv, int dk, int dv, int chunk, int flags, void* stream);
+
+/* ----------------------------------------------------------------- LUT6 */
+/* LUT6 weight format: W[r][c] = lut[r/32][idx(r,c)], lut fp16 [out/32][64],
+ * idx 6-bit, row-major, row r at w + r*in_dim*3/4 bytes, index c at bits
+ * [6c, 6c+6) of the little-endian row stream (4 indices per 3 bytes).
+ * out_dim % 32 == 0, in_dim % 16 == 0. */
+
+/* Unpack n (multiple of 4) indices to one byte each. */
+int anelm_lut6_unpack(uint8_t* idx, const uint8_t* packed, int64_t n, void* stream);
+
+/* y = W x (matvec, cpu_ops.cpp:77-80, on the dequantised weights). */
+int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x,
+                    int out_dim, int in_dim, void* stream);
+
+/* SwiGLU FFN block with residual (qwen3_5.cpp:1335-1354 with the MLP of
+ * :1118-1130): n = rmsnorm(x, norm_w, eps) (skipped when norm_w is NULL);
+ * x += down( silu(gate n) * (up n) ).  x [hidden] is updated in place;
+ * h_scratch [inter] receives the SwiGLU activations. */
+int anelm_lut6_ffn(float* x, float* h_scratch, const float* norm_w, float eps,
+                   const uint8_t* gate_w, const uint16_t* gate_lut,
+                   const uint8_t* up_w, const uint16_t* up_lut,
+                   const uint8_t* down_w, const uint16_t* down_lut,
+                   int hidden, int inter, void* stream);
+
+/* The gate/up half of the FFN block alone (qwen3_5.cpp:1118-1124):
+ * h = silu(gate n) * (up n), n = rmsnorm(x, norm_w, eps) (x when norm_w is
+ * NULL).  x [hidden], h [inter]. */
+int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
+                      const uint8_t* gate_w, const uint16_t* gate_lut,
+                      const uint8_t* up_w, const uint16_t* up_lut,
+                      int hidden, int inter, void* stream);
+
+/* Top-k of logits = W x for a batch of inputs (in-model top-k LM head,
+ * scripts/export_hybrid_chunks.py:409-421).  x [batch][in_dim] fp32;
+ * out_idx / out_val [batch][k], ordered by (value desc, index asc), so
+ * out_idx[b*k] is the greedy token of core/sampling.cpp:47-53.  k <= 64. */
+int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
+                    const float* x, int batch, int out_dim, int in_dim, int k, void* stream);
+
+/* ------------------------------------------------- hybrid decode step */
+/* The layer loop of Qwen35Model::forward (models/llm/qwen3_5.cpp:1278-1356)
+ * over the compute cores: per layer the DeltaNet core (:849-910) or the
+ * full-attention core (:944-1002), then the FFN block with residual
+ * (:1335-1354).  The projections around the cores (first_proj, o_proj) are
+ * not part of it: each layer's core reads its own input buffers and writes
+ * core_out; the FFN chain carries the hidden state x from layer to layer.
+ * Layer kinds follow qwen3_5.cpp:64-71. */
+#define ANELM_LAYER_DELTANET 0
+#define ANELM_LAYER_ATTENTION 1
+
+typedef struct {
+    int kind;
+    /* full-attention core (kind ANELM_LAYER_ATTENTION) */
+    const float* q_gate;        /* [Hq][2D] */
+    const float* k;             /* [Hkv][D] */
+    const float* v;
+    uint16_t* k_cache;          /* fp16 ring [cap][Hkv][D] */
+    uint16_t* v_cache;
+    const float* q_norm_w;
+    const float* k_norm_w;
+    int cache_start, cache_len, cache_capacity, pos;
+    /* DeltaNet core (kind ANELM_LAYER_DELTANET), flags as anelm_deltanet_decode */
+    float* state;               /* [Hv][dk][dv] */
+    const float* dn_q;          /* [Hk][dk] */
+    const float* dn_k;
+    const float* dn_v;          /* [Hv][dv] */
+    const float* dn_a;
+    const float* dn_b;
+    const float* dn_A;
+    const float* dn_dt_bias;
+    const float* dn_z;          /* [Hv][dv] or NULL (no gated norm) */
+    const float* dn_norm_w;
+    int dn_flags;
+    float* core_out;            /* [Hq*D] or [Hv*dv] */
+    /* FFN block: x += down(silu(gate n) * (up n)), n = rmsnorm(x, ffn_norm_w) */
+    const float* ffn_norm_w;
+    const uint8_t* gate_w;
+    const uint16_t* gate_lut;
+    const uint8_t* up_w;
+    const uint16_t* up_lut;
+    const uint8_t* down_w;
+    const uint16_t* down_lut;
+} anelm_hybrid_layer;
+
+typedef struct {
+    int hidden, inter;
+    int n_heads, n_kv_heads, head_dim, rot_dim, rope_mode;
+    float theta, eps;
+    int lin_k_heads, lin_v_heads, lin_dim;
+} anelm_hybrid_dims;
+
+typedef struct anelm_hybrid_step anelm_hybrid_step;
+
+/* Builds a step over n_layers descriptors (copied), x [hidden] and
+ * h_scratch [inter] device buffers.  With use_graph, the step's launches are
+ * captured once into a HIP graph on `stream` (which must not be the null
+ * stream) after one eager warm-up run; each run then replays the same work
+ * -- the attention rings do not advance between replays.  Without it, each
+ * run launches eagerly and advances every attention ring and position by one
+ * token, as the model's decode loop does. */
+int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hybrid_dims* dims,
+                             const anelm_hybrid_layer* layers, int n_layers, float* x,
+                             float* h_scratch, int use_graph, void* stream);
+int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream);
+int anelm_hybrid_step_destroy(anelm_hybrid_step* step);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANELM_H */

@@ -1,0 +1,104 @@
+"""GPU parity of the LUT6 kernels: exhaustive unpack, GEMV, the fused
+SwiGLU FFN block with residual, and the top-k LM head."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_close, rel_l2, to_dev, to_host
+from workloads import lut6_matrix, widen
+
+pytestmark = pytest.mark.gpu
+
+
+def test_unpack_exhaustive(anelm, dev):
+    """All 2^24 three-byte patterns unpack bit-exactly."""
+    w = np.arange(1 << 24, dtype=np.uint32)
+    packed = np.stack([w & 0xff, (w >> 8) & 0xff, (w >> 16) & 0xff], 1).astype(np.uint8).reshape(-1)
+    idx = to_host(anelm.ops.lut6_unpack(to_dev(packed, dev), 4 << 24)).reshape(-1, 4)
+    for j in range(4):
+        assert np.array_equal(idx[:, j].astype(np.uint32), (w >> (6 * j)) & 63)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(9216, 2560), (2560, 9216), (96, 160), (64, 1024),
+                                            (3584, 1024), (1024, 3584), (256, 16384 - 16)])
+def test_gemv(anelm, orc, dev, out_dim, in_dim):
+    packed, lut, _ = lut6_matrix(600 + out_dim, out_dim, in_dim)
+    x = np.random.default_rng(601).standard_normal(in_dim).astype(np.float32)
+    got = to_host(anelm.ops.lut6_gemv(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev),
+                                      out_dim, in_dim))
+    assert_close(got, orc.lut6_matvec(packed, lut, x, out_dim, in_dim), what=f"{out_dim}x{in_dim}")
+
+
+@pytest.mark.parametrize("hidden,inter", [(2560, 9216), (1024, 3584), (64, 96)])
+def test_ffn_block(anelm, orc, dev, hidden, inter):
+    """x += down(silu(gate n) * (up n)), n = rmsnorm(x, w)."""
+    g, u, d = (lut6_matrix(610 + i, *shape) for i, shape in
+               enumerate([(inter, hidden), (inter, hidden), (hidden, inter)]))
+    rng = np.random.default_rng(611)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    xd = to_dev(x, dev)
+    h = torch.empty(inter, device=dev)
+    dg, du, dd = ((to_dev(m[0], dev), to_dev(m[1], dev)) for m in (g, u, d))
+    anelm.ops.lut6_ffn_(xd, h, to_dev(w, dev), 1e-6, dg, du, dd, hidden, inter)
+    n = orc.rmsnorm(x, w, 1e-6)
+    want = x + orc.lut6_ffn(n, g[:2], u[:2], d[:2], hidden, inter)
+    assert_close(to_host(xd), want, what="ffn")
+    # without the norm
+    xd = to_dev(x, dev)
+    anelm.ops.lut6_ffn_(xd, h, None, 1e-6, dg, du, dd, hidden, inter)
+    assert_close(to_host(xd), x + orc.lut6_ffn(x, g[:2], u[:2], d[:2], hidden, inter))
+
+
+def _check_topk(orc, idx, val, logits, k):
+    """Indices bit-exact against the oracle's top-k of the oracle logits
+    wherever neighbouring values are separated by more than the fp32
+    summation-order error; values within the parity bar."""
+    oi, ov = orc.topk(logits, k)
+    assert_close(val, ov, rel=1e-5, max_abs=1e-4)
+    rest = logits.copy()
+    rest[oi] = -np.inf
+    gaps = np.abs(np.diff(np.concatenate([ov, [rest.max()]])))
+    tol = 1e-5 * max(1.0, float(np.abs(ov).max()))
+    safe = np.all(gaps > tol)
+    if safe:
+        assert np.array_equal(idx, oi)
+    else:   # near-ties: the sets agree up to swaps inside tied groups
+        assert set(idx[:-1]) <= set(np.nonzero(logits >= ov[-1] - tol)[0])
+    return safe
+
+
+@pytest.mark.parametrize("out_dim,in_dim,batch,k", [(262144, 2560, 2, 32), (4096, 1024, 3, 64),
+                                                    (8192, 2560, 1, 1)])
+def test_topk(anelm, orc, dev, out_dim, in_dim, batch, k):
+    packed, lut, _ = lut6_matrix(620 + k, out_dim, in_dim)
+    x = np.random.default_rng(621).standard_normal((batch, in_dim)).astype(np.float32)
+    idx, val = anelm.ops.lut6_topk(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim,
+                                   in_dim, k)
+    idx, val = to_host(idx), to_host(val)
+    for b in range(batch):
+        logits = orc.lut6_matvec(packed, lut, x[b], out_dim, in_dim)
+        _check_topk(orc, idx[b], val[b], logits, k)
+        if k == 1:
+            assert idx[b, 0] == orc.argmax(logits)
+
+
+def test_topk_ties_prefer_lower_index(anelm, orc, dev):
+    """Two identical rows of one LUT group give bit-identical logits: the
+    lower row index ranks first (core/sampling.cpp:47-53 keeps the first
+    maximum)."""
+    out_dim, in_dim = 2048, 256
+    packed, lut, _ = lut6_matrix(630, out_dim, in_dim)
+    x = np.random.default_rng(631).standard_normal(in_dim).astype(np.float32)
+    logits = orc.lut6_matvec(packed, lut, x, out_dim, in_dim)
+    top = int(np.argmax(logits))
+    twin = (top // 32) * 32 + ((top % 32) + 16) % 32
+    packed = packed.copy()
+    packed[twin] = packed[top]
+    dp, dl, dx = to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev)
+    for k in (1, 2, 8):
+        idx, val = anelm.ops.lut6_topk(dp, dl, dx, out_dim, in_dim, k)
+        idx, val = to_host(idx)[0], to_host(val)[0]
+        assert idx[0] == min(top, twin)
+        if k > 1:
+            assert idx[1] == max(top, twin) and val[0] == val[1]

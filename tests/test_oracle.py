@@ -1,0 +1,448 @@
+"""Pins the CPU oracle (oracle/anelm_oracle.c) before it is trusted as the
+checker.  The reference ships no tests or golden vectors for this path, and
+its cpu_ops.cpp needs Apple Accelerate (unbuildable here), so every oracle
+function is checked against what the mathematics fixes: float64 brute force
+written independently in numpy, closed forms, special cases and invariants.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from workloads import (attn_decode_case, deltanet_case, f16, lut6_dense, lut6_matrix, pack_lut6,
+                       widen)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+# ------------------------------------------------------------------ fp16
+def test_f16_to_f32_exhaustive(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    got = orc.f16_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_round_to_nearest_even(orc):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 200000),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 1e9, 2.0 ** -24, 2.0 ** -25,
+                  2.0 ** -25 * 1.0000001, 3 * 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 * (1 - 2 ** -11),
+                  1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, np.inf, -np.inf], np.float32),
+        # every fp16 value and the midpoints between neighbours (ties)
+        np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float32),
+    ])
+    x = x.astype(np.float32)
+    mids = (x[-0x7c00:-1].astype(np.float64) + x[-0x7bff:].astype(np.float64)) / 2
+    x = np.concatenate([x, mids.astype(np.float32)])
+    assert x.dtype == np.float32
+    got = orc.f32_to_f16(x)
+    assert np.array_equal(got, _f16_rne_reference(x))
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, x.astype(np.float16).view(np.uint16))
+
+
+def _f16_rne_reference(x):
+    """Round-to-nearest-even onto the fp16 grid, derived independently of any
+    float16 cast: the fp16 spacing of |x|'s binade is 2^(e-10) (e >= -14),
+    np.rint rounds half to even exactly in float64, and the rounded value is
+    then exactly representable, so the final cast cannot round."""
+    a = np.abs(x.astype(np.float64))
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    ulp = np.exp2(np.clip(e, -14, 15) - 10)
+    r = np.rint(a / ulp) * ulp
+    r = np.where(r >= 65520.0, np.inf, r)
+    r = np.where(np.isinf(a), np.inf, r)
+    return (np.copysign(r, x.astype(np.float64))).astype(np.float16).view(np.uint16)
+
+
+# --------------------------------------------------------------- norms
+def test_rmsnorm_closed_form(orc):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((5, 256)).astype(np.float32) * 3
+    w = (1 + 0.02 * rng.standard_normal(256)).astype(np.float32)
+    got = orc.rmsnorm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    assert rel_l2(got, want) < 1e-6
+    # unit weights: the output has RMS 1
+    ones = orc.rmsnorm(x, np.ones(256, np.float32), 0.0)
+    assert np.allclose(np.sqrt((ones.astype(np.float64) ** 2).mean(-1)), 1.0, atol=1e-6)
+
+
+def test_rmsnorm_gated_closed_form(orc):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4, 128)).astype(np.float32)
+    z = rng.standard_normal((4, 128)).astype(np.float32)
+    w = rng.standard_normal(128).astype(np.float32)
+    got = orc.rmsnorm_gated(x, z, w)
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    n = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    want = n * z64 / (1 + np.exp(-z64))     # rmsnorm * silu(z)
+    assert rel_l2(got, want) < 1e-6
+
+
+def test_l2_normalize(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(128).astype(np.float32) * 7
+    got = orc.l2_normalize(x)
+    assert abs(np.linalg.norm(got.astype(np.float64)) - 1) < 1e-6
+    assert rel_l2(got, x / np.linalg.norm(x.astype(np.float64))) < 1e-6
+    # the eps (1e-12) keeps a zero vector at zero
+    assert np.all(orc.l2_normalize(np.zeros(16, np.float32)) == 0)
+
+
+def test_activations(orc):
+    x = np.linspace(-20, 20, 1001).astype(np.float32)
+    z = np.linspace(5, -5, 1001).astype(np.float32)
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    assert rel_l2(orc.silu(x), x64 / (1 + np.exp(-x64))) < 1e-6
+    assert rel_l2(orc.mul_sigmoid(x, z), x64 / (1 + np.exp(-z64))) < 1e-6
+
+
+def test_softmax(orc):
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(777) * 5).astype(np.float32)
+    got = orc.softmax(x)
+    e = np.exp(x.astype(np.float64) - x.max())
+    assert rel_l2(got, e / e.sum()) < 1e-6
+    assert abs(got.astype(np.float64).sum() - 1) < 1e-5
+    assert np.allclose(orc.softmax(np.full(10, 3.0, np.float32)), 0.1)
+
+
+def test_matvec(orc):
+    rng = np.random.default_rng(5)
+    W = rng.standard_normal((33, 70)).astype(np.float32)
+    x = rng.standard_normal(70).astype(np.float32)
+    assert rel_l2(orc.matvec(W, x), W.astype(np.float64) @ x) < 1e-6
+    # a transposed operand would give a different answer
+    assert rel_l2(orc.matvec(W[:, :33].T.copy(), x[:33]), W[:, :33].astype(np.float64) @ x[:33]) > 0.1
+
+
+# ----------------------------------------------------------------- RoPE
+def _rope_ref(v, rot, pos, theta, mode):
+    """float64 rotation; the frequency is rounded to fp32 as the reference
+    computes it (1.0f / powf(theta, i/rot)), the angle pos*freq is exact here."""
+    v = v.astype(np.float64).copy()
+    half = rot // 2
+    for j in range(half):
+        freq = float(np.float32(1.0 / float(np.float32(theta ** float(np.float32(2 * j / rot))))))
+        a = float(np.float32(pos * freq))
+        c, s = math.cos(a), math.sin(a)
+        i0, i1 = (2 * j, 2 * j + 1) if mode == 0 else (j, j + half)
+        v0, v1 = v[..., i0].copy(), v[..., i1].copy()
+        v[..., i0] = v0 * c - v1 * s
+        v[..., i1] = v0 * s + v1 * c
+    return v
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("pos", [0, 1, 512, 8191])
+def test_rope(orc, mode, pos):
+    rng = np.random.default_rng(6 + pos)
+    D, rot, nq, nkv = 256, 64, 3, 2
+    q = rng.standard_normal((nq, 2 * D)).astype(np.float32)
+    k = rng.standard_normal((nkv, D)).astype(np.float32)
+    gq, gk = orc.apply_rope(q, k, nq, nkv, D, 2 * D, D, rot, pos, 1e7, mode=mode)
+    # dims >= rot_dim and the gate half of q are untouched
+    assert np.array_equal(gq[:, rot:], q[:, rot:])
+    assert np.array_equal(gk[:, rot:], k[:, rot:])
+    if pos == 0:
+        assert np.array_equal(gq, q) and np.array_equal(gk, k)
+    # float64 reference with the reference's fp32 frequency; powf/cosf may
+    # differ from the correctly rounded values by an ulp, which a large
+    # position amplifies in the angle
+    tol = 1e-5 if pos < 1000 else 2e-3
+    assert rel_l2(gq[:, :rot], _rope_ref(q[:, :rot], rot, pos, 1e7, mode)) < tol
+    assert rel_l2(gk[:, :rot], _rope_ref(k[:, :rot], rot, pos, 1e7, mode)) < tol
+    # with explicit cos/sin rows (the table path) the rotation is plain fp32
+    # arithmetic, reproduced exactly by numpy float32
+    c = rng.standard_normal(rot // 2).astype(np.float32)
+    s = rng.standard_normal(rot // 2).astype(np.float32)
+    tq, _ = orc.apply_rope(q, k, nq, nkv, D, 2 * D, D, rot, pos, 1e7, c, s, mode=mode)
+    i0 = np.arange(0, rot, 2) if mode == 0 else np.arange(rot // 2)
+    i1 = i0 + (1 if mode == 0 else rot // 2)
+    ref = q.copy()
+    ref[:, i0] = q[:, i0] * c - q[:, i1] * s
+    ref[:, i1] = q[:, i0] * s + q[:, i1] * c
+    assert np.array_equal(tq, ref)
+    # rotation preserves the norm of every rotated pair
+    half = rot // 2
+    idx0 = np.arange(0, rot, 2) if mode == 0 else np.arange(half)
+    idx1 = idx0 + (1 if mode == 0 else half)
+    n_in = q[:, idx0].astype(np.float64) ** 2 + q[:, idx1].astype(np.float64) ** 2
+    n_out = gq[:, idx0].astype(np.float64) ** 2 + gq[:, idx1].astype(np.float64) ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5)
+
+
+def test_rope_half_split_is_a_permutation_of_interleaved(orc):
+    rng = np.random.default_rng(7)
+    D, rot = 128, 64
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    perm = np.concatenate([np.arange(0, rot, 2), np.arange(1, rot, 2), np.arange(rot, D)])
+    inter, _ = orc.apply_rope(x, x, 1, 0, D, D, D, rot, 37, 1e7, mode=0)
+    half, _ = orc.apply_rope(x[:, perm], x, 1, 0, D, D, D, rot, 37, 1e7, mode=1)
+    assert np.array_equal(half, inter[:, perm])
+
+
+def test_rope_table_matches_on_the_fly(orc):
+    c, s = orc.rope_table(600, 64, 1e7)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((2, 256)).astype(np.float32)
+    for pos in (0, 5, 599):
+        a, _ = orc.apply_rope(q, q, 2, 0, 256, 256, 256, 64, pos, 1e7)
+        b, _ = orc.apply_rope(q, q, 2, 0, 256, 256, 256, 64, pos, 1e7, c[pos], s[pos])
+        assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------------ attention
+def _attn_ref(q, kc, vc, nh, nkv, D, qs, start, length, cap):
+    """float64 softmax attention over ring slots start..start+length-1."""
+    out = np.zeros((nh, D))
+    if length <= 0:
+        return out
+    slots = (start + np.arange(length)) % cap
+    K = kc.reshape(cap, nkv, D)[slots].astype(np.float64)
+    V = vc.reshape(cap, nkv, D)[slots].astype(np.float64)
+    for h in range(nh):
+        g = h // (nh // nkv)
+        qh = q.reshape(-1)[h * qs:h * qs + D].astype(np.float64)
+        sc = K[:, g] @ qh / math.sqrt(D)
+        p = np.exp(sc - sc.max())
+        out[h] = (p / p.sum()) @ V[:, g]
+    return out
+
+
+@pytest.mark.parametrize("nh,nkv,start,length,cap", [
+    (8, 2, 0, 513, 2048), (16, 4, 1500, 700, 2048), (4, 4, 0, 1, 8), (8, 1, 5, 64, 64),
+    (2, 2, 63, 64, 64)])
+def test_gqa_attention_brute_force(orc, nh, nkv, start, length, cap):
+    rng = np.random.default_rng(9 + length)
+    D = 64
+    q = rng.standard_normal((nh, 2 * D)).astype(np.float32)
+    kc = rng.standard_normal((cap, nkv, D)).astype(np.float32)
+    vc = rng.standard_normal((cap, nkv, D)).astype(np.float32)
+    got = orc.gqa_attention(q, kc, vc, nh, nkv, D, 2 * D, start, length, cap)
+    assert rel_l2(got, _attn_ref(q, kc, vc, nh, nkv, D, 2 * D, start, length, cap)) < 1e-5
+
+
+def test_gqa_attention_special_cases(orc):
+    rng = np.random.default_rng(10)
+    D, cap = 32, 16
+    kc = rng.standard_normal((cap, 2, D)).astype(np.float32)
+    vc = rng.standard_normal((cap, 2, D)).astype(np.float32)
+    q = rng.standard_normal((4, D)).astype(np.float32)
+    # cache_len <= 0 -> zeros (cpu_ops.cpp:152-155)
+    assert np.all(orc.gqa_attention(q, kc, vc, 4, 2, D, D, 0, 0, cap) == 0)
+    # one key -> that key's value row, per kv head (heads 0,1 -> kv 0; 2,3 -> kv 1)
+    one = orc.gqa_attention(q, kc, vc, 4, 2, D, D, 7, 1, cap)
+    assert np.allclose(one[:2], vc[7, 0], atol=1e-6) and np.allclose(one[2:], vc[7, 1], atol=1e-6)
+    # a zero query gives uniform weights -> the mean of the values
+    z = orc.gqa_attention(np.zeros_like(q), kc, vc, 4, 2, D, D, 3, 10, cap)
+    slots = (3 + np.arange(10)) % cap
+    assert np.allclose(z[0], vc[slots, 0].mean(0), atol=1e-5)
+    # ring order: start != 0 equals the rotated contiguous cache
+    rot = orc.gqa_attention(q, np.roll(kc, -9, 0), np.roll(vc, -9, 0), 4, 2, D, D, 0, 12, cap)
+    ring = orc.gqa_attention(q, kc, vc, 4, 2, D, D, 9, 12, cap)
+    assert rel_l2(ring, rot) < 1e-6
+
+
+def test_full_attn_decode_composition(orc):
+    c = attn_decode_case(11, n_heads=4, n_kv_heads=2, head_dim=64, cached=40, capacity=48, start=20)
+    out, kc, vc, st, ln = orc.full_attn_decode(
+        c.q_gate, c.k, c.v, c.k_cache, c.v_cache, c.q_norm_w, c.k_norm_w, c.n_heads, c.n_kv_heads,
+        c.head_dim, c.rot_dim, c.pos, c.theta, c.eps, 0, True, c.start, c.length, c.capacity)
+    assert (st, ln) == (20, 41)
+    D = c.head_dim
+    qn = np.stack([_rms64(c.q_gate[h, :D], c.q_norm_w) for h in range(4)])
+    kn = np.stack([_rms64(c.k[h], c.k_norm_w) for h in range(2)])
+    qn = _rope_ref(qn, c.rot_dim, c.pos, c.theta, 0)
+    kn = _rope_ref(kn, c.rot_dim, c.pos, c.theta, 0)
+    slot = (20 + 40) % 48
+    assert np.array_equal(kc[slot], f16(kn)) and np.array_equal(vc[slot], f16(c.v))
+    ref = _attn_ref(qn, widen(kc), widen(vc), 4, 2, D, D, 20, 41, 48)
+    ref = ref / (1 + np.exp(-c.q_gate[:, D:].astype(np.float64)))
+    assert rel_l2(out, ref) < 1e-5
+    # full ring: the oldest slot is overwritten and start advances
+    _, kc2, _, st2, ln2 = orc.full_attn_decode(
+        c.q_gate, c.k, c.v, c.k_cache, c.v_cache, c.q_norm_w, c.k_norm_w, 4, 2, D, c.rot_dim,
+        c.pos, c.theta, c.eps, 0, True, 5, 48, 48)
+    assert (st2, ln2) == (6, 48) and np.array_equal(kc2[5], f16(kn))
+
+
+def _rms64(x, w, eps=1e-6):
+    x = x.astype(np.float64)
+    return x / np.sqrt((x ** 2).mean() + eps) * w
+
+
+def test_prefill_is_decode_per_row(orc):
+    rng = np.random.default_rng(12)
+    S, Hq, Hkv, D = 50, 4, 2, 32
+    q, k, v = (f16(rng.standard_normal((S, h, D))) for h in (Hq, Hkv, Hkv))
+    got = orc.prefill_attention(q, k, v)
+    for t in (0, 1, 17, 49):
+        ref = _attn_ref(widen(q[t]), widen(k), widen(v), Hq, Hkv, D, D, 0, t + 1, S)
+        assert rel_l2(got[t], ref) < 1e-5
+    assert np.allclose(got[0, :2], widen(v[0, 0]), atol=1e-6)   # row 0 sees only key 0
+    part = orc.prefill_attention(q, k, v, 10, 20)
+    assert np.array_equal(part, got[10:20])
+
+
+# ------------------------------------------------------------- DeltaNet
+def _ssm_ref(S, q, k, v, decay, beta, order):
+    S = S.astype(np.float64)
+    q, k, v = (x.astype(np.float64) for x in (q, k, v))
+    if order == 0:
+        delta = v - S.T @ k
+        S = decay * S + beta * np.outer(k, delta)
+    else:
+        S = decay * S
+        delta = beta * (v - S.T @ k)
+        S = S + np.outer(k, delta)
+    return S.T @ q, S
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_ssm_step_brute_force(orc, order):
+    rng = np.random.default_rng(13)
+    S = (0.1 * rng.standard_normal((128, 96))).astype(np.float32)
+    q, k = (rng.standard_normal(128).astype(np.float32) for _ in range(2))
+    v = rng.standard_normal(96).astype(np.float32)
+    y, S2 = orc.ssm_step(S, q, k, v, 0.83, 0.61, order)
+    yr, Sr = _ssm_ref(S, q, k, v, 0.83, 0.61, order)
+    assert rel_l2(y, yr) < 1e-5 and rel_l2(S2, Sr) < 1e-6
+
+
+def test_ssm_step_special_cases(orc):
+    rng = np.random.default_rng(14)
+    q, k = (rng.standard_normal(64).astype(np.float32) for _ in range(2))
+    v = rng.standard_normal(32).astype(np.float32)
+    # zero state: S' = beta k v^T, y = beta (k.q) v
+    y, S2 = orc.ssm_step(np.zeros((64, 32), np.float32), q, k, v, 0.5, 0.7, 0)
+    assert np.allclose(S2, 0.7 * np.outer(k, v), atol=1e-6)
+    assert np.allclose(y, 0.7 * float(k.astype(np.float64) @ q) * v, rtol=1e-5, atol=1e-5)
+    # beta = 0, decay = 1: state unchanged, y = S^T q
+    S = rng.standard_normal((64, 32)).astype(np.float32)
+    y, S2 = orc.ssm_step(S, q, k, v, 1.0, 0.0, 0)
+    assert np.array_equal(S2, S) and rel_l2(y, S.T.astype(np.float64) @ q) < 1e-6
+    # both update orders agree when decay = 1 ...
+    ya, Sa = orc.ssm_step(S, q, k, v, 1.0, 0.4, 0)
+    yb, Sb = orc.ssm_step(S, q, k, v, 1.0, 0.4, 1)
+    assert rel_l2(Sa, Sb) < 1e-6 and rel_l2(ya, yb) < 1e-5
+    # ... and differ otherwise (the retrieval reads the un-decayed state in cpu_ops order)
+    ya, _ = orc.ssm_step(S, q, k, v, 0.5, 0.4, 0)
+    yb, _ = orc.ssm_step(S, q, k, v, 0.5, 0.4, 1)
+    assert rel_l2(ya, yb) > 1e-2
+
+
+def test_deltanet_decode_composition(orc):
+    c = deltanet_case(15, Hk=2, Hv=4, dk=128, dv=128)
+    for flags in (1, 3, 5):
+        y, S2 = orc.deltanet_decode(c.state, c.q, c.k, c.v, c.a, c.b, c.A, c.dt_bias, flags,
+                                    c.z, c.norm_w)
+        for h in range(4):
+            kh = h // 2
+            qq = c.q[kh].astype(np.float64) / np.linalg.norm(c.q[kh].astype(np.float64)) / math.sqrt(128)
+            kk = c.k[kh].astype(np.float64) / np.linalg.norm(c.k[kh].astype(np.float64))
+            beta = 1 / (1 + math.exp(-c.b[h]))
+            decay = math.exp(-c.A[h] * math.log1p(math.exp(c.a[h] + c.dt_bias[h])))
+            yr, Sr = _ssm_ref(c.state[h], qq, kk, c.v[h], decay, beta, (flags >> 1) & 1)
+            if flags & 4:
+                n = yr / np.sqrt((yr ** 2).mean() + 1e-6) * c.norm_w
+                yr = n * c.z[h] / (1 + np.exp(-c.z[h].astype(np.float64)))
+            assert rel_l2(y[h], yr) < 1e-5 and rel_l2(S2[h], Sr) < 1e-5
+
+
+def test_deltanet_prefill_is_sequential_decode(orc):
+    c = deltanet_case(16, Hk=2, Hv=4, S=9)
+    y, S2 = orc.deltanet_prefill(c.state, c.q, c.k, c.v, c.a, c.b, c.A, c.dt_bias, 1)
+    state = c.state
+    for t in range(9):
+        yt, state = orc.deltanet_decode(state, c.q[t], c.k[t], c.v[t], c.a[t], c.b[t], c.A,
+                                        c.dt_bias, 1)
+        assert np.array_equal(yt, y[t])
+    assert np.array_equal(state, S2)
+
+
+def test_conv1d_update_ring(orc):
+    rng = np.random.default_rng(17)
+    C, K = 10, 4
+    w = rng.standard_normal((C, K)).astype(np.float32)
+    st = np.zeros((C, K - 1), np.float32)
+    pos = 0
+    hist = []
+    for t in range(9):
+        x = rng.standard_normal(C).astype(np.float32)
+        hist.append(x.astype(np.float64))
+        y, st, pos = orc.conv1d_update(st, pos, x, w, K)
+        # y = sum_j w[:, j] * x_{t-(K-1)+j} (zeros before the first input)
+        past = [hist[t - (K - 1) + j] if t - (K - 1) + j >= 0 else np.zeros(C) for j in range(K)]
+        ref = sum(w[:, j] * past[j] for j in range(K))
+        assert rel_l2(y, ref) < 1e-6
+        assert pos == (t + 1) % (K - 1)
+
+
+# ----------------------------------------------------------------- LUT6
+def test_lut6_unpack_exhaustive(orc):
+    """Every 24-bit pattern unpacks to the four 6-bit fields, LSB first."""
+    w = np.arange(1 << 24, dtype=np.uint32)
+    packed = np.stack([w & 0xff, (w >> 8) & 0xff, (w >> 16) & 0xff], 1).astype(np.uint8).reshape(-1)
+    idx = orc.lut6_unpack(packed, 4 << 24).reshape(-1, 4).astype(np.uint32)
+    for j in range(4):
+        assert np.array_equal(idx[:, j], (w >> (6 * j)) & 63)
+    assert np.array_equal(orc.lut6_pack(idx.astype(np.uint8).reshape(-1)), packed)
+
+
+def test_lut6_pack_matches_numpy_packer(orc):
+    rng = np.random.default_rng(18)
+    idx = rng.integers(0, 64, 4096, dtype=np.uint8)
+    assert np.array_equal(orc.lut6_pack(idx), pack_lut6(idx))
+    # the bit layout of the first group by hand: i0 | i1<<6 | i2<<12 | i3<<18
+    p = orc.lut6_pack(np.array([1, 2, 3, 63], np.uint8))
+    assert int(p[0]) | int(p[1]) << 8 | int(p[2]) << 16 == 1 | 2 << 6 | 3 << 12 | 63 << 18
+
+
+def test_lut6_matvec_dequant(orc):
+    packed, lut, idx = lut6_matrix(19, 96, 160, lut_std=1.0)
+    x = np.random.default_rng(20).standard_normal(160).astype(np.float32)
+    W = lut6_dense(idx, lut)
+    got = orc.lut6_matvec(packed, lut, x, 96, 160)
+    assert rel_l2(got, W.astype(np.float64) @ x) < 1e-6
+    # rows use the LUT of their own 32-row group
+    lut_shift = np.roll(lut, 1, axis=0)
+    assert rel_l2(orc.lut6_matvec(packed, lut_shift, x, 96, 160), W.astype(np.float64) @ x) > 0.1
+    assert np.array_equal(orc.lut6_matvec(packed, lut, x, 96, 160, 32, 64), got[32:64])
+
+
+def test_lut6_ffn_swiglu(orc):
+    H, I = 64, 96
+    g = lut6_matrix(21, I, H, 0.3)
+    u = lut6_matrix(22, I, H, 0.3)
+    d = lut6_matrix(23, H, I, 0.3)
+    x = np.random.default_rng(24).standard_normal(H).astype(np.float32)
+    got = orc.lut6_ffn(x, g[:2], u[:2], d[:2], H, I)
+    G, U, Dn = (lut6_dense(m[2], m[1]).astype(np.float64) for m in (g, u, d))
+    gx = G @ x
+    ref = Dn @ (gx / (1 + np.exp(-gx)) * (U @ x))
+    assert rel_l2(got, ref) < 1e-5
+
+
+def test_topk_and_argmax(orc):
+    rng = np.random.default_rng(25)
+    logits = rng.standard_normal(10000).astype(np.float32)
+    logits[[17, 4000, 9999]] = 9.0   # ties at the top: index order decides
+    logits[[3, 5]] = 8.5
+    idx, val = orc.topk(logits, 32)
+    order = np.lexsort((np.arange(logits.size), -logits.astype(np.float64)))[:32]
+    assert np.array_equal(idx, order) and np.array_equal(val, logits[order])
+    assert list(idx[:5]) == [17, 4000, 9999, 3, 5]
+    assert orc.argmax(logits) == 17
+    assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
