@@ -96,16 +96,61 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }
 
-// Full-wave (64-lane) sum; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+// Value of the stage-M exchange partner of this lane.  The partner differs
+// from the lane in bit M and agrees in every bit above M:
+//   M = 1, 2 : lane ^ M                     (DPP quad permute)
+//   M = 4    : mirror within 8 lanes        (DPP row_half_mirror)
+//   M = 8    : mirror within 16 lanes       (DPP row_mirror)
+//   M = 16   : lane ^ 16 within 32 lanes    (ds_swizzle, no LDS access)
+//   M = 32   : lane ^ 32                    (ds_bpermute)
+// Butterfly reductions that visit M from high to low only rely on those two
+// properties, so they sum exactly the same lane sets as a pure XOR butterfly.
+template <int M>
+__device__ __forceinline__ float partner(float v) {
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (M == 1) r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M == 4) r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+    else if constexpr (M == 8) r = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
+    else if constexpr (M == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);
+    else r = __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), x);
+    return __int_as_float(r);
+}
+
+template <int M = 32>
+__device__ __forceinline__ float wave_sum_from(float v) {
+    if constexpr (M >= 1) return wave_sum_from<M / 2>(v + partner<M>(v));
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+template <int M = 32>
+__device__ __forceinline__ float wave_max_from(float v) {
+    if constexpr (M >= 1) return wave_max_from<M / 2>(fmaxf(v, partner<M>(v)));
     return v;
+}
+
+// Full-wave (64-lane) sum / max; every lane receives the result.
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_from<32>(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_max_from<32>(v); }
+
+// Reduces R partial values held by each of L consecutive lanes (L a power of
+// two <= 32, lanes aligned to L) so that lane li = lane % L ends with the
+// totals of value indices (R/L)*li + j in v[j], j < R/L.  Each stage halves
+// the live values: the lane keeps the half selected by its stage bit and
+// adds the partner's copy of it.
+template <int L, int R, int M = L / 2, int N = R>
+__device__ __forceinline__ void transpose_reduce(float (&v)[R], int li) {
+    static_assert(R >= L, "transpose_reduce needs R >= L");
+    if constexpr (M >= 1) {
+        const bool up = (li & M) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; i++) {
+            const float send = up ? v[i] : v[i + N / 2];
+            const float keep = up ? v[i + N / 2] : v[i];
+            v[i] = keep + partner<M>(send);
+        }
+        transpose_reduce<L, R, M / 2, N / 2>(v, li);
+    }
 }
 
 // Block-wide sum for blockDim.x == NT (multiple of 64); `red` holds NT/64

@@ -6,8 +6,9 @@
 // and re-reads K/V per q head; here one workgroup owns (kv head, key split) and
 // scores all G = Hq/Hkv query heads of that kv head against each K/V row read
 // once.  Splits are merged with the standard (max, sum, unnormalised output)
-// log-sum-exp combine, done by the last workgroup of each split group (two
-// levels), so the whole step is one launch.
+// log-sum-exp combine in a second small kernel (a kernel boundary publishes
+// the partials; an in-kernel last-block combine would need agent-scope fences,
+// each of which writes back the L2 of the issuing XCD).
 #include "anelm_internal.hpp"
 
 #include <algorithm>
@@ -19,7 +20,6 @@ namespace {
 
 constexpr int kNT = 256;      // threads per workgroup
 constexpr int kNW = kNT / 64;  // waves per workgroup
-constexpr int kMaxKps = 512;  // keys per split held in LDS
 
 struct DecodeParams {
     float* out;
@@ -30,10 +30,8 @@ struct DecodeParams {
     int n_kv_heads;
     int start, len, cap;       // ring mode
     float scale;
-    int kps, max_splits, cg, max_groups;
-    float* part;       // level-1 partials [seq][Hkv][max_splits][G][D+2]
-    float* part2;      // level-2 partials [seq][Hkv][max_groups][G][D+2]
-    uint32_t* cnt;     // [seq][Hkv][max_groups] level-1, then [seq][Hkv] level-2
+    int kps, max_splits;
+    float* part;       // partials [seq][Hkv][max_splits][G][D+2]: m, l, o[D]
     // paged mode: pages [page][Hkv][page_size][D]; key t of sequence s is
     // row t % page_size of page page_table[s*max_pages + t/page_size]
     int paged;
@@ -59,11 +57,8 @@ struct DecodeParams {
 struct SeqView {
     const float* q;
     float* out;
-    int len, n_splits, n_groups;
+    int len, n_splits;
     float* part;
-    float* part2;
-    uint32_t* cnt1;
-    uint32_t* cnt2;
 };
 
 template <typename KV> struct Raw8;
@@ -94,29 +89,24 @@ __device__ __forceinline__ void to_f32(const Raw8<float>& r, float (&f)[8]) {
     f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
 }
 
+template <typename KV> __device__ __forceinline__ Raw8<KV> make_raw(const float* v);
+template <> __device__ __forceinline__ Raw8<uint16_t> make_raw<uint16_t>(const float* v) {
+    Raw8<uint16_t> r;
+    r.a.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+    r.a.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    r.a.z = (uint32_t)f2h(v[4]) | ((uint32_t)f2h(v[5]) << 16);
+    r.a.w = (uint32_t)f2h(v[6]) | ((uint32_t)f2h(v[7]) << 16);
+    return r;
+}
+template <> __device__ __forceinline__ Raw8<float> make_raw<float>(const float* v) {
+    Raw8<float> r;
+    r.a = make_float4(v[0], v[1], v[2], v[3]);
+    r.b = make_float4(v[4], v[5], v[6], v[7]);
+    return r;
+}
+
 __device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f2h(v); }
 __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
-
-// Reduces R partial values held by each of L consecutive lanes so that lane
-// `li` (0..L-1) ends with the totals of value indices (R/L)*li + j in v[j].
-template <int L, int R>
-__device__ __forceinline__ void transpose_reduce(float (&v)[R], int li) {
-    static_assert(R >= L, "transpose_reduce needs R >= L");
-    int n = R;
-#pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) {
-        const bool up = (li & m) != 0;
-#pragma unroll
-        for (int i = 0; i < R / 2; i++) {
-            if (i < n / 2) {
-                float send = up ? v[i] : v[i + n / 2];
-                float keep = up ? v[i + n / 2] : v[i];
-                v[i] = keep + shfl_xor(send, m);
-            }
-        }
-        n >>= 1;
-    }
-}
 
 // RMSNorm (cpu_ops.cpp:24-30) + RoPE (cpu_ops.cpp:40-63) of one D-vector held
 // in shared memory, in place.  All threads participate.
@@ -131,42 +121,15 @@ __device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p,
     for (int j = threadIdx.x; j < p.rot_pairs; j += kNT) {
         const int i0 = p.rope_mode == 0 ? 2 * j : j;
         const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
-        const float c = p.cs[j], s = p.sn[j];
+        // read through a pointer into the argument segment: indexing the
+        // by-value array directly expands into a select over every entry
+        const float* cs = p.cs;
+        const float* sn = p.sn;
+        const float c = cs[j], s = sn[j];
         const float v0 = row[i0], v1 = row[i1];
         rotate_pair(row[i0], row[i1], v0, v1, c, s);
     }
     __syncthreads();
-}
-
-// Merges `n` partial records (m, l, o[D]) for G heads at src (record stride
-// G*(D+2) floats) into one record at dst, or, when `final_out` is set, into
-// the normalised (and optionally gated) output rows.
-template <int D, int G>
-__device__ void combine(const float* src, int n, float* dst, bool final_out, int kvh,
-                        const DecodeParams& p, const SeqView& sv) {
-    constexpr int REC = D + 2;
-    for (int e = threadIdx.x; e < G * D; e += kNT) {
-        const int g = e / D, d = e % D;
-        float M = -INFINITY;
-        for (int s = 0; s < n; s++) M = fmaxf(M, src[(size_t)(s * G + g) * REC]);
-        float L = 0.f, O = 0.f;
-        for (int s = 0; s < n; s++) {
-            const float* r = src + (size_t)(s * G + g) * REC;
-            const float f = __expf(r[0] - M);
-            L += r[1] * f;
-            O += r[2 + d] * f;
-        }
-        if (final_out) {
-            const int h = kvh * G + g;
-            float y = O / L;
-            if (p.gate) y = y / (1.0f + expf(-sv.q[(size_t)h * p.q_stride + D + d]));
-            sv.out[(size_t)h * D + d] = y;
-        } else {
-            float* r = dst + (size_t)g * REC;
-            if (d == 0) { r[0] = M; r[1] = L; }
-            r[2 + d] = O;
-        }
-    }
 }
 
 template <typename KV, int D, int G>
@@ -180,10 +143,9 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
 
     __shared__ float q_s[G][D];
     __shared__ float kn_s[D];
-    __shared__ float sc[G][kMaxKps];
+    __shared__ float sc[G][256 / G];
     __shared__ float red_o[kNW][G][D];
     __shared__ float red[kNW];
-    __shared__ int flag;
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -203,49 +165,20 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
     sv.n_splits = (sv.len + p.kps - 1) / p.kps;
     if (split >= sv.n_splits) return;
-    sv.n_groups = (sv.n_splits + p.cg - 1) / p.cg;
     sv.q = p.q + (size_t)seq * Hkv * G * p.q_stride;
     sv.out = p.out + (size_t)seq * Hkv * G * D;
     sv.part = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * G * REC;
-    sv.part2 = p.part2 + ((size_t)seq * Hkv + kvh) * p.max_groups * G * REC;
-    sv.cnt1 = p.cnt + ((size_t)seq * Hkv + kvh) * p.max_groups;
-    sv.cnt2 = p.cnt + (size_t)p.n_seqs * Hkv * p.max_groups + (size_t)seq * Hkv + kvh;
 
-    const int t0 = split * p.kps;
-    const int nk = min(p.kps, sv.len - t0);
+    constexpr int KPS = KPB * KB;     // keys per split (= 256 / G)
+    const int t0 = split * KPS;
+    const int nk = min(KPS, sv.len - t0);
     const size_t tok_stride = (size_t)Hkv * D;
     const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
     const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
+    const bool owner = p.fused && split == sv.n_splits - 1;   // holds the newest key
 
-    // ---- q rows (and, for the split holding the newest key, the append)
-    for (int g = 0; g < G; g++) {
-        const float* src = sv.q + (size_t)(kvh * G + g) * p.q_stride;
-        for (int d = tid; d < D; d += kNT) q_s[g][d] = src[d];
-    }
-    __syncthreads();
-    if (p.fused) {
-        for (int g = 0; g < G; g++) norm_rope_row<D>(q_s[g], p.q_norm_w, p, red);
-        if (split == sv.n_splits - 1) {
-            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
-            __syncthreads();
-            norm_rope_row<D>(kn_s, p.k_norm_w, p, red);
-            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
-            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
-            for (int d = tid; d < D; d += kNT) {
-                store_kv(kw + d, kn_s[d]);
-                store_kv(vw + d, p.v_new[(size_t)kvh * D + d]);
-            }
-            __threadfence();
-            __syncthreads();
-        }
-    }
-
-    float qr[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
-
+    // ---- every K and V row of this lane is requested first, so the HBM
+    // latency overlaps the q prologue below
     const int32_t* ptab = p.paged ? p.page_table + (size_t)seq * p.max_pages : nullptr;
     auto row_ptr = [&](const KV* base, int t) -> const KV* {
         const int lt = t0 + t;
@@ -258,21 +191,60 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         if (phys >= p.cap) phys -= p.cap;
         return base + (size_t)phys * tok_stride + (size_t)kvh * D + dl * 8;
     };
-
-    // ---- scores: KB instructions of key rows per batch, one transpose reduce
-    for (int it = 0; it < nk; it += KPB * KB) {
-        Raw8<KV> raw[KB];
+    Raw8<KV> rk[KB], rv[KB];
 #pragma unroll
-        for (int b = 0; b < KB; b++) {
-            const int t = it + b * KPB + w * KPI + sub;
-            if (t < nk) raw[b] = load_raw(row_ptr(kc, t));
+    for (int b = 0; b < KB; b++) {
+        const int t = b * KPB + w * KPI + sub;
+        if (t < nk) {
+            rk[b] = load_raw(row_ptr(kc, t));
+            rv[b] = load_raw(row_ptr(vc, t));
         }
+    }
+
+    // ---- q rows (and, for the split holding the newest key, the append)
+    for (int g = 0; g < G; g++) {
+        const float* src = sv.q + (size_t)(kvh * G + g) * p.q_stride;
+        for (int d = tid; d < D; d += kNT) q_s[g][d] = src[d];
+    }
+    __syncthreads();
+    if (p.fused) {
+        for (int g = 0; g < G; g++) norm_rope_row<D>(q_s[g], p.q_norm_w, p, red);
+        if (owner) {
+            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
+            __syncthreads();
+            norm_rope_row<D>(kn_s, p.k_norm_w, p, red);
+            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
+            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
+            for (int d = tid; d < D; d += kNT) {
+                store_kv(kw + d, kn_s[d]);
+                store_kv(vw + d, p.v_new[(size_t)kvh * D + d]);
+            }
+            // The row loads above ran before the append: the newest key and
+            // value come from the prologue instead, rounded as stored.
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                if (b * KPB + w * KPI + sub == nk - 1) {
+                    rk[b] = make_raw<KV>(kn_s + dl * 8);
+                    rv[b] = make_raw<KV>(p.v_new + (size_t)kvh * D + dl * 8);
+                }
+            }
+        }
+    }
+
+    float qr[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
+
+    // ---- scores: one transpose reduction over the KB rows of each lane
+    {
         float part[KB * G];
 #pragma unroll
         for (int b = 0; b < KB; b++) {
-            const int t = it + b * KPB + w * KPI + sub;
+            const int t = b * KPB + w * KPI + sub;
             float kf[8];
-            to_f32(raw[b], kf);
+            to_f32(rk[b], kf);
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 float s = 0.f;
@@ -283,7 +255,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         }
         transpose_reduce<LPK, KB * G>(part, dl);
         const int b = dl / G, g = dl % G;
-        const int t = it + b * KPB + w * KPI + sub;
+        const int t = b * KPB + w * KPI + sub;
         if (t < nk) sc[g][t] = part[0] * p.scale;
     }
     __syncthreads();
@@ -314,25 +286,17 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
-    for (int it = 0; it < nk; it += KPB * KB) {
-        Raw8<KV> raw[KB];
 #pragma unroll
-        for (int b = 0; b < KB; b++) {
-            const int t = it + b * KPB + w * KPI + sub;
-            if (t < nk) raw[b] = load_raw(row_ptr(vc, t));
-        }
+    for (int b = 0; b < KB; b++) {
+        const int t = b * KPB + w * KPI + sub;
+        if (t < nk) {
+            float vf[8];
+            to_f32(rv[b], vf);
 #pragma unroll
-        for (int b = 0; b < KB; b++) {
-            const int t = it + b * KPB + w * KPI + sub;
-            if (t < nk) {
-                float vf[8];
-                to_f32(raw[b], vf);
+            for (int g = 0; g < G; g++) {
+                const float pg = sc[g][t];
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float pg = sc[g][t];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pg, vf[i], acc[g][i]);
-                }
+                for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pg, vf[i], acc[g][i]);
             }
         }
     }
@@ -373,49 +337,87 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         rec[(size_t)g * REC + 2 + d] = o;
         if (d == 0) { rec[(size_t)g * REC] = mloc[g]; rec[(size_t)g * REC + 1] = lloc[g]; }
     }
-    __threadfence();
-    __syncthreads();
-    const int grp = split / p.cg;
-    const int gsize = min(p.cg, sv.n_splits - grp * p.cg);
-    if (tid == 0) {
-        uint32_t* c = sv.cnt1 + grp;
-        const uint32_t old = atomicAdd(c, 1u);
-        flag = (old == (uint32_t)gsize - 1);
-        if (flag) atomicExch(c, 0u);
+}
+
+// Log-sum-exp merge of the split partials of one (sequence, q head) for 64
+// output dims per workgroup: M = max m_s, L = sum l_s e^(m_s-M),
+// O = sum o_s e^(m_s-M), out = O / L, then the sigmoid gate.  The 256
+// threads first turn all m_s into weights e^(m_s-M) in LDS, then four groups
+// of 64 threads sum interleaved quarters of the splits.
+constexpr int kCombineChunk = 1024;   // splits weighed per LDS pass
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p) {
+    constexpr int REC = D + 2;
+    __shared__ float f[kCombineChunk];
+    __shared__ float red[4];
+    __shared__ float osum[4][64];
+    const int tid = threadIdx.x, dq = tid & 63, grp = tid >> 6;
+    const int d = blockIdx.x * 64 + dq;
+    const int h = blockIdx.y, seq = blockIdx.z;
+    const int Hkv = p.n_kv_heads;
+    const int kvh = h / G, g = h % G;
+    const int len = p.paged ? min(p.seq_lens[seq], p.len) : p.len;
+    const int n = (len + p.kps - 1) / p.kps;
+    if (n <= 1) return;   // written directly by the split kernel (or zeros)
+    const size_t rs = (size_t)G * REC;   // record stride between splits
+    const float* base = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * rs + (size_t)g * REC;
+    float M = -INFINITY;
+    for (int s = tid; s < n; s += 256) M = fmaxf(M, base[(size_t)s * rs]);
+    M = block_max<256>(M, red);
+    float L = 0.f, O = 0.f;
+    for (int c0 = 0; c0 < n; c0 += kCombineChunk) {
+        const int cn = min(kCombineChunk, n - c0);
+        float lpart = 0.f;
+        for (int s = tid; s < cn; s += 256) {
+            const float* r = base + (size_t)(c0 + s) * rs;
+            const float w = __expf(r[0] - M);
+            f[s] = w;
+            lpart += r[1] * w;
+        }
+        L += block_sum<256>(lpart, red);   // (its barriers also publish f)
+        int s = grp;
+        for (; s + 12 < cn; s += 16) {
+            const float o0 = base[(size_t)(c0 + s) * rs + 2 + d];
+            const float o1 = base[(size_t)(c0 + s + 4) * rs + 2 + d];
+            const float o2 = base[(size_t)(c0 + s + 8) * rs + 2 + d];
+            const float o3 = base[(size_t)(c0 + s + 12) * rs + 2 + d];
+            O += f[s] * o0 + f[s + 4] * o1 + f[s + 8] * o2 + f[s + 12] * o3;
+        }
+        for (; s < cn; s += 4) O += f[s] * base[(size_t)(c0 + s) * rs + 2 + d];
+        __syncthreads();
     }
+    osum[grp][dq] = O;
     __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    const float* src = sv.part + (size_t)grp * p.cg * G * REC;
-    if (sv.n_groups == 1) {
-        combine<D, G>(src, gsize, nullptr, true, kvh, p, sv);
-        return;
+    if (grp == 0) {
+        float y = (osum[0][dq] + osum[1][dq] + osum[2][dq] + osum[3][dq]) / L;
+        const float* q = p.q + (size_t)seq * Hkv * G * p.q_stride;
+        if (p.gate) y = y / (1.0f + expf(-q[(size_t)h * p.q_stride + D + d]));
+        p.out[((size_t)seq * Hkv * G + h) * D + d] = y;
     }
-    combine<D, G>(src, gsize, sv.part2 + (size_t)grp * G * REC, false, kvh, p, sv);
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(sv.cnt2, 1u);
-        flag = (old == (uint32_t)sv.n_groups - 1);
-        if (flag) atomicExch(sv.cnt2, 0u);
+}
+
+template <typename KV, int D, int G>
+int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
+    ANELM_LAUNCHED("attn_decode_kernel");
+    if (p.max_splits > 1) {
+        dim3 cgrid(D / 64, grid.y * G, grid.z);
+        hipLaunchKernelGGL((attn_combine_kernel<D, G>), cgrid, dim3(256), 0, st, p);
+        ANELM_LAUNCHED("attn_combine_kernel");
     }
-    __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    combine<D, G>(sv.part2, sv.n_groups, nullptr, true, kvh, p, sv);
+    return ANELM_OK;
 }
 
 template <typename KV, int D>
 int launch_d(DecodeParams& p, int G, dim3 grid, hipStream_t st) {
     switch (G) {
-        case 1: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1>), grid, dim3(kNT), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 2>), grid, dim3(kNT), 0, st, p); break;
-        case 4: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 4>), grid, dim3(kNT), 0, st, p); break;
-        case 8: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 8>), grid, dim3(kNT), 0, st, p); break;
+        case 1: return launch_g<KV, D, 1>(p, grid, st);
+        case 2: return launch_g<KV, D, 2>(p, grid, st);
+        case 4: return launch_g<KV, D, 4>(p, grid, st);
+        case 8: return launch_g<KV, D, 8>(p, grid, st);
         default: return set_error(ANELM_EINVAL, "n_heads/n_kv_heads = %d unsupported (1,2,4,8)", G);
     }
-    ANELM_LAUNCHED("attn_decode_kernel");
-    return ANELM_OK;
 }
 
 template <typename KV>
@@ -428,44 +430,27 @@ int launch_kv(DecodeParams& p, int D, int G, dim3 grid, hipStream_t st) {
     }
 }
 
-// Chooses the split layout and workspace for one decode call, then launches.
-// `max_len` bounds every sequence's key count; `n_seqs` sequences (1 in ring
-// mode).  Splits aim at about two workgroups per compute unit.
+// Sets the split layout and workspace for one decode call, then launches.
+// A split is 256/G keys: every lane of the workgroup then loads all of its
+// K and V rows at once.  `max_len` bounds every sequence's key count;
+// `n_seqs` sequences (1 in ring mode).
 int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, int max_len,
                hipStream_t st) {
     const int Hkv = p.n_kv_heads;
     const int G = n_heads / Hkv;
-    Device* dev = device();
-    if (!dev) return ANELM_EHIP;
-    const int target = 2 * dev->num_cus;
-    int per_seq = std::max(1, target / (Hkv * n_seqs));
-    if (n_seqs > 1) per_seq = std::max(1, 2 * per_seq);  // ragged: average length ~ max/2
-    int splits = std::min(per_seq, (max_len + 63) / 64);
-    int kps = (max_len + splits - 1) / splits;
-    kps = (kps + 15) & ~15;
-    kps = std::min(std::max(kps, 16), kMaxKps);
+    const int kps = 256 / G;
     const int max_splits = (max_len + kps - 1) / kps;
-    int cg = 1;
-    while (cg * cg < max_splits) cg++;
-    const int max_groups = (max_splits + cg - 1) / cg;
     p.kps = kps;
     p.max_splits = max_splits;
-    p.cg = cg;
-    p.max_groups = max_groups;
     p.n_seqs = n_seqs;
     const size_t rec = (size_t)G * (D + 2);
     if (max_splits > 1) {
-        const size_t pairs = (size_t)n_seqs * Hkv;
-        const size_t need = pairs * ((size_t)max_splits + max_groups) * rec * sizeof(float);
+        const size_t need = (size_t)n_seqs * Hkv * max_splits * rec * sizeof(float);
         float* ws = static_cast<float*>(workspace(need, st));
         if (!ws) return ANELM_ENOMEM;
         p.part = ws;
-        p.part2 = ws + pairs * max_splits * rec;
-        p.cnt = counters(pairs * max_groups + pairs);
-        if (!p.cnt) return ANELM_ERANGE;
     } else {
-        p.part = p.part2 = nullptr;
-        p.cnt = nullptr;
+        p.part = nullptr;
     }
     dim3 grid(max_splits, Hkv, n_seqs);
     return kv_dtype == ANELM_F16 ? launch_kv<uint16_t>(p, D, G, grid, st)

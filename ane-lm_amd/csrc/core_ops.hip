@@ -69,7 +69,9 @@ __global__ void rope_kernel(const RopeArgs a) {
     float* v = (h < a.nq) ? a.q + (size_t)h * a.qs : a.k + (size_t)(h - a.nq) * a.ks;
     const int i0 = a.mode == 0 ? 2 * j : j;
     const int i1 = a.mode == 0 ? 2 * j + 1 : j + a.pairs;
-    const float c = a.cs[j], s = a.sn[j];
+    const float* cs = a.cs;   // pointer into the argument segment (see attn_decode.hip)
+    const float* sn = a.sn;
+    const float c = cs[j], s = sn[j];
     const float v0 = v[i0], v1 = v[i1];
     rotate_pair(v[i0], v[i1], v0, v1, c, s);
 }

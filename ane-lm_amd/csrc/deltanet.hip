@@ -1,15 +1,15 @@
-// Gated DeltaNet decode step for all value heads (dk = dv = 128).
+// Gated DeltaNet: decode step for all value heads and sequence prefill
+// (dk = dv = 128).
 //
 // Reference: models/llm/qwen3_5.cpp:879-908 calling ssm_step
 // (core/cpu_ops.cpp:131-146).  The reference reads each 64 KiB head state five
-// times and writes it twice across four BLAS calls; here a workgroup owns a
-// 32-column slab of one head's state, holds it in registers, and reads and
-// writes it exactly once:
+// times and writes it twice across four BLAS calls; here a workgroup holds a
+// slab of state columns in registers and reads and writes it exactly once:
 //   Sk[j] = sum_i S[i][j] k[i];  delta[j] = v[j] - Sk[j]
 //   S'[i][j] = decay S[i][j] + beta k[i] delta[j];  y[j] = sum_i S'[i][j] q[i]
-// Column j depends only on column j, so the four slabs of a head are
-// independent; only the optional gated RMSNorm epilogue needs the whole head,
-// and the last slab to finish (per-head counter) applies it.
+// Column j depends only on column j, so slabs of a head are independent.  The
+// gated RMSNorm epilogue needs a whole head's y, so that variant gives one
+// workgroup the whole head instead of combining slabs across workgroups.
 #include "anelm_internal.hpp"
 
 #include <math.h>
@@ -19,11 +19,6 @@ namespace {
 
 constexpr int kDK = 128;
 constexpr int kDV = 128;
-constexpr int kCB = 32;               // columns per workgroup
-constexpr int kNT = 256;              // threads per workgroup
-constexpr int kRC = kNT / kCB;        // row chunks (8)
-constexpr int kRPT = kDK / kRC;       // rows per thread (16)
-constexpr int kSlabs = kDV / kCB;     // workgroups per head (4)
 
 struct DnParams {
     float* y;
@@ -37,24 +32,31 @@ struct DnParams {
     const float* dt_bias;
     const float* z;
     const float* norm_w;
-    float* ybuf;        // [Hv][dv] pre-norm outputs when the epilogue runs
-    uint32_t* cnt;      // [Hv]
     int Hk, Hv, flags;
 };
 
-__global__ __launch_bounds__(kNT) void deltanet_decode_kernel(const DnParams p) {
+// CB state columns per workgroup of NT threads: thread t owns column
+// t % CB for rows [(t / CB) * RPT, +RPT).
+template <int CB, int NT, bool GATED>
+__global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
+    constexpr int RC = NT / CB;       // row chunks
+    constexpr int RPT = kDK / RC;     // rows per thread
+    static_assert(!GATED || CB == kDV, "the gated epilogue needs the whole head");
     __shared__ float qs[kDK], ks[kDK];
-    __shared__ float red_a[kRC][kCB];
-    __shared__ float red[kNT / 64];
-    __shared__ float yrow[kDV];
-    __shared__ int flag;
+    __shared__ float red_a[RC][CB];
+    __shared__ float red[NT / 64];
 
     const int h = blockIdx.y;
-    const int slab = blockIdx.x;
     const int tid = threadIdx.x;
-    const int c = tid % kCB, rc = tid / kCB;
-    const int j = slab * kCB + c;
+    const int c = tid % CB, rc = tid / CB;
+    const int j = blockIdx.x * CB + c;
     const int kh = h / (p.Hv / p.Hk);
+
+    // The state slab is requested first; the prologue below overlaps it.
+    float* S = p.state + (size_t)h * kDK * kDV;
+    float s[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; r++) s[r] = S[(size_t)(rc * RPT + r) * kDV + j];
 
     // q, k of the key head: optional l2 normalisation (cpu_ops.cpp:82-87) and
     // the 1/sqrt(dk) query scale (qwen3_5.cpp:879-887).
@@ -64,8 +66,8 @@ __global__ __launch_bounds__(kNT) void deltanet_decode_kernel(const DnParams p) 
         kv = p.k[(size_t)kh * kDK + tid];
     }
     if (p.flags & ANELM_DN_L2NORM) {
-        const float sq = block_sum<kNT>(qv * qv, red);
-        const float sk = block_sum<kNT>(kv * kv, red);
+        const float sq = block_sum<NT>(qv * qv, red);
+        const float sk = block_sum<NT>(kv * kv, red);
         qv = qv * (1.0f / sqrtf(sq + 1e-12f));
         kv = kv * (1.0f / sqrtf(sk + 1e-12f));
     }
@@ -77,32 +79,27 @@ __global__ __launch_bounds__(kNT) void deltanet_decode_kernel(const DnParams p) 
     const float sp = logf(1.0f + expf(p.a[h] + p.dt_bias[h]));
     const float decay = expf(-p.A[h] * sp);
     const bool tf = (p.flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
+    const float vj = p.v[(size_t)h * kDV + j];
     __syncthreads();
-
-    float* S = p.state + (size_t)h * kDK * kDV;
-    float s[kRPT];
-#pragma unroll
-    for (int r = 0; r < kRPT; r++) s[r] = S[(size_t)(rc * kRPT + r) * kDV + j];
 
     float part = 0.f;
 #pragma unroll
-    for (int r = 0; r < kRPT; r++) {
+    for (int r = 0; r < RPT; r++) {
         if (tf) s[r] = decay * s[r];
-        part = fmaf(s[r], ks[rc * kRPT + r], part);
+        part = fmaf(s[r], ks[rc * RPT + r], part);
     }
     red_a[rc][c] = part;
     __syncthreads();
     float sk = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRC; i++) sk += red_a[i][c];
-    const float vj = p.v[(size_t)h * kDV + j];
+    for (int i = 0; i < RC; i++) sk += red_a[i][c];
     const float delta = tf ? (vj - sk) * beta : vj - sk;
     __syncthreads();
 
     float yp = 0.f;
 #pragma unroll
-    for (int r = 0; r < kRPT; r++) {
-        const int i = rc * kRPT + r;
+    for (int r = 0; r < RPT; r++) {
+        const int i = rc * RPT + r;
         const float n = tf ? fmaf(ks[i], delta, s[r]) : fmaf(beta * ks[i], delta, decay * s[r]);
         S[(size_t)i * kDV + j] = n;
         yp = fmaf(n, qs[i], yp);
@@ -111,36 +108,20 @@ __global__ __launch_bounds__(kNT) void deltanet_decode_kernel(const DnParams p) 
     __syncthreads();
     float yj = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRC; i++) yj += red_a[i][c];
+    for (int i = 0; i < RC; i++) yj += red_a[i][c];
 
-    if (!(p.flags & ANELM_DN_GATED_NORM)) {
+    if constexpr (!GATED) {
         if (rc == 0) p.y[(size_t)h * kDV + j] = yj;
-        return;
-    }
-    // Gated RMSNorm epilogue (cpu_ops.cpp:32-38) by the last slab of head h.
-    if (rc == 0) p.ybuf[(size_t)h * kDV + j] = yj;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(p.cnt + h, 1u);
-        flag = (old == kSlabs - 1);
-        if (flag) atomicExch(p.cnt + h, 0u);
-    }
-    __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    float yv = 0.f;
-    if (tid < kDV) {
-        yv = p.ybuf[(size_t)h * kDV + tid];
-        yrow[tid] = yv;
-    }
-    const float ss = block_sum<kNT>(yv * yv, red);
-    const float inv = 1.0f / sqrtf(ss / (float)kDV + 1e-6f);
-    if (tid < kDV) {
-        const float zi = p.z[(size_t)h * kDV + tid];
-        float o = (yrow[tid] * inv) * p.norm_w[tid];
-        o = o / (1.0f + expf(-zi));
-        p.y[(size_t)h * kDV + tid] = o * zi;
+    } else {
+        // rmsnorm_gated (cpu_ops.cpp:32-38): rmsnorm(y, w, 1e-6) * sigmoid(z) * z
+        const float ss = block_sum<NT>(rc == 0 ? yj * yj : 0.f, red);
+        const float inv = 1.0f / sqrtf(ss / (float)kDV + 1e-6f);
+        if (rc == 0) {
+            const float zi = p.z[(size_t)h * kDV + j];
+            float o = (yj * inv) * p.norm_w[j];
+            o = o / (1.0f + expf(-zi));
+            p.y[(size_t)h * kDV + j] = o * zi;
+        }
     }
 }
 
@@ -174,29 +155,34 @@ __global__ __launch_bounds__(kDK) void dn_prep_kernel(float* qn, float* kn, floa
     }
 }
 
+constexpr int kScanCB = 32;                 // columns per scan workgroup
+constexpr int kScanNT = 256;
+constexpr int kScanRC = kScanNT / kScanCB;  // 8 row chunks
+constexpr int kScanRPT = kDK / kScanRC;     // 16 rows per thread
+
 // Sequential scan over tokens: a workgroup owns a 32-column slab of one
 // head's state in registers for the whole sequence (one HBM read and write of
 // the state per call); per token it reads q, k, v and the gates and writes y.
-__global__ __launch_bounds__(kNT) void dn_scan_kernel(float* y, float* state, const float* qn,
-                                                      const float* kn, const float* v,
-                                                      const float* beta, const float* decay, int S,
-                                                      int Hk, int Hv, int flags) {
-    __shared__ float red_a[2][kRC][kCB];
+__global__ __launch_bounds__(kScanNT) void dn_scan_kernel(float* y, float* state, const float* qn,
+                                                          const float* kn, const float* v,
+                                                          const float* beta, const float* decay,
+                                                          int S, int Hk, int Hv, int flags) {
+    __shared__ float red_a[2][kScanRC][kScanCB];
     const int h = blockIdx.y, slab = blockIdx.x, tid = threadIdx.x;
-    const int c = tid % kCB, rc = tid / kCB;
-    const int j = slab * kCB + c;
+    const int c = tid % kScanCB, rc = tid / kScanCB;
+    const int j = slab * kScanCB + c;
     const int kh = h / (Hv / Hk);
     const bool tf = (flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
     float* Sp = state + (size_t)h * kDK * kDV;
-    float s[kRPT];
+    float s[kScanRPT];
 #pragma unroll
-    for (int r = 0; r < kRPT; r++) s[r] = Sp[(size_t)(rc * kRPT + r) * kDV + j];
+    for (int r = 0; r < kScanRPT; r++) s[r] = Sp[(size_t)(rc * kScanRPT + r) * kDV + j];
     for (int t = 0; t < S; t++) {
-        const float* kt = kn + ((size_t)t * Hk + kh) * kDK + rc * kRPT;
-        const float* qt = qn + ((size_t)t * Hk + kh) * kDK + rc * kRPT;
-        float kr[kRPT], qr[kRPT];
+        const float* kt = kn + ((size_t)t * Hk + kh) * kDK + rc * kScanRPT;
+        const float* qt = qn + ((size_t)t * Hk + kh) * kDK + rc * kScanRPT;
+        float kr[kScanRPT], qr[kScanRPT];
 #pragma unroll
-        for (int r = 0; r < kRPT; r += 4) {
+        for (int r = 0; r < kScanRPT; r += 4) {
             const float4 k4 = *reinterpret_cast<const float4*>(kt + r);
             const float4 q4 = *reinterpret_cast<const float4*>(qt + r);
             kr[r] = k4.x; kr[r + 1] = k4.y; kr[r + 2] = k4.z; kr[r + 3] = k4.w;
@@ -207,7 +193,7 @@ __global__ __launch_bounds__(kNT) void dn_scan_kernel(float* y, float* state, co
         const int buf = t & 1;
         float part = 0.f;
 #pragma unroll
-        for (int r = 0; r < kRPT; r++) {
+        for (int r = 0; r < kScanRPT; r++) {
             if (tf) s[r] = dc * s[r];
             part = fmaf(s[r], kr[r], part);
         }
@@ -215,11 +201,11 @@ __global__ __launch_bounds__(kNT) void dn_scan_kernel(float* y, float* state, co
         __syncthreads();
         float sk = 0.f;
 #pragma unroll
-        for (int i = 0; i < kRC; i++) sk += red_a[buf][i][c];
+        for (int i = 0; i < kScanRC; i++) sk += red_a[buf][i][c];
         const float delta = tf ? (vj - sk) * bt : vj - sk;
         float yp = 0.f;
 #pragma unroll
-        for (int r = 0; r < kRPT; r++) {
+        for (int r = 0; r < kScanRPT; r++) {
             s[r] = tf ? fmaf(kr[r], delta, s[r]) : fmaf(bt * kr[r], delta, dc * s[r]);
             yp = fmaf(s[r], qr[r], yp);
         }
@@ -229,12 +215,12 @@ __global__ __launch_bounds__(kNT) void dn_scan_kernel(float* y, float* state, co
         if (rc == 0) {
             float yj = 0.f;
 #pragma unroll
-            for (int i = 0; i < kRC; i++) yj += red_a[buf][i][c];
+            for (int i = 0; i < kScanRC; i++) yj += red_a[buf][i][c];
             y[((size_t)t * Hv + h) * kDV + j] = yj;
         }
     }
 #pragma unroll
-    for (int r = 0; r < kRPT; r++) Sp[(size_t)(rc * kRPT + r) * kDV + j] = s[r];
+    for (int r = 0; r < kScanRPT; r++) Sp[(size_t)(rc * kScanRPT + r) * kDV + j] = s[r];
 }
 
 }  // namespace
@@ -279,12 +265,11 @@ extern "C" int anelm_deltanet_decode(float* y, float* state, const float* q, con
         ANELM_NONNULL(norm_w);
         p.z = z;
         p.norm_w = norm_w;
-        p.ybuf = static_cast<float*>(workspace((size_t)Hv * kDV * sizeof(float), st));
-        if (!p.ybuf) return ANELM_ENOMEM;
-        p.cnt = counters((size_t)Hv);
-        if (!p.cnt) return ANELM_ERANGE;
+        hipLaunchKernelGGL((deltanet_decode_kernel<128, 512, true>), dim3(1, Hv), dim3(512), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((deltanet_decode_kernel<32, 256, false>), dim3(kDV / 32, Hv), dim3(256), 0,
+                           st, p);
     }
-    hipLaunchKernelGGL(deltanet_decode_kernel, dim3(kSlabs, Hv), dim3(kNT), 0, st, p);
     ANELM_LAUNCHED("deltanet_decode_kernel");
     return ANELM_OK;
 }
@@ -320,8 +305,8 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
     hipLaunchKernelGGL(dn_prep_kernel, dim3(S, Hk), dim3(kDK), 0, st, qn, kn, beta, decay, q, k, a, b,
                        A, dt_bias, Hk, Hv, flags);
     ANELM_LAUNCHED("dn_prep_kernel");
-    hipLaunchKernelGGL(dn_scan_kernel, dim3(kSlabs, Hv), dim3(kNT), 0, st, y, state, qn, kn, v, beta,
-                       decay, S, Hk, Hv, flags);
+    hipLaunchKernelGGL(dn_scan_kernel, dim3(kDV / kScanCB, Hv), dim3(kScanNT), 0, st, y, state, qn,
+                       kn, v, beta, decay, S, Hk, Hv, flags);
     ANELM_LAUNCHED("dn_scan_kernel");
     return ANELM_OK;
 }

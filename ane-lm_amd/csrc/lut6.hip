@@ -1,19 +1,21 @@
-// LUT6-palettised weight kernels: unpack, GEMV, fused RMSNorm + SwiGLU
-// gate/up, down projection with residual, and the top-k LM head.
+// LUT6-palettised weight kernels: unpack, GEMV, the FFN block (RMSNorm +
+// gate/up + SwiGLU + down + residual), and the top-k LM head.
 //
 // Format: W[r][c] = lut[r/32][idx(r,c)] with a 64-entry fp16 LUT per 32-row
 // group; index c of row r sits at bits [6c, 6c+6) of the row's little-endian
 // byte stream (4 indices per 3 bytes, row stride in_dim*3/4 bytes).
 //
-// GEMV mapping: a wave owns a few rows of one 32-row group.  The row is split
-// in 12-byte chunks (16 indices, dword aligned); lane l takes chunks
-// l, l+64, l+128, ... so every load instruction of a wave reads 768
-// contiguous bytes.  The group's 64 LUT entries live one per lane (as fp32)
-// and each 6-bit index is resolved with ds_bpermute (a cross-lane read that
-// needs no LDS storage and has no bank conflicts).  x is held in registers
-// for the lane's chunks, so each weight costs one extract, one permute and
-// one FMA.  Reference math: matvec (core/cpu_ops.cpp:77-80) on the dequantised
-// weights; SwiGLU as models/llm/qwen3_5.cpp:1118-1130.
+// GEMV mapping.  A workgroup (4 waves) owns 4*RPW rows of ONE 32-row group.
+// A row is split into 12-byte chunks (16 indices, dword aligned); lane l takes
+// chunks l, l+64, l+128, ... so every load instruction of a wave reads 768
+// contiguous bytes.  The weight loads are issued first, so their latency is
+// covered by the rest of the prologue: staging x into LDS (with the fused
+// RMSNorm or SwiGLU) and building the group's pair table -- 4096 float2
+// entries T[(i1 << 6) | i0] = (lut[i0], lut[i1]).  Two adjacent 6-bit indices
+// are one contiguous 12-bit field of the row stream, so one extract and one
+// 8-byte LDS read dequantise two weights.  Reference math: matvec
+// (core/cpu_ops.cpp:77-80) on the dequantised weights; SwiGLU as
+// models/llm/qwen3_5.cpp:1118-1130.
 #include "anelm_internal.hpp"
 
 #include <math.h>
@@ -23,125 +25,161 @@ namespace {
 
 constexpr int kNT = 256;
 constexpr int kNW = kNT / 64;
+constexpr int kPairs = 4096;
 
-__device__ __forceinline__ uint32_t idx6(const uint32_t (&w)[3], int k) {
-    const int bit = 6 * k, d = bit >> 5, sh = bit & 31;
-    if (sh <= 26) return (w[d] >> sh) & 63u;
-    const uint64_t two = ((uint64_t)w[d + 1] << 32) | w[d];
-    return (uint32_t)(two >> sh) & 63u;
-}
-
-__device__ __forceinline__ float lut_lookup(uint32_t idx, int lut_bits) {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute((int)(idx << 2), lut_bits));
-}
-
-// Dot product of one 16-index chunk with 16 x values.
-__device__ __forceinline__ float chunk_dot(const uint3& wv, const float* xr, int lut_bits, float acc) {
-    const uint32_t w[3] = {wv.x, wv.y, wv.z};
-#pragma unroll
-    for (int k = 0; k < 16; k++) acc = fmaf(lut_lookup(idx6(w, k), lut_bits), xr[k], acc);
-    return acc;
-}
-
-// Loads the lane's x chunks (chunks lane + 64*j) from shared memory.
-template <int NJ>
-__device__ __forceinline__ void load_x(float (&xr)[NJ][16], const float* xs, int nch, int lane) {
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int c = lane + 64 * j;
-#pragma unroll
-        for (int i = 0; i < 16; i++) xr[j][i] = (c < nch) ? xs[c * 16 + i] : 0.f;
+// Bit-field [bit, bit+n) of the 96-bit chunk (w0 | w1<<32 | w2<<64).
+template <int BIT, int N>
+__device__ __forceinline__ uint32_t field(uint32_t w0, uint32_t w1, uint32_t w2) {
+    constexpr int d = BIT >> 5, sh = BIT & 31;
+    const uint32_t lo = d == 0 ? w0 : (d == 1 ? w1 : w2);
+    if constexpr (sh + N <= 32) {
+        return (lo >> sh) & ((1u << N) - 1u);
+    } else {
+        const uint32_t hi = d == 0 ? w1 : w2;
+        return __builtin_amdgcn_alignbit(hi, lo, sh) & ((1u << N) - 1u);
     }
 }
 
-// Stages x (optionally RMS-normalised with weight nw) into shared memory.
-__device__ void stage_x(float* xs, const float* x, const float* nw, float eps, int n, float* red) {
+// Builds the pair table of LUT group `lut64` in shared memory: entry
+// (i1 << 6) | i0 holds lut[i0] in its low half and lut[i1] in its high half.
+__device__ __forceinline__ void build_pairs(uint32_t* tab, const uint16_t* lut64) {
+    for (int e = threadIdx.x; e < kPairs; e += kNT)
+        tab[e] = (uint32_t)lut64[e & 63] | ((uint32_t)lut64[e >> 6] << 16);
+}
+
+__device__ __forceinline__ float lo_half(uint32_t p) {
+    return __half2float(__ushort_as_half((unsigned short)(p & 0xffffu)));
+}
+__device__ __forceinline__ float hi_half(uint32_t p) {
+    return __half2float(__ushort_as_half((unsigned short)(p >> 16)));
+}
+
+// Dot product of one 16-index chunk with its 16 x values (fp16 weights
+// widened exactly; fp32 products and sums).
+__device__ __forceinline__ void chunk_dot(const uint32_t* tab, uint32_t w0, uint32_t w1, uint32_t w2,
+                                          const float (&xr)[16], float& a0, float& a1) {
+    uint32_t p[8];
+    p[0] = tab[field<0, 12>(w0, w1, w2)];
+    p[1] = tab[field<12, 12>(w0, w1, w2)];
+    p[2] = tab[field<24, 12>(w0, w1, w2)];
+    p[3] = tab[field<36, 12>(w0, w1, w2)];
+    p[4] = tab[field<48, 12>(w0, w1, w2)];
+    p[5] = tab[field<60, 12>(w0, w1, w2)];
+    p[6] = tab[field<72, 12>(w0, w1, w2)];
+    p[7] = tab[field<84, 12>(w0, w1, w2)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        a0 = fmaf(lo_half(p[k]), xr[2 * k], a0);
+        a1 = fmaf(hi_half(p[k]), xr[2 * k + 1], a1);
+    }
+}
+
+// x staging modes
+enum : int { kStageCopy = 0, kStageNorm = 1, kStageSwiglu = 2 };
+
+// Stages the GEMV input vector into shared memory:
+//   copy:   xs = x
+//   norm:   xs = rmsnorm(x, nw, eps)           (cpu_ops.cpp:24-30)
+//   swiglu: xs = silu(x) * x2                  (qwen3_5.cpp:1123-1126)
+template <int MODE>
+__device__ void stage_x(float* xs, const float* x, const float* x2, const float* nw, float eps, int n,
+                        float* red) {
+    if (MODE == kStageSwiglu) {
+        for (int i = threadIdx.x; i < n; i += kNT) {
+            const float g = x[i];
+            xs[i] = (g / (1.0f + expf(-g))) * x2[i];
+        }
+        return;
+    }
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kNT) {
         const float v = x[i];
         xs[i] = v;
         ss += v * v;
     }
-    if (nw) {
+    if (MODE == kStageNorm && nw != nullptr) {
         ss = block_sum<kNT>(ss, red);
         const float inv = 1.0f / sqrtf(ss / (float)n + eps);
         for (int i = threadIdx.x; i < n; i += kNT) xs[i] = (xs[i] * inv) * nw[i];
     }
-    __syncthreads();
 }
 
-// Row dot products for RPW consecutive rows starting at r0 (all in one group).
-template <int NJ, int RPW>
-__device__ __forceinline__ void rows_dot(float (&acc)[RPW], const uint8_t* W, const uint16_t* lut,
-                                         int r0, size_t row_bytes, int nch, int lane,
-                                         const float (&xr)[NJ][16]) {
-    const int lut_bits = __float_as_int(h2f(lut[(size_t)(r0 >> 5) * 64 + lane]));
-    uint3 wv[RPW][NJ];
+struct GemvArgs {
+    // up to two matrices sharing the input: blocks [0, blocks0) use matrix 0
+    const uint8_t* w[2];
+    const uint16_t* lut[2];
+    float* y[2];
+    int blocks0;
+    int out_dim, in_dim;
+    const float* x;
+    const float* x2;       // swiglu second operand
+    const float* nw;       // rmsnorm weight
+    float eps;
+    int residual;          // y[r] += result instead of y[r] = result
+};
+
+// Rows [r0, r0 + 4*RPW) of one matrix; one 32-row LUT group per workgroup.
+template <int NJ, int RPW, int STAGE>
+__global__ __launch_bounds__(kNT) void lut6_gemv_kernel(const GemvArgs a) {
+    static_assert(kNW * RPW <= 32, "a workgroup must stay inside one LUT group");
+    extern __shared__ float smem[];
+    uint32_t* tab = reinterpret_cast<uint32_t*>(smem);
+    float* xs = smem + kPairs;
+    __shared__ float red[kNW];
+
+    const int m = blockIdx.x < a.blocks0 ? 0 : 1;
+    const int blk = m == 0 ? blockIdx.x : blockIdx.x - a.blocks0;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int rb0 = blk * kNW * RPW;             // first row of the workgroup
+    const int r0 = rb0 + w * RPW;                // first row of this wave
+    const int nch = a.in_dim / 16;
+    const size_t row_bytes = (size_t)a.in_dim * 3 / 4;
+    const uint8_t* W = a.w[m];
+
+    // 1. weight loads first
+    uint32_t wv[RPW][NJ][3];
 #pragma unroll
     for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
             const int c = lane + 64 * j;
-            wv[r][j] = (c < nch) ? *reinterpret_cast<const uint3*>(W + (size_t)(r0 + r) * row_bytes + (size_t)c * 12)
-                                 : make_uint3(0u, 0u, 0u);
+            uint3 t = make_uint3(0u, 0u, 0u);
+            if (c < nch) t = *reinterpret_cast<const uint3*>(W + (size_t)(r0 + r) * row_bytes + (size_t)c * 12);
+            wv[r][j][0] = t.x;
+            wv[r][j][1] = t.y;
+            wv[r][j][2] = t.z;
         }
+    // 2. pair table and staged x while the weights are in flight
+    build_pairs(tab, a.lut[m] + (size_t)(rb0 >> 5) * 64);
+    stage_x<STAGE>(xs, a.x, a.x2, a.nw, a.eps, a.in_dim, red);
+    __syncthreads();
+    float xr[NJ][16];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c = lane + 64 * j;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c < nch) v = reinterpret_cast<const float4*>(xs + c * 16)[q];
+            xr[j][4 * q] = v.x;
+            xr[j][4 * q + 1] = v.y;
+            xr[j][4 * q + 2] = v.z;
+            xr[j][4 * q + 3] = v.w;
+        }
+    }
+    // 3. dot products
+    float res = 0.f;
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-        float a = 0.f;
+        float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int j = 0; j < NJ; j++) a = chunk_dot(wv[r][j], xr[j], lut_bits, a);
-        acc[r] = wave_sum(a);
+        for (int j = 0; j < NJ; j++) chunk_dot(tab, wv[r][j][0], wv[r][j][1], wv[r][j][2], xr[j], a0, a1);
+        const float s = wave_sum(a0 + a1);
+        if (lane == r) res = s;
     }
-}
-
-// y[r] = (residual ? y[r] : 0) + W x.  Rows per workgroup = 4 * RPW.
-template <int NJ, int RPW>
-__global__ __launch_bounds__(kNT) void lut6_gemv_kernel(float* y, const uint8_t* W, const uint16_t* lut,
-                                                        const float* x, int out_dim, int in_dim,
-                                                        int residual) {
-    extern __shared__ float xs[];
-    __shared__ float red[kNW];
-    stage_x(xs, x, nullptr, 0.f, in_dim, red);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * kNW + w) * RPW;
-    if (r0 >= out_dim) return;
-    const int nch = in_dim / 16;
-    float xr[NJ][16];
-    load_x<NJ>(xr, xs, nch, lane);
-    float acc[RPW];
-    rows_dot<NJ, RPW>(acc, W, lut, r0, (size_t)in_dim * 3 / 4, nch, lane, xr);
     if (lane < RPW) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < RPW; r++) if (lane == r) v = acc[r];
-        y[r0 + lane] = residual ? y[r0 + lane] + v : v;
-    }
-}
-
-// h[r] = silu(gate_r . n) * (up_r . n), n = rmsnorm(x, nw) (or x when nw is NULL).
-template <int NJ, int RPW>
-__global__ __launch_bounds__(kNT) void lut6_gateup_kernel(float* h, const uint8_t* Wg, const uint16_t* lg,
-                                                          const uint8_t* Wu, const uint16_t* lu,
-                                                          const float* x, const float* nw, float eps,
-                                                          int inter, int hidden) {
-    extern __shared__ float xs[];
-    __shared__ float red[kNW];
-    stage_x(xs, x, nw, eps, hidden, red);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * kNW + w) * RPW;
-    if (r0 >= inter) return;
-    const int nch = hidden / 16;
-    const size_t rb = (size_t)hidden * 3 / 4;
-    float xr[NJ][16];
-    load_x<NJ>(xr, xs, nch, lane);
-    float ag[RPW], au[RPW];
-    rows_dot<NJ, RPW>(ag, Wg, lg, r0, rb, nch, lane, xr);
-    rows_dot<NJ, RPW>(au, Wu, lu, r0, rb, nch, lane, xr);
-    if (lane < RPW) {
-        float g = ag[0], u = au[0];
-#pragma unroll
-        for (int r = 1; r < RPW; r++) if (lane == r) { g = ag[r]; u = au[r]; }
-        h[r0 + lane] = (g / (1.0f + expf(-g))) * u;
+        float* y = a.y[m] + r0 + lane;
+        *y = a.residual ? *y + res : res;
     }
 }
 
@@ -156,6 +194,15 @@ __global__ void lut6_unpack_kernel(uint8_t* idx, const uint8_t* packed, int64_t 
     o.z = (uint8_t)((w >> 12) & 63u);
     o.w = (uint8_t)((w >> 18) & 63u);
     *reinterpret_cast<uchar4*>(idx + 4 * g) = o;
+}
+
+// h = silu(g) * u (qwen3_5.cpp:1123-1126)
+__global__ void swiglu_kernel(float* h, const float* g, const float* u, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float gv = g[i];
+        h[i] = (gv / (1.0f + expf(-gv))) * u[i];
+    }
 }
 
 // ---------------------------------------------------------------- top-k
@@ -227,56 +274,33 @@ __global__ __launch_bounds__(kNT) void topk_stage2(const float* cv, const int* c
     }
 }
 
-constexpr int kMaxNJ = 16;   // in_dim up to 16384
+constexpr int kMaxNJ = 11;   // in_dim up to 11264: pair table 16 KiB + x 44 KiB of LDS
 
+// Rows per wave: 4 while the lane's x chunks are few; 2 for wide inputs so the
+// register footprint (x + weights in flight) keeps two waves per SIMD.
 template <int NJ>
-int gemv_nj(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int out_dim,
-            int in_dim, int residual, hipStream_t st) {
-    constexpr int RPW = (NJ <= 4) ? 4 : 2;
+constexpr int rows_per_wave() { return NJ <= 4 ? 4 : 2; }
+
+template <int NJ, int STAGE>
+int gemv_launch(GemvArgs a, int n_mats, hipStream_t st) {
+    constexpr int RPW = rows_per_wave<NJ>();
     const int rows_per_block = kNW * RPW;
-    const int blocks = (out_dim + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((lut6_gemv_kernel<NJ, RPW>), dim3(blocks), dim3(kNT),
-                       (size_t)in_dim * sizeof(float), st, y, w, lut, x, out_dim, in_dim, residual);
+    const int blocks = a.out_dim / rows_per_block;
+    a.blocks0 = blocks;
+    const size_t lds = (size_t)kPairs * sizeof(uint32_t) + (size_t)a.in_dim * sizeof(float);
+    hipLaunchKernelGGL((lut6_gemv_kernel<NJ, RPW, STAGE>), dim3(blocks * n_mats), dim3(kNT), lds, st, a);
     ANELM_LAUNCHED("lut6_gemv_kernel");
     return ANELM_OK;
 }
 
-template <int NJ>
-int gateup_nj(float* h, const uint8_t* wg, const uint16_t* lg, const uint8_t* wu,
-              const uint16_t* lu, const float* x, const float* nw, float eps, int inter,
-              int hidden, hipStream_t st) {
-    constexpr int RPW = (NJ <= 4) ? 4 : 2;
-    const int rows_per_block = kNW * RPW;
-    const int blocks = (inter + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((lut6_gateup_kernel<NJ, RPW>), dim3(blocks), dim3(kNT),
-                       (size_t)hidden * sizeof(float), st, h, wg, lg, wu, lu, x, nw, eps, inter,
-                       hidden);
-    ANELM_LAUNCHED("lut6_gateup_kernel");
-    return ANELM_OK;
-}
-
-int gemv_dispatch(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int out_dim,
-                  int in_dim, int residual, hipStream_t st) {
-    const int nj = (in_dim / 16 + 63) / 64;
+template <int STAGE>
+int gemv_dispatch(GemvArgs a, int n_mats, hipStream_t st) {
+    const int nj = (a.in_dim / 16 + 63) / 64;
     switch (nj) {
-#define CASE(N) case N: return gemv_nj<N>(y, w, lut, x, out_dim, in_dim, residual, st);
-        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
-        CASE(9) CASE(10) CASE(11) CASE(12) CASE(13) CASE(14) CASE(15) CASE(16)
+#define CASE(N) case N: return gemv_launch<N, STAGE>(a, n_mats, st);
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(10) CASE(11)
 #undef CASE
-        default: return set_error(ANELM_ERANGE, "lut6: in_dim %d beyond %d", in_dim, kMaxNJ * 1024);
-    }
-}
-
-int gateup_dispatch(float* h, const uint8_t* wg, const uint16_t* lg, const uint8_t* wu,
-                    const uint16_t* lu, const float* x, const float* nw, float eps, int inter,
-                    int hidden, hipStream_t st) {
-    const int nj = (hidden / 16 + 63) / 64;
-    switch (nj) {
-#define CASE(N) case N: return gateup_nj<N>(h, wg, lg, wu, lu, x, nw, eps, inter, hidden, st);
-        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
-        CASE(9) CASE(10) CASE(11) CASE(12) CASE(13) CASE(14) CASE(15) CASE(16)
-#undef CASE
-        default: return set_error(ANELM_ERANGE, "lut6: hidden %d beyond %d", hidden, kMaxNJ * 1024);
+        default: return set_error(ANELM_ERANGE, "lut6: in_dim %d beyond %d", a.in_dim, kMaxNJ * 1024);
     }
 }
 
@@ -285,6 +309,25 @@ int check_shape(int out_dim, int in_dim) {
     ANELM_REQUIRE(in_dim > 0 && in_dim % 16 == 0, "lut6: in_dim %d must be a positive multiple of 16", in_dim);
     ANELM_REQUIRE(in_dim <= kMaxNJ * 1024, "lut6: in_dim %d beyond %d", in_dim, kMaxNJ * 1024);
     return ANELM_OK;
+}
+
+// g = gate n, u = up n with n = rmsnorm(x) (or x).
+int gate_up(float* g, float* u, const float* x, const float* norm_w, float eps, const uint8_t* gw,
+            const uint16_t* gl, const uint8_t* uw, const uint16_t* ul, int hidden, int inter,
+            hipStream_t st) {
+    GemvArgs a{};
+    a.w[0] = gw;
+    a.lut[0] = gl;
+    a.y[0] = g;
+    a.w[1] = uw;
+    a.lut[1] = ul;
+    a.y[1] = u;
+    a.out_dim = inter;
+    a.in_dim = hidden;
+    a.x = x;
+    a.nw = norm_w;
+    a.eps = eps;
+    return norm_w ? gemv_dispatch<kStageNorm>(a, 2, st) : gemv_dispatch<kStageCopy>(a, 2, st);
 }
 
 }  // namespace
@@ -314,29 +357,30 @@ int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float
     ANELM_NONNULL(x);
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
-    return gemv_dispatch(y, w, lut, x, out_dim, in_dim, 0, as_stream(stream));
+    GemvArgs a{};
+    a.w[0] = w;
+    a.lut[0] = lut;
+    a.y[0] = y;
+    a.out_dim = out_dim;
+    a.in_dim = in_dim;
+    a.x = x;
+    return gemv_dispatch<kStageCopy>(a, 1, as_stream(stream));
 }
 
-int anelm_lut6_ffn(float* x, float* h_scratch, const float* norm_w, float eps,
-                   const uint8_t* gate_w, const uint16_t* gate_lut, const uint8_t* up_w,
-                   const uint16_t* up_lut, const uint8_t* down_w, const uint16_t* down_lut,
-                   int hidden, int inter, void* stream) {
+int anelm_lut6_gate_up(float* g, float* u, const float* x, const float* norm_w, float eps,
+                       const uint8_t* gate_w, const uint16_t* gate_lut, const uint8_t* up_w,
+                       const uint16_t* up_lut, int hidden, int inter, void* stream) {
+    ANELM_NONNULL(g);
+    ANELM_NONNULL(u);
     ANELM_NONNULL(x);
-    ANELM_NONNULL(h_scratch);
     ANELM_NONNULL(gate_w);
     ANELM_NONNULL(gate_lut);
     ANELM_NONNULL(up_w);
     ANELM_NONNULL(up_lut);
-    ANELM_NONNULL(down_w);
-    ANELM_NONNULL(down_lut);
     int rc = check_shape(inter, hidden);
     if (rc) return rc;
-    rc = check_shape(hidden, inter);
-    if (rc) return rc;
-    hipStream_t st = as_stream(stream);
-    rc = gateup_dispatch(h_scratch, gate_w, gate_lut, up_w, up_lut, x, norm_w, eps, inter, hidden, st);
-    if (rc) return rc;
-    return gemv_dispatch(x, down_w, down_lut, h_scratch, hidden, inter, 1, st);
+    return gate_up(g, u, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter,
+                   as_stream(stream));
 }
 
 int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
@@ -350,8 +394,47 @@ int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
     ANELM_NONNULL(up_lut);
     int rc = check_shape(inter, hidden);
     if (rc) return rc;
-    return gateup_dispatch(h, gate_w, gate_lut, up_w, up_lut, x, norm_w, eps, inter, hidden,
-                           as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    float* gu = static_cast<float*>(workspace((size_t)2 * inter * sizeof(float), st));
+    if (!gu) return ANELM_ENOMEM;
+    rc = gate_up(gu, gu + inter, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((inter + 255) / 256), dim3(256), 0, st, h, gu, gu + inter, inter);
+    ANELM_LAUNCHED("swiglu_kernel");
+    return ANELM_OK;
+}
+
+int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
+                   const uint8_t* gate_w, const uint16_t* gate_lut, const uint8_t* up_w,
+                   const uint16_t* up_lut, const uint8_t* down_w, const uint16_t* down_lut,
+                   int hidden, int inter, void* stream) {
+    ANELM_NONNULL(x);
+    ANELM_NONNULL(gu_scratch);
+    ANELM_NONNULL(gate_w);
+    ANELM_NONNULL(gate_lut);
+    ANELM_NONNULL(up_w);
+    ANELM_NONNULL(up_lut);
+    ANELM_NONNULL(down_w);
+    ANELM_NONNULL(down_lut);
+    int rc = check_shape(inter, hidden);
+    if (rc) return rc;
+    rc = check_shape(hidden, inter);
+    if (rc) return rc;
+    hipStream_t st = as_stream(stream);
+    float* g = gu_scratch;
+    float* u = gu_scratch + inter;
+    rc = gate_up(g, u, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter, st);
+    if (rc) return rc;
+    GemvArgs a{};
+    a.w[0] = down_w;
+    a.lut[0] = down_lut;
+    a.y[0] = x;
+    a.out_dim = hidden;
+    a.in_dim = inter;
+    a.x = g;
+    a.x2 = u;
+    a.residual = 1;
+    return gemv_dispatch<kStageSwiglu>(a, 1, st);
 }
 
 int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
@@ -379,8 +462,14 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     float* cv = reinterpret_cast<float*>(ws + logits_bytes);
     int* ci = reinterpret_cast<int*>(ws + logits_bytes + (size_t)batch * n_cand * sizeof(float));
     for (int b = 0; b < batch; b++) {
-        rc = gemv_dispatch(logits + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim,
-                           in_dim, 0, st);
+        GemvArgs a{};
+        a.w[0] = w;
+        a.lut[0] = lut;
+        a.y[0] = logits + (size_t)b * out_dim;
+        a.out_dim = out_dim;
+        a.in_dim = in_dim;
+        a.x = x + (size_t)b * in_dim;
+        rc = gemv_dispatch<kStageCopy>(a, 1, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(kNT), 0, st, logits, out_dim, k,

@@ -209,11 +209,23 @@ def lut6_gemv(w, lut, x, out_dim, in_dim, out=None):
     return out
 
 
-def lut6_ffn_(x, h_scratch, norm_w, eps, gate, up, down, hidden, inter):
-    """x += down(silu(gate n) * (up n)), n = rmsnorm(x, norm_w); gate/up/down = (w, lut)."""
-    call("anelm_lut6_ffn", _p(x), _p(h_scratch), _p(norm_w), eps, _p(gate[0]), _p(gate[1]),
+def lut6_ffn_(x, gu_scratch, norm_w, eps, gate, up, down, hidden, inter):
+    """x += down(silu(gate n) * (up n)), n = rmsnorm(x, norm_w); gate/up/down = (w, lut);
+    gu_scratch holds 2*inter floats."""
+    if gu_scratch.numel() < 2 * inter:
+        raise ValueError("gu_scratch needs 2*inter floats")
+    call("anelm_lut6_ffn", _p(x), _p(gu_scratch), _p(norm_w), eps, _p(gate[0]), _p(gate[1]),
          _p(up[0]), _p(up[1]), _p(down[0]), _p(down[1]), hidden, inter, _s())
     return x
+
+
+def lut6_gate_up(x, norm_w, eps, gate, up, hidden, inter):
+    """(gate n, up n), n = rmsnorm(x, norm_w) (x when norm_w is None)."""
+    g = torch.empty(inter, device=x.device, dtype=_F32)
+    u = torch.empty(inter, device=x.device, dtype=_F32)
+    call("anelm_lut6_gate_up", _p(g), _p(u), _p(x), _p(norm_w), eps, _p(gate[0]), _p(gate[1]),
+         _p(up[0]), _p(up[1]), hidden, inter, _s())
+    return g, u
 
 
 def lut6_topk(w, lut, x, out_dim, in_dim, k):

@@ -55,9 +55,9 @@ def step_bytes(c=CFG):
 
 def gateup_bytes(c=CFG):
     """Algorithmic bytes of one gate/up launch: two LUT6 matrices [inter][hidden],
-    their LUTs, x and the norm weight read once, h written once."""
+    their LUTs, x and the norm weight read once, g and u written once."""
     H, I = c["hidden"], c["inter"]
-    return 2 * (I * H * 3 // 4 + (I // 32) * 64 * 2) + 2 * H * 4 + I * 4
+    return 2 * (I * H * 3 // 4 + (I // 32) * 64 * 2) + 2 * H * 4 + 2 * I * 4
 
 
 def build_step(anelm, torch, dev, seed=0, use_graph=True):
@@ -119,7 +119,7 @@ def build_step(anelm, torch, dev, seed=0, use_graph=True):
             setattr(L, name, ten.data_ptr())
         keep.append(t)
     x = randn(H)
-    h = torch.empty(I, device=dev)
+    h = torch.empty(2 * I, device=dev)
     keep.append({"x": x, "h": h})
     dims = anelm.HybridDims(H, I, Hq, Hkv, D, c["rot_dim"], 0, c["theta"], c["eps"], Hk, Hv, dl)
     torch.cuda.synchronize()
@@ -137,26 +137,28 @@ def time_gateup(anelm, torch, keep, n=50):
     timed with HIP events on the stream it is launched on."""
     c = CFG
     xv = torch.randn(c["hidden"], device="cuda")
-    hv = torch.empty(c["inter"], device="cuda")
+    gv = torch.empty(c["inter"], device="cuda")
+    uv = torch.empty(c["inter"], device="cuda")
     stream = torch.cuda.current_stream()
     s = ctypes.c_void_p(stream.cuda_stream)
     # rotate over all 32 layers' weights so every launch streams from HBM
     mats = [k for k in keep if isinstance(k, dict) and "gate_w" in k]
     arglist = []
     for m in mats:
-        arglist.append((ctypes.c_void_p(hv.data_ptr()), ctypes.c_void_p(xv.data_ptr()),
+        arglist.append((ctypes.c_void_p(gv.data_ptr()), ctypes.c_void_p(uv.data_ptr()),
+                        ctypes.c_void_p(xv.data_ptr()),
                         ctypes.c_void_p(m["ffn_norm_w"].data_ptr()), ctypes.c_float(c["eps"]),
                         ctypes.c_void_p(m["gate_w"].data_ptr()), ctypes.c_void_p(m["gate_lut"].data_ptr()),
                         ctypes.c_void_p(m["up_w"].data_ptr()), ctypes.c_void_p(m["up_lut"].data_ptr()),
                         c["hidden"], c["inter"], s))
     for a in arglist[:4]:
-        anelm.call("anelm_lut6_swiglu", *a)
+        anelm.call("anelm_lut6_gate_up", *a)
     durs = []
     for i in range(n):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        anelm.call("anelm_lut6_swiglu", *arglist[i % len(arglist)])
+        anelm.call("anelm_lut6_gate_up", *arglist[i % len(arglist)])
         e1.record(stream)
         durs.append((e0, e1))
     torch.cuda.synchronize()
@@ -297,7 +299,8 @@ def main():
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": b["total"],
         "wall_s": round(wall, 4),
-        "roofline": {"bound": "hbm", "kernel": "lut6_gateup_kernel", "achieved": round(gu_gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "lut6_gemv_kernel (gate+up, 2 x 9216x2560)",
+                     "achieved": round(gu_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": None, "bytes_per_launch": gu_b, "avg_us": round(gu_avg, 3),
                      "median_us": round(gu_med, 3)},

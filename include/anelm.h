@@ -191,14 +191,22 @@ int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float
 /* SwiGLU FFN block with residual (qwen3_5.cpp:1335-1354 with the MLP of
  * :1118-1130): n = rmsnorm(x, norm_w, eps) (skipped when norm_w is NULL);
  * x += down( silu(gate n) * (up n) ).  x [hidden] is updated in place;
- * h_scratch [inter] receives the SwiGLU activations. */
-int anelm_lut6_ffn(float* x, float* h_scratch, const float* norm_w, float eps,
+ * gu_scratch [2*inter] receives gate n and up n. */
+int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
                    const uint8_t* gate_w, const uint16_t* gate_lut,
                    const uint8_t* up_w, const uint16_t* up_lut,
                    const uint8_t* down_w, const uint16_t* down_lut,
                    int hidden, int inter, void* stream);
 
-/* The gate/up half of the FFN block alone (qwen3_5.cpp:1118-1124):
+/* The two projections of the FFN block (qwen3_5.cpp:1118-1122):
+ * g = gate n, u = up n, n = rmsnorm(x, norm_w, eps) (x when norm_w is NULL).
+ * One launch over both matrices.  g, u [inter]. */
+int anelm_lut6_gate_up(float* g, float* u, const float* x, const float* norm_w, float eps,
+                       const uint8_t* gate_w, const uint16_t* gate_lut,
+                       const uint8_t* up_w, const uint16_t* up_lut,
+                       int hidden, int inter, void* stream);
+
+/* The gate/up half of the FFN block alone (qwen3_5.cpp:1118-1126):
  * h = silu(gate n) * (up n), n = rmsnorm(x, norm_w, eps) (x when norm_w is
  * NULL).  x [hidden], h [inter]. */
 int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
@@ -268,7 +276,7 @@ typedef struct {
 typedef struct anelm_hybrid_step anelm_hybrid_step;
 
 /* Builds a step over n_layers descriptors (copied), x [hidden] and
- * h_scratch [inter] device buffers.  With use_graph, the step's launches are
+ * h_scratch [2*inter] device buffers.  With use_graph, the step's launches are
  * captured once into a HIP graph on `stream` (which must not be the null
  * stream) after one eager warm-up run; each run then replays the same work
  * -- the attention rings do not advance between replays.  Without it, each
