@@ -183,6 +183,290 @@ __global__ __launch_bounds__(kNT) void lut6_gemv_kernel(const GemvArgs a) {
     }
 }
 
+// ------------------------------------------------------- tile GEMV (fast path)
+//
+// Geometry.  A row holds C = in_dim/16 chunks of 12 bytes; a tile of T rows
+// is T*C contiguous chunks.  One wave instruction reads 64 consecutive
+// chunks (768 bytes).  With P = C / gcd(C, 64) waves per matrix, wave w of a
+// matrix issues instructions w, w+P, w+2P, ... of the tile, so lane l always
+// sees the same chunk position pos = (64w + l) % C, on row RP*m + d of
+// instruction m, where RP = 64P/C and d = (64w + l) / C.  Every lane
+// therefore needs the 16 x values of ONE chunk for the whole tile: they sit
+// in registers, split into an fp16 high part and a 2^11-scaled fp16 low
+// part, and each pair of weights is dotted with both halves by
+// v_dot2_f32_f16 (fp16 products are exact in fp32, so the result carries
+// about 22 bits of x).  A 12-bit index pair selects one dword of the LDS pair
+// table T[(i1 << 6) | i0] = lut[i0] | lut[i1] << 16, built from the group's
+// LUT held one entry per lane.  Partial sums are reduced through LDS in a
+// fixed order, so results are deterministic.
+//
+// A workgroup has NMAT * P waves: NMAT = 2 runs gate and up over the same
+// rows (same geometry, one pair table each) so the SwiGLU product
+// (qwen3_5.cpp:1123-1126) is formed in the epilogue.  The small loads (LUT,
+// x, norm weight) are issued before the weight stream, because vector memory
+// waits complete in order.
+
+constexpr float kLoScale = 2048.0f;   // 2^11: low part of x kept in fp16 normal range
+
+// Output modes of the tile kernel.
+enum : int { kOutY = 0, kOutGU = 1, kOutH = 2 };
+
+struct TileArgs {
+    const uint8_t* w[2];
+    const uint16_t* lut[2];
+    float* y[2];          // kOutY: y[0]; kOutGU: g = y[0], u = y[1]; kOutH: h = y[0]
+    const float* x;
+    const float* nw;      // RMSNorm weight (NULL: no norm)
+    float eps;
+    int n_mat;            // 1 or 2
+    int mode;             // kOut*
+    int residual;         // kOutY: y += W x
+    int in_dim, C, P, RP, T;
+    int tpr;              // reduction threads per row (power of two <= 64)
+};
+
+// LDS byte offset of the pair-table entry addressed by the 12-bit field at
+// bit B of the 96-bit chunk, OR-ed with the table base `tb` (bit 14).
+template <int B>
+__device__ __forceinline__ uint32_t pair_addr(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t tb) {
+    uint32_t v;
+    if constexpr (B == 0) {
+        v = w0 << 2;
+    } else {
+        constexpr int s = B - 2, d = s >> 5, sh = s & 31;
+        const uint32_t lo = d == 0 ? w0 : (d == 1 ? w1 : w2);
+        const uint32_t hi = d == 0 ? w1 : w2;
+        v = (sh + 14 <= 32) ? (lo >> sh) : __builtin_amdgcn_alignbit(hi, lo, sh);
+    }
+    return (v & 0x3FFCu) | tb;
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+// Word 3 of a raw (unformatted, stride 0) buffer descriptor on gfx9-class GPUs.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ float dot2(uint32_t p, uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, p), __builtin_bit_cast(half2_t, x), acc,
+                                  false);
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const char* base, uint32_t byte_off) {
+    return *reinterpret_cast<const uint32_t*>(base + byte_off);
+}
+
+// One 16-index chunk against the lane's x halves.
+__device__ __forceinline__ float chunk_dot2(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1,
+                                            uint32_t w2, const uint32_t (&xh)[8],
+                                            const uint32_t (&xl)[8]) {
+    uint32_t p[8];
+    p[0] = lds_u32(lds, pair_addr<0>(w0, w1, w2, tb));
+    p[1] = lds_u32(lds, pair_addr<12>(w0, w1, w2, tb));
+    p[2] = lds_u32(lds, pair_addr<24>(w0, w1, w2, tb));
+    p[3] = lds_u32(lds, pair_addr<36>(w0, w1, w2, tb));
+    p[4] = lds_u32(lds, pair_addr<48>(w0, w1, w2, tb));
+    p[5] = lds_u32(lds, pair_addr<60>(w0, w1, w2, tb));
+    p[6] = lds_u32(lds, pair_addr<72>(w0, w1, w2, tb));
+    p[7] = lds_u32(lds, pair_addr<84>(w0, w1, w2, tb));
+    float h0 = 0.f, h1 = 0.f, l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+        h0 = dot2(p[k], xh[k], h0);
+        h1 = dot2(p[k + 1], xh[k + 1], h1);
+        l0 = dot2(p[k], xl[k], l0);
+        l1 = dot2(p[k + 1], xl[k + 1], l1);
+    }
+    return (h0 + h1) + (l0 + l1) * (1.0f / kLoScale);
+}
+
+template <int NI>
+__global__ __launch_bounds__(1024) void lut6_tile_kernel(const TileArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    __shared__ float ssp[16];
+    __shared__ float fin[2][32];
+
+    const int C = a.C, P = a.P;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int mt = wi / P, w = wi - mt * P;       // matrix, wave within the matrix
+    const int g = 64 * w + lane;                  // lane index within the matrix's waves
+    const int d = g / C, pos = g - d * C;
+    const int r0 = blockIdx.x * a.T;              // first row of the tile
+    const int grp = r0 >> 5;                      // LUT group
+    const bool xl_owner = mt == 0 && g < C;       // loads x for chunk `pos`
+    const int n_waves = a.n_mat * P;
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + a.n_mat * 16384);   // [16][C]
+
+    // 1. small loads first: LUT entries, x chunk, norm weight chunk
+    const uint32_t lut0 = a.lut[0][(size_t)grp * 64 + lane];
+    const uint32_t lut1 = a.n_mat > 1 ? a.lut[1][(size_t)grp * 64 + lane] : 0u;
+    float4 xv[4], nv[4];
+    if (xl_owner) {
+        const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)pos * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) xv[q] = xp[q];
+        if (a.nw) {
+            const float4* np = reinterpret_cast<const float4*>(a.nw + (size_t)pos * 16);
+#pragma unroll
+            for (int q = 0; q < 4; q++) nv[q] = np[q];
+        }
+    }
+    // 2. the weight stream of this lane
+    // (select, not a.w[mt]: a runtime index into the argument struct becomes a
+    // vector load whose wait would also wait for the x loads above)
+    // Raw buffer loads over the tile (bounds-checked by the descriptor): the
+    // base stays in scalar registers, the lane offset is 32-bit, and the
+    // per-instruction step is a scalar offset.
+    const uint8_t* Wt = (mt ? a.w[1] : a.w[0]) + (size_t)r0 * C * 12;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Wt, 0, a.T * C * 12, kBufferRsrcWord3);
+    const int voff = (w * 64 + lane) * 12;
+    u32x3 wv[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) wv[m] = __builtin_amdgcn_raw_buffer_load_b96(rsrc, voff, m * P * 768, 0);
+    // 3. pair tables: wave wi writes rows i1 = wi, wi + n_waves, ... of both
+    for (int ri = wi; ri < a.n_mat * 64; ri += n_waves) {
+        const int tm = ri >> 6, i1 = ri & 63;
+        const uint32_t mine = tm ? lut1 : lut0;
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)mine, i1);
+        *reinterpret_cast<uint32_t*>(lds + tm * 16384 + i1 * 256 + lane * 4) = mine | (hi << 16);
+    }
+    // 4. RMSNorm statistics over x (each position is owned once)
+    float ss = 0.f;
+    if (xl_owner && a.nw) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            ss += xv[q].x * xv[q].x + xv[q].y * xv[q].y + xv[q].z * xv[q].z + xv[q].w * xv[q].w;
+    }
+    if (a.nw && mt == 0) {
+        ss = wave_sum(ss);
+        if (lane == 0) ssp[w] = ss;
+    }
+    __syncthreads();
+    if (xl_owner) {
+        float xf[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            xf[4 * q] = xv[q].x; xf[4 * q + 1] = xv[q].y; xf[4 * q + 2] = xv[q].z; xf[4 * q + 3] = xv[q].w;
+        }
+        if (a.nw) {
+            float tot = 0.f;
+            for (int i = 0; i < P; i++) tot += ssp[i];
+            const float inv = 1.0f / sqrtf(tot / (float)a.in_dim + a.eps);
+            float nf[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                nf[4 * q] = nv[q].x; nf[4 * q + 1] = nv[q].y; nf[4 * q + 2] = nv[q].z; nf[4 * q + 3] = nv[q].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) xf[i] = (xf[i] * inv) * nf[i];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const _Float16 h0 = (_Float16)xf[2 * k], h1 = (_Float16)xf[2 * k + 1];
+            const _Float16 l0 = (_Float16)((xf[2 * k] - (float)h0) * kLoScale);
+            const _Float16 l1 = (_Float16)((xf[2 * k + 1] - (float)h1) * kLoScale);
+            xs[k * C + pos] = __builtin_bit_cast(uint32_t, half2_t{h0, h1});
+            xs[(8 + k) * C + pos] = __builtin_bit_cast(uint32_t, half2_t{l0, l1});
+        }
+    }
+    __syncthreads();
+    uint32_t xh[8], xl[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        xh[k] = xs[k * C + pos];
+        xl[k] = xs[(8 + k) * C + pos];
+    }
+    // 5. dot products
+    const uint32_t tb = (uint32_t)mt * 16384u;
+    float part[NI];
+#pragma unroll
+    for (int m = 0; m < NI; m++) part[m] = chunk_dot2(lds, tb, wv[m].x, wv[m].y, wv[m].z, xh, xl);
+    // 6. row sums: partials [mt][m][g] in LDS (over the dead tables), then
+    // tpr threads per row sum the C partials of the row in a fixed order.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);
+    const int stride = 64 * P;
+#pragma unroll
+    for (int m = 0; m < NI; m++) red[(mt * NI + m) * stride + g] = part[m];
+    __syncthreads();
+    {
+        const int tpr = a.tpr, T = a.T;
+        const int grp_t = tid / tpr, j = tid - grp_t * tpr;
+        float s = 0.f;
+        const bool active = grp_t < a.n_mat * T;
+        int rm = 0, rr = 0;
+        if (active) {
+            rm = grp_t / T;
+            rr = grp_t - rm * T;
+            const int m = rr / a.RP, dd = rr - m * a.RP;
+            const float* src = red + (rm * NI + m) * stride + C * dd;
+            for (int i = j; i < C; i += tpr) s += src[i];
+        }
+        for (int msk = tpr >> 1; msk >= 1; msk >>= 1) s += __shfl_xor(s, msk, 64);
+        if (active && j == 0) fin[rm][rr] = s;
+    }
+    __syncthreads();
+    if (tid < a.T) {
+        const int r = r0 + tid;
+        if (a.mode == kOutH) {
+            const float gv = fin[0][tid];
+            a.y[0][r] = (gv / (1.0f + expf(-gv))) * fin[1][tid];
+        } else if (a.mode == kOutGU) {
+            a.y[0][r] = fin[0][tid];
+            a.y[1][r] = fin[1][tid];
+        } else {
+            a.y[0][r] = a.residual ? a.y[0][r] + fin[0][tid] : fin[0][tid];
+        }
+    }
+}
+
+// Tile geometry for in_dim, or false when the fast path does not apply.
+struct TileGeom {
+    int C, P, RP;
+};
+bool tile_geom(int in_dim, int n_mat, TileGeom& g) {
+    if (in_dim % 32 != 0) return false;
+    const int C = in_dim / 16;
+    int gc = 64;
+    while (C % gc) gc >>= 1;
+    const int P = C / gc;
+    if (P * n_mat > 16) return false;
+    g.C = C;
+    g.P = P;
+    g.RP = 64 / gc;
+    return g.RP <= 32;
+}
+
+// Launches the tile kernel with about `want_ni` instructions per wave (rows
+// per tile = NI * RP, at most 32 so a tile stays in one LUT group).
+int tile_launch(TileArgs a, const TileGeom& g, int out_dim, int want_ni, hipStream_t st) {
+    a.C = g.C;
+    a.P = g.P;
+    a.RP = g.RP;
+    int ni = want_ni;
+    while (ni > 1 && ni * g.RP > 32) ni >>= 1;
+    a.T = ni * g.RP;
+    const int nt = a.n_mat * g.P * 64;
+    int tpr = 64;
+    while (tpr > 1 && a.n_mat * a.T * tpr > nt) tpr >>= 1;
+    a.tpr = tpr;
+    const size_t tabs = (size_t)a.n_mat * 16384 + (size_t)g.C * 64;
+    const size_t red = (size_t)a.n_mat * ni * g.P * 64 * 4;
+    const size_t lds = tabs > red ? tabs : red;
+    const dim3 grid(out_dim / a.T), block(nt);
+    switch (ni) {
+        case 1: hipLaunchKernelGGL(lut6_tile_kernel<1>, grid, block, lds, st, a); break;
+        case 2: hipLaunchKernelGGL(lut6_tile_kernel<2>, grid, block, lds, st, a); break;
+        case 4: hipLaunchKernelGGL(lut6_tile_kernel<4>, grid, block, lds, st, a); break;
+        case 8: hipLaunchKernelGGL(lut6_tile_kernel<8>, grid, block, lds, st, a); break;
+        default: hipLaunchKernelGGL(lut6_tile_kernel<16>, grid, block, lds, st, a); break;
+    }
+    ANELM_LAUNCHED("lut6_tile_kernel");
+    return ANELM_OK;
+}
+
 __global__ void lut6_unpack_kernel(uint8_t* idx, const uint8_t* packed, int64_t groups) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= groups) return;
@@ -311,10 +595,35 @@ int check_shape(int out_dim, int in_dim) {
     return ANELM_OK;
 }
 
-// g = gate n, u = up n with n = rmsnorm(x) (or x).
-int gate_up(float* g, float* u, const float* x, const float* norm_w, float eps, const uint8_t* gw,
-            const uint16_t* gl, const uint8_t* uw, const uint16_t* ul, int hidden, int inter,
-            hipStream_t st) {
+// g = gate n, u = up n with n = rmsnorm(x) (or x); with h != NULL the SwiGLU
+// product h = silu(g) * u is written instead.  Only the fallback path stores
+// g and u then: into the given buffers (h may alias g), else the workspace.
+int gate_up(float* g, float* u, float* h, const float* x, const float* norm_w, float eps,
+            const uint8_t* gw, const uint16_t* gl, const uint8_t* uw, const uint16_t* ul, int hidden,
+            int inter, hipStream_t st) {
+    TileGeom geo;
+    if (tile_geom(hidden, 2, geo)) {
+        TileArgs a{};
+        a.w[0] = gw;
+        a.lut[0] = gl;
+        a.w[1] = uw;
+        a.lut[1] = ul;
+        a.y[0] = h ? h : g;
+        a.y[1] = h ? nullptr : u;
+        a.x = x;
+        a.nw = norm_w;
+        a.eps = eps;
+        a.n_mat = 2;
+        a.mode = h ? kOutH : kOutGU;
+        a.in_dim = hidden;
+        return tile_launch(a, geo, inter, 8, st);
+    }
+    if (h && !(g && u)) {
+        float* gu = static_cast<float*>(workspace((size_t)2 * inter * sizeof(float), st));
+        if (!gu) return ANELM_ENOMEM;
+        g = gu;
+        u = gu + inter;
+    }
     GemvArgs a{};
     a.w[0] = gw;
     a.lut[0] = gl;
@@ -327,7 +636,38 @@ int gate_up(float* g, float* u, const float* x, const float* norm_w, float eps, 
     a.x = x;
     a.nw = norm_w;
     a.eps = eps;
-    return norm_w ? gemv_dispatch<kStageNorm>(a, 2, st) : gemv_dispatch<kStageCopy>(a, 2, st);
+    int rc = norm_w ? gemv_dispatch<kStageNorm>(a, 2, st) : gemv_dispatch<kStageCopy>(a, 2, st);
+    if (rc || !h) return rc;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((inter + 255) / 256), dim3(256), 0, st, h, g, u, inter);
+    ANELM_LAUNCHED("swiglu_kernel");
+    return ANELM_OK;
+}
+
+// y = W x, or y += W x with `residual`.
+int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int out_dim, int in_dim,
+         int residual, hipStream_t st) {
+    TileGeom geo;
+    if (tile_geom(in_dim, 1, geo)) {
+        TileArgs a{};
+        a.w[0] = w;
+        a.lut[0] = lut;
+        a.y[0] = y;
+        a.x = x;
+        a.n_mat = 1;
+        a.mode = kOutY;
+        a.residual = residual;
+        a.in_dim = in_dim;
+        return tile_launch(a, geo, out_dim, 8, st);
+    }
+    GemvArgs a{};
+    a.w[0] = w;
+    a.lut[0] = lut;
+    a.y[0] = y;
+    a.out_dim = out_dim;
+    a.in_dim = in_dim;
+    a.x = x;
+    a.residual = residual;
+    return gemv_dispatch<kStageCopy>(a, 1, st);
 }
 
 }  // namespace
@@ -357,14 +697,7 @@ int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float
     ANELM_NONNULL(x);
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
-    GemvArgs a{};
-    a.w[0] = w;
-    a.lut[0] = lut;
-    a.y[0] = y;
-    a.out_dim = out_dim;
-    a.in_dim = in_dim;
-    a.x = x;
-    return gemv_dispatch<kStageCopy>(a, 1, as_stream(stream));
+    return gemv(y, w, lut, x, out_dim, in_dim, 0, as_stream(stream));
 }
 
 int anelm_lut6_gate_up(float* g, float* u, const float* x, const float* norm_w, float eps,
@@ -379,7 +712,7 @@ int anelm_lut6_gate_up(float* g, float* u, const float* x, const float* norm_w, 
     ANELM_NONNULL(up_lut);
     int rc = check_shape(inter, hidden);
     if (rc) return rc;
-    return gate_up(g, u, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter,
+    return gate_up(g, u, nullptr, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter,
                    as_stream(stream));
 }
 
@@ -394,14 +727,8 @@ int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
     ANELM_NONNULL(up_lut);
     int rc = check_shape(inter, hidden);
     if (rc) return rc;
-    hipStream_t st = as_stream(stream);
-    float* gu = static_cast<float*>(workspace((size_t)2 * inter * sizeof(float), st));
-    if (!gu) return ANELM_ENOMEM;
-    rc = gate_up(gu, gu + inter, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter, st);
-    if (rc) return rc;
-    hipLaunchKernelGGL(swiglu_kernel, dim3((inter + 255) / 256), dim3(256), 0, st, h, gu, gu + inter, inter);
-    ANELM_LAUNCHED("swiglu_kernel");
-    return ANELM_OK;
+    return gate_up(nullptr, nullptr, h, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter,
+                   as_stream(stream));
 }
 
 int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
@@ -421,20 +748,11 @@ int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
     rc = check_shape(hidden, inter);
     if (rc) return rc;
     hipStream_t st = as_stream(stream);
-    float* g = gu_scratch;
-    float* u = gu_scratch + inter;
-    rc = gate_up(g, u, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut, hidden, inter, st);
+    float* h = gu_scratch;
+    rc = gate_up(gu_scratch, gu_scratch + inter, h, x, norm_w, eps, gate_w, gate_lut, up_w, up_lut,
+                 hidden, inter, st);
     if (rc) return rc;
-    GemvArgs a{};
-    a.w[0] = down_w;
-    a.lut[0] = down_lut;
-    a.y[0] = x;
-    a.out_dim = hidden;
-    a.in_dim = inter;
-    a.x = g;
-    a.x2 = u;
-    a.residual = 1;
-    return gemv_dispatch<kStageSwiglu>(a, 1, st);
+    return gemv(x, down_w, down_lut, h, hidden, inter, 1, st);
 }
 
 int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
@@ -462,14 +780,7 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     float* cv = reinterpret_cast<float*>(ws + logits_bytes);
     int* ci = reinterpret_cast<int*>(ws + logits_bytes + (size_t)batch * n_cand * sizeof(float));
     for (int b = 0; b < batch; b++) {
-        GemvArgs a{};
-        a.w[0] = w;
-        a.lut[0] = lut;
-        a.y[0] = logits + (size_t)b * out_dim;
-        a.out_dim = out_dim;
-        a.in_dim = in_dim;
-        a.x = x + (size_t)b * in_dim;
-        rc = gemv_dispatch<kStageCopy>(a, 1, st);
+        rc = gemv(logits + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, 0, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(kNT), 0, st, logits, out_dim, k,

@@ -191,7 +191,8 @@ int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float
 /* SwiGLU FFN block with residual (qwen3_5.cpp:1335-1354 with the MLP of
  * :1118-1130): n = rmsnorm(x, norm_w, eps) (skipped when norm_w is NULL);
  * x += down( silu(gate n) * (up n) ).  x [hidden] is updated in place;
- * gu_scratch [2*inter] receives gate n and up n. */
+ * gu_scratch [2*inter] is scratch: its first inter entries receive
+ * h = silu(gate n) * (up n), the rest is undefined. */
 int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
                    const uint8_t* gate_w, const uint16_t* gate_lut,
                    const uint8_t* up_w, const uint16_t* up_lut,
