@@ -81,13 +81,14 @@ enum : int { kStageCopy = 0, kStageNorm = 1, kStageSwiglu = 2 };
 //   copy:   xs = x
 //   norm:   xs = rmsnorm(x, nw, eps)           (cpu_ops.cpp:24-30)
 //   swiglu: xs = silu(x) * x2                  (qwen3_5.cpp:1123-1126)
+// then rounded to fp16 (the LUT6 matrices take fp16 activations).
 template <int MODE>
 __device__ void stage_x(float* xs, const float* x, const float* x2, const float* nw, float eps, int n,
                         float* red) {
     if (MODE == kStageSwiglu) {
         for (int i = threadIdx.x; i < n; i += kNT) {
             const float g = x[i];
-            xs[i] = (g / (1.0f + expf(-g))) * x2[i];
+            xs[i] = (float)(_Float16)((g / (1.0f + expf(-g))) * x2[i]);
         }
         return;
     }
@@ -100,7 +101,9 @@ __device__ void stage_x(float* xs, const float* x, const float* x2, const float*
     if (MODE == kStageNorm && nw != nullptr) {
         ss = block_sum<kNT>(ss, red);
         const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-        for (int i = threadIdx.x; i < n; i += kNT) xs[i] = (xs[i] * inv) * nw[i];
+        for (int i = threadIdx.x; i < n; i += kNT) xs[i] = (float)(_Float16)((xs[i] * inv) * nw[i]);
+    } else {
+        for (int i = threadIdx.x; i < n; i += kNT) xs[i] = (float)(_Float16)xs[i];
     }
 }
 
@@ -192,10 +195,10 @@ __global__ __launch_bounds__(kNT) void lut6_gemv_kernel(const GemvArgs a) {
 // sees the same chunk position pos = (64w + l) % C, on row RP*m + d of
 // instruction m, where RP = 64P/C and d = (64w + l) / C.  Every lane
 // therefore needs the 16 x values of ONE chunk for the whole tile: they sit
-// in registers, split into an fp16 high part and a 2^11-scaled fp16 low
-// part, and each pair of weights is dotted with both halves by
-// v_dot2_f32_f16 (fp16 products are exact in fp32, so the result carries
-// about 22 bits of x).  A 12-bit index pair selects one dword of the LDS pair
+// in registers as fp16 pairs -- the LUT6 matrices take fp16 activations, as
+// the reference's CoreML models do (core/coreml_runtime.cpp:331-336) -- and
+// v_dot2_f32_f16 dots two weights with two x values, accumulating in fp32
+// (fp16 products are exact in fp32).  A 12-bit index pair selects one dword of the LDS pair
 // table T[(i1 << 6) | i0] = lut[i0] | lut[i1] << 16, built from the group's
 // LUT held one entry per lane.  Partial sums are reduced through LDS in a
 // fixed order, so results are deterministic.
@@ -205,8 +208,6 @@ __global__ __launch_bounds__(kNT) void lut6_gemv_kernel(const GemvArgs a) {
 // (qwen3_5.cpp:1123-1126) is formed in the epilogue.  The small loads (LUT,
 // x, norm weight) are issued before the weight stream, because vector memory
 // waits complete in order.
-
-constexpr float kLoScale = 2048.0f;   // 2^11: low part of x kept in fp16 normal range
 
 // Output modes of the tile kernel.
 enum : int { kOutY = 0, kOutGU = 1, kOutH = 2 };
@@ -256,10 +257,9 @@ __device__ __forceinline__ uint32_t lds_u32(const char* base, uint32_t byte_off)
     return *reinterpret_cast<const uint32_t*>(base + byte_off);
 }
 
-// One 16-index chunk against the lane's x halves.
+// One 16-index chunk against the lane's fp16 x pairs.
 __device__ __forceinline__ float chunk_dot2(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1,
-                                            uint32_t w2, const uint32_t (&xh)[8],
-                                            const uint32_t (&xl)[8]) {
+                                            uint32_t w2, const uint32_t (&xh)[8]) {
     uint32_t p[8];
     p[0] = lds_u32(lds, pair_addr<0>(w0, w1, w2, tb));
     p[1] = lds_u32(lds, pair_addr<12>(w0, w1, w2, tb));
@@ -269,15 +269,13 @@ __device__ __forceinline__ float chunk_dot2(const char* lds, uint32_t tb, uint32
     p[5] = lds_u32(lds, pair_addr<60>(w0, w1, w2, tb));
     p[6] = lds_u32(lds, pair_addr<72>(w0, w1, w2, tb));
     p[7] = lds_u32(lds, pair_addr<84>(w0, w1, w2, tb));
-    float h0 = 0.f, h1 = 0.f, l0 = 0.f, l1 = 0.f;
+    float h0 = 0.f, h1 = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k += 2) {
         h0 = dot2(p[k], xh[k], h0);
         h1 = dot2(p[k + 1], xh[k + 1], h1);
-        l0 = dot2(p[k], xl[k], l0);
-        l1 = dot2(p[k + 1], xl[k + 1], l1);
     }
-    return (h0 + h1) + (l0 + l1) * (1.0f / kLoScale);
+    return h0 + h1;
 }
 
 template <int NI>
@@ -296,7 +294,7 @@ __global__ __launch_bounds__(1024) void lut6_tile_kernel(const TileArgs a) {
     const int grp = r0 >> 5;                      // LUT group
     const bool xl_owner = mt == 0 && g < C;       // loads x for chunk `pos`
     const int n_waves = a.n_mat * P;
-    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + a.n_mat * 16384);   // [16][C]
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + a.n_mat * 16384);   // [8][C]
 
     // 1. small loads first: LUT entries, x chunk, norm weight chunk
     const uint32_t lut0 = a.lut[0][(size_t)grp * 64 + lane];
@@ -365,24 +363,18 @@ __global__ __launch_bounds__(1024) void lut6_tile_kernel(const TileArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const _Float16 h0 = (_Float16)xf[2 * k], h1 = (_Float16)xf[2 * k + 1];
-            const _Float16 l0 = (_Float16)((xf[2 * k] - (float)h0) * kLoScale);
-            const _Float16 l1 = (_Float16)((xf[2 * k + 1] - (float)h1) * kLoScale);
             xs[k * C + pos] = __builtin_bit_cast(uint32_t, half2_t{h0, h1});
-            xs[(8 + k) * C + pos] = __builtin_bit_cast(uint32_t, half2_t{l0, l1});
         }
     }
     __syncthreads();
-    uint32_t xh[8], xl[8];
+    uint32_t xh[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        xh[k] = xs[k * C + pos];
-        xl[k] = xs[(8 + k) * C + pos];
-    }
+    for (int k = 0; k < 8; k++) xh[k] = xs[k * C + pos];
     // 5. dot products
     const uint32_t tb = (uint32_t)mt * 16384u;
     float part[NI];
 #pragma unroll
-    for (int m = 0; m < NI; m++) part[m] = chunk_dot2(lds, tb, wv[m].x, wv[m].y, wv[m].z, xh, xl);
+    for (int m = 0; m < NI; m++) part[m] = chunk_dot2(lds, tb, wv[m].x, wv[m].y, wv[m].z, xh);
     // 6. row sums: partials [mt][m][g] in LDS (over the dead tables), then
     // tpr threads per row sum the C partials of the row in a fixed order.
     __syncthreads();
@@ -452,7 +444,7 @@ int tile_launch(TileArgs a, const TileGeom& g, int out_dim, int want_ni, hipStre
     int tpr = 64;
     while (tpr > 1 && a.n_mat * a.T * tpr > nt) tpr >>= 1;
     a.tpr = tpr;
-    const size_t tabs = (size_t)a.n_mat * 16384 + (size_t)g.C * 64;
+    const size_t tabs = (size_t)a.n_mat * 16384 + (size_t)g.C * 32;
     const size_t red = (size_t)a.n_mat * ni * g.P * 64 * 4;
     const size_t lds = tabs > red ? tabs : red;
     const dim3 grid(out_dim / a.T), block(nt);

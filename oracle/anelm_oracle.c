@@ -455,18 +455,26 @@ void orc_lut6_dequant_row(float* w, const uint8_t* packed_row, const uint16_t* l
 }
 
 /* matvec (core/cpu_ops.cpp:77-80) on the dequantised rows; row r uses the
- * 64-entry fp16 LUT of its 32-row group r/32. */
+ * 64-entry fp16 LUT of its 32-row group r/32.  The input vector is rounded to
+ * fp16 first (round to nearest even): the reference runs its LUT6 matrices
+ * only inside CoreML models whose inputs are fp16 (scripts/export_hybrid_chunks.py:507
+ * declares x float16; core/coreml_runtime.cpp:331-336 converts the fp32
+ * activations with vImageConvert_PlanarFtoPlanar16F).  Products and the sum
+ * are fp32. */
 void orc_lut6_matvec(float* y, const uint8_t* packed, const uint16_t* lut, const float* x,
                      int out_dim, int in_dim, int row_begin, int row_end) {
     (void)out_dim;
     float* w = (float*)malloc(sizeof(float) * (size_t)in_dim);
+    float* xh = (float*)malloc(sizeof(float) * (size_t)in_dim);
+    for (int c = 0; c < in_dim; c++) xh[c] = orc_f16_to_f32(orc_f32_to_f16(x[c]));
     long row_bytes = (long)in_dim * 3 / 4;
     for (int r = row_begin; r < row_end; r++) {
         orc_lut6_dequant_row(w, packed + (long)r * row_bytes, lut + (long)(r / 32) * 64, in_dim);
         float s = 0.0f;
-        for (int c = 0; c < in_dim; c++) s += w[c] * x[c];
+        for (int c = 0; c < in_dim; c++) s += w[c] * xh[c];
         y[r - row_begin] = s;
     }
+    free(xh);
     free(w);
 }
 

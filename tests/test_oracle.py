@@ -415,10 +415,13 @@ def test_lut6_matvec_dequant(orc):
     x = np.random.default_rng(20).standard_normal(160).astype(np.float32)
     W = lut6_dense(idx, lut)
     got = orc.lut6_matvec(packed, lut, x, 96, 160)
-    assert rel_l2(got, W.astype(np.float64) @ x) < 1e-6
+    # the input enters as fp16 (round to nearest even), as at the CoreML boundary
+    x16 = widen(f16(x)).astype(np.float64)
+    assert rel_l2(got, W.astype(np.float64) @ x16) < 1e-6
+    assert rel_l2(got, W.astype(np.float64) @ x.astype(np.float64)) > 1e-5
     # rows use the LUT of their own 32-row group
     lut_shift = np.roll(lut, 1, axis=0)
-    assert rel_l2(orc.lut6_matvec(packed, lut_shift, x, 96, 160), W.astype(np.float64) @ x) > 0.1
+    assert rel_l2(orc.lut6_matvec(packed, lut_shift, x, 96, 160), W.astype(np.float64) @ x16) > 0.1
     assert np.array_equal(orc.lut6_matvec(packed, lut, x, 96, 160, 32, 64), got[32:64])
 
 
@@ -430,8 +433,10 @@ def test_lut6_ffn_swiglu(orc):
     x = np.random.default_rng(24).standard_normal(H).astype(np.float32)
     got = orc.lut6_ffn(x, g[:2], u[:2], d[:2], H, I)
     G, U, Dn = (lut6_dense(m[2], m[1]).astype(np.float64) for m in (g, u, d))
-    gx = G @ x
-    ref = Dn @ (gx / (1 + np.exp(-gx)) * (U @ x))
+    x16 = widen(f16(x)).astype(np.float64)
+    gx = G @ x16
+    h = (gx / (1 + np.exp(-gx)) * (U @ x16)).astype(np.float32)
+    ref = Dn @ widen(f16(h)).astype(np.float64)
     assert rel_l2(got, ref) < 1e-5
 
 
