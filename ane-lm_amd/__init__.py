@@ -63,6 +63,7 @@ SIGNATURES = {
     "anelm_lut6_topk": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "anelm_hybrid_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P, _I, _P],
     "anelm_hybrid_step_run": [_P, _P],
+    "anelm_hybrid_step_status": [_P, _IP],
     "anelm_hybrid_step_destroy": [_P],
     # compat tier (host pointers, synchronous)
     "anelm_cpu_silu_vec_inplace": [_P, _I, _P],
@@ -149,5 +150,9 @@ class HybridDims(ctypes.Structure):
 
 LAYER_DELTANET = 0
 LAYER_ATTENTION = 1
+STEP_EAGER = 0
+STEP_GRAPH = 1
+STEP_PERSISTENT = 2
+STEP_STATIC = 4
 
 from . import ops  # noqa: E402,F401

@@ -73,6 +73,15 @@ void rope_row(float* cos_out, float* sin_out, int rot_dim, int pos, float theta)
 
 constexpr int kMaxRotPairs = 128;
 
+// Persistent decode step (step_persistent.hip): one kernel launch per step.
+struct PersistentStep;
+int persistent_create(PersistentStep** out, const anelm_hybrid_dims* dims,
+                      const anelm_hybrid_layer* layers, int n_layers, float* x, float* h,
+                      hipStream_t stream);
+int persistent_run(PersistentStep* s, bool advance, hipStream_t stream);
+int persistent_status(PersistentStep* s, int* status);
+void persistent_destroy(PersistentStep* s);
+
 // ------------------------------------------------------------- device code
 
 __device__ __forceinline__ float h2f(uint16_t h) {

@@ -12,8 +12,10 @@ struct anelm_hybrid_step {
     float* x = nullptr;
     float* h = nullptr;
     bool use_graph = false;
+    int mode = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    anelm::PersistentStep* ps = nullptr;
 };
 
 namespace anelm {
@@ -57,13 +59,17 @@ using namespace anelm;
 
 extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hybrid_dims* dims,
                                         const anelm_hybrid_layer* layers, int n_layers, float* x,
-                                        float* h_scratch, int use_graph, void* stream) {
+                                        float* h_scratch, int mode, void* stream) {
     ANELM_NONNULL(out);
     ANELM_NONNULL(dims);
     ANELM_NONNULL(layers);
     ANELM_NONNULL(x);
     ANELM_NONNULL(h_scratch);
     ANELM_REQUIRE(n_layers > 0, "hybrid_step: n_layers %d", n_layers);
+    ANELM_REQUIRE(mode == ANELM_STEP_EAGER || mode == ANELM_STEP_GRAPH || mode == ANELM_STEP_PERSISTENT ||
+                      mode == (ANELM_STEP_PERSISTENT | ANELM_STEP_STATIC),
+                  "hybrid_step: mode %d unknown", mode);
+    const bool use_graph = mode == ANELM_STEP_GRAPH;
     ANELM_REQUIRE(!use_graph || stream != nullptr, "hybrid_step: graph capture needs a non-null stream");
     for (int i = 0; i < n_layers; i++)
         ANELM_REQUIRE(layers[i].kind == ANELM_LAYER_ATTENTION || layers[i].kind == ANELM_LAYER_DELTANET,
@@ -73,8 +79,18 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
     s->layers.assign(layers, layers + n_layers);
     s->x = x;
     s->h = h_scratch;
-    s->use_graph = use_graph != 0;
+    s->use_graph = use_graph;
+    s->mode = mode;
     hipStream_t st = as_stream(stream);
+    if (mode & ANELM_STEP_PERSISTENT) {
+        const int rc = persistent_create(&s->ps, dims, layers, n_layers, x, h_scratch, st);
+        if (rc != ANELM_OK) {
+            delete s;
+            return rc;
+        }
+        *out = s;
+        return ANELM_OK;
+    }
     if (s->use_graph) {
         // Warm-up: grows the workspace outside the capture.
         int rc = launch_all(s, st, false);
@@ -109,6 +125,7 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
 extern "C" int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream) {
     ANELM_NONNULL(step);
     hipStream_t st = as_stream(stream);
+    if (step->ps) return persistent_run(step->ps, (step->mode & ANELM_STEP_STATIC) == 0, st);
     if (step->use_graph) {
         ANELM_HIP(hipGraphLaunch(step->exec, st));
         return ANELM_OK;
@@ -116,8 +133,16 @@ extern "C" int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream) {
     return launch_all(step, st, true);
 }
 
+extern "C" int anelm_hybrid_step_status(anelm_hybrid_step* step, int* status) {
+    ANELM_NONNULL(step);
+    ANELM_NONNULL(status);
+    *status = 0;
+    return step->ps ? persistent_status(step->ps, status) : ANELM_OK;
+}
+
 extern "C" int anelm_hybrid_step_destroy(anelm_hybrid_step* step) {
     if (!step) return ANELM_OK;
+    if (step->ps) persistent_destroy(step->ps);
     if (step->exec) (void)hipGraphExecDestroy(step->exec);
     if (step->graph) (void)hipGraphDestroy(step->graph);
     delete step;

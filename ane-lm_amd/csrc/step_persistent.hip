@@ -1,0 +1,1476 @@
+// Persistent decode step: the whole layer loop of Qwen35Model::forward
+// (models/llm/qwen3_5.cpp:1278-1356) over the compute cores -- per layer the
+// DeltaNet core (:849-910) or the full-attention core (:944-1002), then the
+// LUT6 SwiGLU FFN with RMSNorm and residual (:1335-1354, MLP :1118-1130) --
+// as ONE kernel launch with one workgroup per compute unit.
+//
+// Why one launch: a decode step is ~100 dependent phases of 2-35 MB each.
+// As separate kernels every phase pays launch, ramp-up and drain (~4.5 us
+// measured for a 35 MB read on MI355X).  Here the phases are separated by a
+// grid barrier instead, and each workgroup issues the weight / KV / state
+// loads of the NEXT phase before it waits on the barrier, so HBM keeps
+// streaming while the barrier resolves.
+//
+// Phase order is the model's dependency chain, per layer L:
+//   core(L) -> barrier -> gate/up(L) -> barrier -> down(L) -> barrier -> core(L+1)
+// (the projections around the cores are not part of the step; the chain keeps
+// the order they would impose).
+//
+// Workgroup = 10 compute waves + 1 control wave.  Compute waves only stream
+// bulk data (weights, KV rows, state) and compute.  The control wave does all
+// cross-workgroup traffic: it stores the phase outputs, arrives at and polls
+// the barrier, and stages the next phase's small inputs (x, h, q, ...) into
+// LDS.  Vector-memory waits complete in issue order, so a poll issued by a
+// wave with bulk loads in flight could not complete before them; keeping the
+// polls in a wave without bulk loads leaves those loads in flight.
+//
+// Cross-workgroup data (x, h, split partials) is written and read with
+// device-scope coherent accesses (relaxed agent-scope atomics; sc1 buffer
+// loads); the barrier counters are relaxed agent-scope atomics issued after the
+// writer's stores have completed (s_waitcnt vmcnt(0)).  Counters sit on
+// separate 256-byte lines (same-line atomics serialise): 16 group counters, a
+// root counter, and one release flag per group.  Every wait is bounded: on
+// timeout the kernel sets an abort flag that all waits observe, records a
+// status word, and every workgroup exits.
+#include "anelm_internal.hpp"
+
+#include <math.h>
+#include <string.h>
+#include <vector>
+
+struct anelm_hybrid_step;
+
+namespace anelm {
+namespace pk {
+
+constexpr int kCW = 10;               // compute waves
+constexpr int kNW = kCW + 1;          // + control wave
+constexpr int kNT = kNW * 64;         // threads per workgroup
+constexpr int kCtl = kCW;             // control wave index
+
+constexpr int kW3 = 0x00020000;       // raw buffer descriptor word 3 (gfx9 class)
+constexpr int kSc1 = 16;              // buffer-load cache policy: device-scope coherent
+
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- sync words
+constexpr int kPad = 64;              // 256 bytes per slot
+constexpr int kNG = 16;               // barrier groups
+constexpr int kMaxPhases = 192;       // 3 per layer -> up to 64 layers
+constexpr int kMaxLayers = 64;
+constexpr int kMaxKvh = 8;
+constexpr int kSplitGroups = 8;       // two-level split combine
+constexpr int kSplitsPerGroup = 8;    // splits per group (64 splits per kv head)
+constexpr long kGrpOff = 0;
+constexpr long kRootOff = kGrpOff + (long)kMaxPhases * kNG * kPad;
+constexpr long kRelOff = kRootOff + (long)kMaxPhases * kPad;
+constexpr long kGcOff = kRelOff + (long)kMaxPhases * kNG * kPad;          // [layer][kvh][group]
+constexpr long kHcOff = kGcOff + (long)kMaxLayers * kMaxKvh * kSplitGroups * kPad;  // [layer][kvh]
+constexpr long kFinOff = kHcOff + (long)kMaxLayers * kMaxKvh * kPad;
+constexpr long kAbortOff = kFinOff + kPad;
+constexpr long kStatusOff = kAbortOff + kPad;
+constexpr long kSyncWords = kStatusOff + kPad;
+constexpr int kSpinLimit = 1 << 22;   // ~0.1-0.5 s of polling before abort
+
+// ------------------------------------------------------------------ LDS map
+constexpr int kLdsTab = 0;            // 6 pair tables x 16 KiB (GEMV); attention scratch
+constexpr int kLdsXs = 98304;         // fp16 x pairs [8][C], C <= 768
+constexpr int kLdsMisc = 122880;      // 16 KiB of per-phase small buffers
+constexpr int kLdsCtl = 139008;       // control ints (last 256 bytes)
+constexpr int kLdsBytes = 139264;
+
+constexpr int kAttnD = 256;           // head_dim of the persistent attention core
+constexpr int kAttnG = 4;             // q heads per kv head
+constexpr int kDnD = 128;             // DeltaNet key / value dim
+
+struct PLayer {
+    int kind;
+    int ring_start, ring_len, slot;   // ring after the append (len includes the new key)
+    const float* q_gate;
+    const float* k;
+    const float* v;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    const float* q_norm_w;
+    const float* k_norm_w;
+    const float* rope;                // cos[rot/2] then sin[rot/2]
+    float* state;
+    const float* dn_q;
+    const float* dn_k;
+    const float* dn_v;
+    const float* dn_a;
+    const float* dn_b;
+    const float* dn_A;
+    const float* dn_dt_bias;
+    const float* dn_z;
+    const float* dn_norm_w;
+    int dn_flags;
+    int pad_;
+    float* core_out;
+    const float* ffn_norm_w;
+    const uint8_t* w[3];              // gate, up, down
+    const uint16_t* lut[3];
+};
+
+struct PArgs {
+    const PLayer* __restrict__ layers;
+    int n_layers;
+    float* x;                         // [H]
+    float* h;                         // [I]
+    float* part;                      // [Hkv][splits][G][D+2]
+    float* gpart;                     // [Hkv][8][G][D+2]
+    unsigned* sync;
+    int H, I;
+    int gu_C, gu_P, gu_RP, gu_rows;
+    int d_C, d_P, d_RP, d_rows;
+    int Hkv, splits, kps, rot_pairs, rope_mode, cap;
+    float eps, scale;
+    int Hk, Hv;
+};
+
+// ------------------------------------------------------------- primitives
+__device__ __forceinline__ unsigned ld_sc(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ldf_sc(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_sc(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stf_sc(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned add_sc(unsigned* p, unsigned v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Compiler-only memory barrier: bounds how far the optimiser may batch loads
+// (register pressure); emits no instruction.
+__device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
+// Returns v unchanged through an empty asm: values derived from the result
+// cannot be hoisted out of the layer loop, which would keep dozens of per-lane
+// addresses live across every phase.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+// Arguments and layer descriptors are read through constant-address-space
+// pointers (scalar loads, kept off the vector-memory queue), laundered per
+// layer so nothing derived from them is hoisted out of the layer loop.
+// The host pass only parses the device functions; it has no constant
+// address space, so it sees plain const pointers.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef const __attribute__((address_space(4))) PArgs CArgs;
+typedef const __attribute__((address_space(4))) PLayer CLayer;
+#else
+typedef const PArgs CArgs;
+typedef const PLayer CLayer;
+#endif
+__device__ __forceinline__ CArgs* opaque_args(CArgs* p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+// Waits until every vector memory operation of this wave has completed.
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Workgroup barrier; LDS writes are complete first.  Bulk loads stay in flight.
+__device__ __forceinline__ void wg_sync() { __syncthreads(); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, kW3);
+}
+__device__ __forceinline__ f32x4 ld4_sc(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
+}
+__device__ __forceinline__ f32x4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float dot2(uint32_t p, uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, p), __builtin_bit_cast(half2_t, x), acc,
+                                  false);
+}
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, half2_t{(_Float16)a, (_Float16)b});
+}
+
+// LDS byte offset of the pair-table entry addressed by the 12-bit field at
+// bit B of a 96-bit chunk, OR-ed with the table base tb.
+template <int B>
+__device__ __forceinline__ uint32_t pair_addr(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t tb) {
+    uint32_t v;
+    if constexpr (B == 0) {
+        v = w0 << 2;
+    } else {
+        constexpr int s = B - 2, d = s >> 5, sh = s & 31;
+        const uint32_t lo = d == 0 ? w0 : (d == 1 ? w1 : w2);
+        const uint32_t hi = d == 0 ? w1 : w2;
+        v = (sh + 14 <= 32) ? (lo >> sh) : __builtin_amdgcn_alignbit(hi, lo, sh);
+    }
+    return (v & 0x3FFCu) | tb;
+}
+__device__ __forceinline__ uint32_t lds_u32(const char* base, uint32_t off) {
+    return *reinterpret_cast<const uint32_t*>(base + off);
+}
+__device__ __forceinline__ float chunk_dot(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1,
+                                           uint32_t w2, const uint32_t (&xh)[8]) {
+    uint32_t p[8];
+    p[0] = lds_u32(lds, pair_addr<0>(w0, w1, w2, tb));
+    p[1] = lds_u32(lds, pair_addr<12>(w0, w1, w2, tb));
+    p[2] = lds_u32(lds, pair_addr<24>(w0, w1, w2, tb));
+    p[3] = lds_u32(lds, pair_addr<36>(w0, w1, w2, tb));
+    p[4] = lds_u32(lds, pair_addr<48>(w0, w1, w2, tb));
+    p[5] = lds_u32(lds, pair_addr<60>(w0, w1, w2, tb));
+    p[6] = lds_u32(lds, pair_addr<72>(w0, w1, w2, tb));
+    p[7] = lds_u32(lds, pair_addr<84>(w0, w1, w2, tb));
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+        a0 = dot2(p[k], xh[k], a0);
+        a1 = dot2(p[k + 1], xh[k + 1], a1);
+    }
+    return a0 + a1;
+}
+
+// ----------------------------------------------------------------- barrier
+__device__ void bar_arrive(unsigned* sync, int p) {
+    const unsigned G = gridDim.x, g = blockIdx.x % kNG;
+    const unsigned n_in_g = (G - g + kNG - 1) / kNG;
+    if (add_sc(sync + kGrpOff + ((long)p * kNG + g) * kPad, 1u) == n_in_g - 1u) {
+        if (add_sc(sync + kRootOff + (long)p * kPad, 1u) == (unsigned)kNG - 1u) {
+            for (int k = 0; k < kNG; k++) st_sc(sync + kRelOff + ((long)p * kNG + k) * kPad, 1u);
+        }
+    }
+}
+__device__ bool bar_wait(unsigned* sync, int p) {
+    const unsigned* f = sync + kRelOff + ((long)p * kNG + (blockIdx.x % kNG)) * kPad;
+    for (int it = 0; it < kSpinLimit; it++) {
+        if (ld_sc(f)) return true;
+        if ((it & 255) == 255 && ld_sc(sync + kAbortOff)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    st_sc(sync + kAbortOff, 1u);
+    st_sc(sync + kStatusOff, 1u);
+    return false;
+}
+
+// Per-wave register buffer for a phase's bulk data (one type per phase kind,
+// so the allocator never has to merge buffers of different phases).
+template <int N>
+struct Buf {
+    uint32_t v[N];
+};
+
+// ====================================================================== GEMV
+// Rows [R0, R0 + nrows) of n_mat matrices sharing the input (gate+up, or down).
+// Compute wave w < n_mat*P: matrix mt = w / P, wave wl = w % P of that matrix;
+// lane index g = 64*wl + lane has chunk position pos = g % C on row offset
+// d = g / C of every instruction; instruction m covers rows R0 + RP*m + d.
+struct GemvGeo {
+    int C, P, RP, R0, nrows, g0, ng;
+};
+
+__device__ __forceinline__ GemvGeo gemv_geo(int C, int P, int RP, int rows_per_wg, int N) {
+    GemvGeo q;
+    q.C = C;
+    q.P = P;
+    q.RP = RP;
+    q.R0 = blockIdx.x * rows_per_wg;
+    q.nrows = max(0, min(rows_per_wg, N - q.R0));
+    q.g0 = q.R0 >> 5;
+    q.ng = q.nrows > 0 ? ((q.R0 + q.nrows - 1) >> 5) - q.g0 + 1 : 0;
+    return q;
+}
+
+// Issues the LUT loads and the weight stream of this wave, then builds the
+// pair tables (after the LUT values arrive; the weights stay in flight).
+template <int NI>
+__device__ __forceinline__ void gemv_prefetch(Buf<3 * NI>& b, const GemvGeo& q, const uint8_t* const (&W)[2],
+                                              const uint16_t* const (&LUT)[2], int n_mat, int wave,
+                                              int lane, char* lds) {
+    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    const int mt = wave / q.P, wl = wave - mt * q.P;
+    const uint16_t* lut = mt ? LUT[1] : LUT[0];
+    uint32_t lv0 = 0u, lv1 = 0u, lv2 = 0u;
+    lv0 = lut[(size_t)q.g0 * 64 + lane];
+    if (q.ng > 1) lv1 = lut[(size_t)(q.g0 + 1) * 64 + lane];
+    if (q.ng > 2) lv2 = lut[(size_t)(q.g0 + 2) * 64 + lane];
+    const uint8_t* Wt = (mt ? W[1] : W[0]) + (size_t)q.R0 * q.C * 12;
+    const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
+    const int voff = (wl * 64 + lane) * 12;
+#pragma unroll
+    for (int m = 0; m < NI; m++) {
+        const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, m * q.P * 768, 0);
+        b.v[3 * m] = t.x;
+        b.v[3 * m + 1] = t.y;
+        b.v[3 * m + 2] = t.z;
+    }
+    // pair tables (mt*3 + gi): rows i1 = wl, wl + P, ... of 64
+    for (int gi = 0; gi < q.ng; gi++) {
+        const uint32_t mine = gi == 0 ? lv0 : (gi == 1 ? lv1 : lv2);
+        char* tab = lds + kLdsTab + (mt * 3 + gi) * 16384;
+        for (int i1 = wl; i1 < 64; i1 += q.P) {
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)mine, i1);
+            *reinterpret_cast<uint32_t*>(tab + i1 * 256 + lane * 4) = mine | (hi << 16);
+        }
+    }
+}
+
+// Sums 8 values over each 32-lane half: afterwards lane li (li < 8) of each
+// half holds the half's total of value li in v[0].
+// After the transpose, lanes li and li ^ 8 hold the same value index, so the
+// last two stages need exact XOR partners (a row mirror would pair value li
+// with value 7 - li): lane ^ 8 is DPP row_ror:8 within 16 lanes, lane ^ 16 the
+// swizzle of partner<16>.
+__device__ __forceinline__ void half_sum8(float (&v)[8], int lane) {
+    transpose_reduce<8, 8>(v, lane & 7);
+    v[0] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[0]), 0x128, 0xF, 0xF, false));
+    v[0] += partner<16>(v[0]);
+}
+
+// Compute waves: dot products of the prefetched rows against the staged fp16
+// x pairs; per-half-wave row sums into LDS red[mt][m][hw] (hw = half-wave of
+// the matrix's waves), reduced 8 instructions at a time.
+template <int NI>
+__device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const GemvGeo& q, int n_mat, int wave,
+                                             int lane, char* lds) {
+    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    const int mt = wave / q.P, wl = wave - mt * q.P;
+    const int g = 64 * wl + lane;
+    const int pos = g % q.C;
+    const uint32_t* xs = reinterpret_cast<const uint32_t*>(lds + kLdsXs);
+    uint32_t xh[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) xh[k] = xs[k * q.C + pos];
+    float* red = reinterpret_cast<float*>(lds + kLdsMisc);
+    const int hw = wl * 2 + (lane >> 5);
+#pragma unroll
+    for (int m0 = 0; m0 < NI; m0 += 8) {
+        float part[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int m = m0 + j;
+            if (m < NI) {
+                const int gi = ((q.R0 + q.RP * m) >> 5) - q.g0;
+                const uint32_t tb = (uint32_t)(kLdsTab + (mt * 3 + gi) * 16384);
+                part[j] = chunk_dot(lds, tb, b.v[3 * m], b.v[3 * m + 1], b.v[3 * m + 2], xh);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                part[j] = 0.f;
+            }
+        }
+        half_sum8(part, lane);
+        const int li = lane & 31;
+        if (li < 8 && m0 + li < NI) red[(mt * NI + m0 + li) * 32 + hw] = part[0];
+        // keep the scheduler from hoisting later chunks' lookups (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Control wave: row total of (mt, row r of the workgroup) from the half-wave sums.
+template <int NI>
+__device__ __forceinline__ float gemv_row_sum(const GemvGeo& q, int mt, int r, const char* lds) {
+    const float* red = reinterpret_cast<const float*>(lds + kLdsMisc);
+    const int m = r / q.RP, d = r - m * q.RP;
+    const int per = q.C / 32;               // half-waves per row offset
+    float s = 0.f;
+    for (int hw = d * per; hw < (d + 1) * per; hw++) s += red[(mt * NI + m) * 32 + hw];
+    return s;
+}
+
+// Control wave: stages an input vector (fp32, n floats, n % 256 == 0) as fp16
+// pairs xs[k*C + chunk] into LDS; optional RMSNorm with weight nw (already
+// loaded per lane in nwv).  Reads the vector with device-coherent loads.
+template <int J>
+__device__ __forceinline__ void stage_vec(const float* v, int n, int C, bool norm, const f32x4 (&nwv)[J],
+                                          float eps, int lane, char* lds) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(v, (uint32_t)(n * 4));
+    f32x4 xv[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) xv[j] = ld4_sc(r, (lane + 64 * j) * 16);
+    float inv = 1.0f;
+    if (norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; j++)
+            ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+        ss = wave_sum(ss);
+        inv = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int i0 = 4 * (lane + 64 * j);
+        if (i0 < n) {
+            f32x4 t = xv[j];
+            if (norm) {
+                t.x = (t.x * inv) * nwv[j].x;
+                t.y = (t.y * inv) * nwv[j].y;
+                t.z = (t.z * inv) * nwv[j].z;
+                t.w = (t.w * inv) * nwv[j].w;
+            }
+            const int c = i0 >> 4, k = (i0 & 15) >> 1;
+            xs[k * C + c] = pack_h2(t.x, t.y);
+            xs[(k + 1) * C + c] = pack_h2(t.z, t.w);
+        }
+    }
+}
+
+// ================================================================ attention
+// Workgroup (kv head kvh = wg / splits, split s = wg % splits) over keys
+// [s*kps, s*kps + kps) of the ring.  Key slot t = hw + 20 j (hw = half-wave
+// 0..19 of the 10 compute waves, j < NKJ); each lane covers 8 dims (16 bytes)
+// of its keys.  K rows go straight to LDS (buffer loads with an LDS
+// destination: 1 KiB per wave instruction, rows t = 2w + 20j and 2w + 20j + 1);
+// V chunks go to registers.  Keys past the ring length load as zeros
+// (out-of-range buffer offsets).
+constexpr int kAkOff = kLdsTab;                        // K rows [20*NKJ][256] fp16
+
+template <int NKJ>
+__device__ __forceinline__ void attn_prefetch(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, int wave,
+                                              int lane, char* lds) {
+    if (wave >= kCW) return;
+    const int wg = blockIdx.x;
+    const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
+    if (kvh >= a.Hkv) return;
+    const int hw = wave * 2 + (lane >> 5), dl = lane & 31;
+    const int t0 = sp * a.kps;
+    const uint32_t bytes = (uint32_t)a.cap * a.Hkv * kAttnD * 2;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(L.k_cache, bytes), rv = rsrc(L.v_cache, bytes);
+#pragma unroll
+    for (int j = 0; j < NKJ; j++) {
+        const int t = hw + 20 * j;
+        const int tg = t0 + t;
+        int off = (int)bytes;   // out of range: loads zeros
+        if (t < a.kps && tg < L.ring_len) {
+            int phys = L.ring_start + tg;
+            if (phys >= a.cap) phys -= a.cap;
+            off = ((phys * a.Hkv + kvh) * kAttnD + dl * 8) * 2;
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (__attribute__((address_space(3))) void*)(lds + kAkOff + (wave * 2 + 20 * j) * 512), 16, off,
+            0, 0, 0);
+        const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+        b.v[4 * j] = vv.x; b.v[4 * j + 1] = vv.y; b.v[4 * j + 2] = vv.z; b.v[4 * j + 3] = vv.w;
+    }
+}
+
+// LDS (attention): q_s [4][256] f32 at kLdsMisc; kn/vn fp16 [256] each after it;
+// scores/probabilities [4][kps<=160] and (m, l)[4]; per-wave output sums
+// [10][4][256] f32 in the (idle) table region.
+constexpr int kAqOff = kLdsMisc;                       // 4 KiB
+constexpr int kAknOff = kAqOff + 4096;                 // 512 B
+constexpr int kAvnOff = kAknOff + 512;                 // 512 B
+constexpr int kAscOff = kAvnOff + 512;                 // 4*160*4 = 2560 B
+constexpr int kAmlOff = kAscOff + 2560;                // 32 B
+constexpr int kAflagOff = kAmlOff + 64;                // ints
+constexpr int kAredOff = kLdsTab;                      // 40 KiB
+
+__device__ __forceinline__ float h16(uint32_t w, int hi) {
+    return (float)__builtin_bit_cast(half2_t, w)[hi];
+}
+
+// Control wave: q norm + RoPE for the kv head's 4 q heads; if this split holds
+// the newest key, k norm + RoPE and the fp16 ring append of k and v.
+__device__ void attn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
+    const int wg = blockIdx.x;
+    const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
+    int* flags = reinterpret_cast<int*>(lds + kAflagOff);
+    if (kvh >= a.Hkv) return;
+    const int t_new = L.ring_len - 1 - sp * a.kps;          // local index of the newest key
+    const bool owner = t_new >= 0 && t_new < a.kps;
+    if (lane == 0) flags[0] = owner ? t_new : -1;
+    float* qs = reinterpret_cast<float*>(lds + kAqOff);
+    const float* cs = L.rope;
+    const float* sn = L.rope + a.rot_pairs;
+    // rows: 4 q heads, then (owner) the new key
+    for (int row = 0; row < kAttnG + (owner ? 1 : 0); row++) {
+        const bool isk = row == kAttnG;
+        const float* src = isk ? L.k + (size_t)kvh * kAttnD
+                               : L.q_gate + (size_t)(kvh * kAttnG + row) * 2 * kAttnD;
+        const float* w = isk ? L.k_norm_w : L.q_norm_w;
+        float v[4];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = src[4 * lane + i];
+            ss += v[i] * v[i];
+        }
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)kAttnD + a.eps);
+        float* dst = isk ? reinterpret_cast<float*>(lds + kAscOff) : qs + row * kAttnD;  // k temp in sc
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[4 * lane + i] = (v[i] * inv) * w[4 * lane + i];
+        // RoPE pairs (core/cpu_ops.cpp:40-63): interleaved (2j, 2j+1) or half-split (j, j+rot/2)
+        for (int j = lane; j < a.rot_pairs; j += 64) {
+            const int i0 = a.rope_mode == 0 ? 2 * j : j;
+            const int i1 = a.rope_mode == 0 ? 2 * j + 1 : j + a.rot_pairs;
+            const float v0 = dst[i0], v1 = dst[i1];
+            float o0, o1;
+            rotate_pair(o0, o1, v0, v1, cs[j], sn[j]);
+            dst[i0] = o0;
+            dst[i1] = o1;
+        }
+        if (isk) {
+            // fp16 append of k and v (round to nearest even), kept in LDS for the owner lanes
+            uint16_t* kn = reinterpret_cast<uint16_t*>(lds + kAknOff);
+            uint16_t* vn = reinterpret_cast<uint16_t*>(lds + kAvnOff);
+            uint16_t* kc = L.k_cache + ((size_t)L.slot * a.Hkv + kvh) * kAttnD;
+            uint16_t* vc = L.v_cache + ((size_t)L.slot * a.Hkv + kvh) * kAttnD;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = 4 * lane + i;
+                const uint16_t kh = f2h(dst[d]);
+                const uint16_t vh = f2h(L.v[(size_t)kvh * kAttnD + d]);
+                kn[d] = kh;
+                vn[d] = vh;
+                kc[d] = kh;
+                vc[d] = vh;
+            }
+        }
+    }
+}
+
+// Attention core for one split; writes the split record (m, l, o[256]) per q head.
+template <int NKJ>
+__device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds,
+                             int layer) {
+    const int wg = blockIdx.x;
+    const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
+    const bool active = kvh < a.Hkv;
+    const int tid = wave * 64 + lane;
+    const int nk = active ? max(0, min(a.kps, L.ring_len - sp * a.kps)) : 0;
+    const int* flags = reinterpret_cast<const int*>(lds + kAflagOff);
+    float* sc = reinterpret_cast<float*>(lds + kAscOff);          // [4][160]
+    float* ml = reinterpret_cast<float*>(lds + kAmlOff);          // m[4], l[4]
+    float* red = reinterpret_cast<float*>(lds + kAredOff);        // [10][4][256]
+    const float* qs = reinterpret_cast<const float*>(lds + kAqOff);
+    const int Lg = tid, hw = Lg >> 5, dl = Lg & 31;
+    // -- K rows (LDS) and V chunks (registers) of this wave have landed
+    vm_drain();
+    wg_sync();
+    // -- scores
+    if (active && wave < kCW) {
+        const int t_new = flags[0];
+        const uint32_t* kn = reinterpret_cast<const uint32_t*>(lds + kAknOff);
+        if (t_new >= 0) {   // the newest key was loaded before the append: use the staged row
+            const uint32_t* vn = reinterpret_cast<const uint32_t*>(lds + kAvnOff);
+#pragma unroll
+            for (int j = 0; j < NKJ; j++) {
+                if (hw + 20 * j == t_new) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) b.v[4 * j + i] = vn[dl * 4 + i];
+                }
+            }
+        }
+        float q[kAttnG][8];
+#pragma unroll
+        for (int g = 0; g < kAttnG; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[g][i] = qs[g * kAttnD + dl * 8 + i];
+#pragma unroll
+        for (int j0 = 0; j0 < NKJ; j0 += 2) {
+            float part[8];
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) {
+                const int j = j0 + jj;
+                const int t = hw + 20 * j;
+                u32x4 kr = {0u, 0u, 0u, 0u};
+                if (j < NKJ) {
+                    const uint32_t* src = t == t_new ? kn + dl * 4
+                                                     : reinterpret_cast<const uint32_t*>(lds + kAkOff + t * 512 + dl * 16);
+                    kr = *reinterpret_cast<const u32x4*>(src);
+                }
+                const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
+                float kf[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kf[2 * i] = h16(kw[i], 0);
+                    kf[2 * i + 1] = h16(kw[i], 1);
+                }
+#pragma unroll
+                for (int g = 0; g < kAttnG; g++) {
+                    float sdot = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sdot = fmaf(q[g][i], kf[i], sdot);
+                    part[jj * kAttnG + g] = sdot;
+                }
+            }
+            half_sum8(part, lane);   // lane li < 8: key slot j0 + li/4, head li%4
+            const int li = dl, j = j0 + (li >> 2), g = li & 3;
+            const int t = hw + 20 * j;
+            if (li < 8 && j < NKJ && t < nk) sc[g * 160 + t] = part[0] * a.scale;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wg_sync();
+    // -- softmax statistics per q head (waves 0..3)
+    if (active && wave < kAttnG) {
+        const int g = wave;
+        float m = -INFINITY;
+        for (int t = lane; t < nk; t += 64) m = fmaxf(m, sc[g * 160 + t]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int t = lane; t < nk; t += 64) {
+            const float e = __expf(sc[g * 160 + t] - m);
+            sc[g * 160 + t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            ml[g] = m;
+            ml[kAttnG + g] = l;
+        }
+    }
+    wg_sync();
+    // -- P V, reduced over the 20 half-waves
+    if (active && wave < kCW) {
+        float acc[kAttnG][8];
+#pragma unroll
+        for (int g = 0; g < kAttnG; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NKJ; j++) {
+            const int t = hw + 20 * j;
+            if (t < nk) {
+                float vf[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    vf[2 * i] = h16(b.v[4 * j + i], 0);
+                    vf[2 * i + 1] = h16(b.v[4 * j + i], 1);
+                }
+#pragma unroll
+                for (int g = 0; g < kAttnG; g++) {
+                    const float p = sc[g * 160 + t];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int g = 0; g < kAttnG; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[g][i] += shfl_xor(acc[g][i], 32);
+        if (lane < 32) {
+#pragma unroll
+            for (int g = 0; g < kAttnG; g++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) red[(wave * kAttnG + g) * kAttnD + dl * 8 + i] = acc[g][i];
+        }
+    }
+    wg_sync();
+    // -- split record: m, l, o[256] per q head (device-coherent stores)
+    if (active) {
+        const int rec = kAttnD + 2;
+        float* pr = a.part + ((size_t)kvh * a.splits + sp) * kAttnG * rec;
+        for (int e = tid; e < kAttnG * kAttnD; e += kNT) {
+            const int g = e / kAttnD, d = e - g * kAttnD;
+            float o = 0.f;
+#pragma unroll
+            for (int w = 0; w < kCW; w++) o += red[(w * kAttnG + g) * kAttnD + d];
+            stf_sc(pr + g * rec + 2 + d, o);
+        }
+        if (tid < kAttnG) {
+            stf_sc(pr + tid * rec, nk > 0 ? ml[tid] : -INFINITY);
+            stf_sc(pr + tid * rec + 1, nk > 0 ? ml[kAttnG + tid] : 0.f);
+        }
+    }
+    (void)layer;
+}
+
+// Log-sum-exp merge of N records (stride rstride floats, layout m, l, o[256]
+// per q head, 4 heads per record) into out_rec (same layout) or, when
+// `final`, the gated output.  All threads of the workgroup; every record value
+// a thread needs is loaded before the first is used (one round trip).
+template <int N>
+__device__ void attn_merge(const float* recs, int rstride, float* out_rec, bool final, const PLayer& L,
+                           int kvh, float* lds_m, int tid) {
+    static_assert(N <= 64, "one wave reduces the records of a head");
+    const int rec = kAttnD + 2;
+    // per head: M and the weights e^(m_s - M) in LDS
+    float* wgt = lds_m;                 // [4][64]
+    float* tot = lds_m + 4 * 64;        // M[4], Lsum[4]
+    if (tid < 64 * kAttnG) {
+        const int g = tid >> 6, s = tid & 63;
+        float m = -INFINITY, l = 0.f;
+        if (s < N) {
+            m = ldf_sc(recs + (size_t)s * rstride + g * rec);
+            l = ldf_sc(recs + (size_t)s * rstride + g * rec + 1);
+        }
+        const float M = wave_max(m);
+        const float w = (s < N && m != -INFINITY) ? __expf(m - M) : 0.f;
+        const float Ls = wave_sum(l * w);
+        wgt[g * 64 + s] = w;
+        if (s == 0) {
+            tot[g] = M;
+            tot[4 + g] = Ls;
+        }
+    }
+    __syncthreads();
+    constexpr int E = kAttnG * kAttnD;
+    constexpr int PER = (E + kNT - 1) / kNT;
+    float v[PER][N];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int e = min(tid + k * kNT, E - 1);
+        const int g = e / kAttnD, d = e - g * kAttnD;
+#pragma unroll
+        for (int s = 0; s < N; s++) v[k][s] = ldf_sc(recs + (size_t)s * rstride + g * rec + 2 + d);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int e = tid + k * kNT;
+        if (e >= E) continue;
+        const int g = e / kAttnD, d = e - g * kAttnD;
+        float o = 0.f;
+#pragma unroll
+        for (int s = 0; s < N; s++) o += wgt[g * 64 + s] * v[k][s];
+        if (final) {
+            const int hq = kvh * kAttnG + g;
+            float y = o / tot[4 + g];
+            y = y / (1.0f + expf(-L.q_gate[(size_t)hq * 2 * kAttnD + kAttnD + d]));
+            L.core_out[(size_t)hq * kAttnD + d] = y;
+        } else {
+            stf_sc(out_rec + g * rec + 2 + d, o);
+        }
+    }
+    if (!final && tid < kAttnG) {
+        stf_sc(out_rec + tid * rec, tot[tid]);
+        stf_sc(out_rec + tid * rec + 1, tot[4 + tid]);
+    }
+}
+
+// ================================================================= DeltaNet
+// Workgroup h < Hv owns value head h; compute waves 0..7 hold the state as
+// lane (column quad cq = L & 31, row chunk rc = L >> 5): rows 8rc..8rc+7,
+// columns 4cq..4cq+3.
+constexpr int kDnBuf = 32;
+__device__ __forceinline__ void dn_prefetch(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane) {
+    const int hd = blockIdx.x;
+    if (hd >= a.Hv || wave >= 8) return;
+    const int Lg = wave * 64 + lane, cq = Lg & 31, rc = Lg >> 5;
+    const __amdgpu_buffer_rsrc_t r = rsrc(L.state + (size_t)hd * kDnD * kDnD, kDnD * kDnD * 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, ((8 * rc + i) * kDnD + 4 * cq) * 4, 0, 0);
+        b.v[4 * i] = t.x; b.v[4 * i + 1] = t.y; b.v[4 * i + 2] = t.z; b.v[4 * i + 3] = t.w;
+    }
+}
+
+constexpr int kDqOff = kLdsMisc;            // q[128] k[128] v[128] beta decay ... z[128] nw[128]
+constexpr int kDredOff = kLdsMisc + 4096;   // [8][128] partials
+
+// Control wave: l2 norm of q, k (cpu_ops.cpp:82-87), q scale (qwen3_5.cpp:879-887),
+// beta and decay (qwen3_5.cpp:896-898); z and the gated-norm weight.
+__device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
+    const int hd = blockIdx.x;
+    if (hd >= a.Hv) return;
+    const int kh = hd / (a.Hv / a.Hk);
+    float* s = reinterpret_cast<float*>(lds + kDqOff);
+    float q0 = L.dn_q[(size_t)kh * kDnD + lane], q1 = L.dn_q[(size_t)kh * kDnD + 64 + lane];
+    float k0 = L.dn_k[(size_t)kh * kDnD + lane], k1 = L.dn_k[(size_t)kh * kDnD + 64 + lane];
+    if (L.dn_flags & ANELM_DN_L2NORM) {
+        const float sq = wave_sum(q0 * q0 + q1 * q1);
+        const float sk = wave_sum(k0 * k0 + k1 * k1);
+        const float iq = 1.0f / sqrtf(sq + 1e-12f), ik = 1.0f / sqrtf(sk + 1e-12f);
+        q0 = q0 * iq; q1 = q1 * iq; k0 = k0 * ik; k1 = k1 * ik;
+    }
+    const float qsc = 1.0f / sqrtf((float)kDnD);
+    s[lane] = q0 * qsc;
+    s[64 + lane] = q1 * qsc;
+    s[128 + lane] = k0;
+    s[192 + lane] = k1;
+    s[256 + lane] = L.dn_v[(size_t)hd * kDnD + lane];
+    s[320 + lane] = L.dn_v[(size_t)hd * kDnD + 64 + lane];
+    if (L.dn_flags & ANELM_DN_GATED_NORM) {
+        s[512 + lane] = L.dn_z[(size_t)hd * kDnD + lane];
+        s[576 + lane] = L.dn_z[(size_t)hd * kDnD + 64 + lane];
+        s[640 + lane] = L.dn_norm_w[lane];
+        s[704 + lane] = L.dn_norm_w[64 + lane];
+    }
+    if (lane == 0) {
+        const float beta = 1.0f / (1.0f + expf(-L.dn_b[hd]));
+        const float sp = logf(1.0f + expf(L.dn_a[hd] + L.dn_dt_bias[hd]));
+        s[384] = beta;
+        s[385] = expf(-L.dn_A[hd] * sp);
+    }
+}
+
+// Recurrence (core/cpu_ops.cpp:131-146, or the decay-first order) on the
+// register-held state, state write-back, and the output with the optional
+// gated RMSNorm (core/cpu_ops.cpp:32-38, models/llm/qwen3_5.cpp:902-908).
+__device__ void dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds) {
+    const int hd = blockIdx.x;
+    const bool active = hd < a.Hv;
+    const float* s = reinterpret_cast<const float*>(lds + kDqOff);
+    float* red = reinterpret_cast<float*>(lds + kDredOff);
+    const bool tf = (L.dn_flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
+    const int Lg = wave * 64 + lane, cq = Lg & 31, rc = Lg >> 5;
+    const bool holder = active && wave < 8;
+    float st[8][4];
+    float yp[4] = {0.f, 0.f, 0.f, 0.f};
+    float beta = 0.f, decay = 0.f;
+    if (holder) {
+        beta = s[384];
+        decay = s[385];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) st[i][c] = __builtin_bit_cast(float, b.v[4 * i + c]);
+        // Sk = S^T k over this lane's 8 rows (the decay-first order decays first)
+        float skp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float kr = s[128 + 8 * rc + i];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (tf) st[i][c] = decay * st[i][c];
+                skp[c] = fmaf(st[i][c], kr, skp[c]);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) skp[c] += shfl_xor(skp[c], 32);
+        if (lane < 32) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) red[wave * kDnD + 4 * cq + c] = skp[c];
+        }
+    }
+    wg_sync();
+    if (holder) {
+        float delta[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float sk = 0.f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) sk += red[w * kDnD + 4 * cq + c];
+            const float vj = s[256 + 4 * cq + c];
+            delta[c] = tf ? (vj - sk) * beta : vj - sk;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float kr = s[128 + 8 * rc + i], qr = s[8 * rc + i];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float n = tf ? fmaf(kr, delta[c], st[i][c]) : fmaf(beta * kr, delta[c], decay * st[i][c]);
+                st[i][c] = n;
+                yp[c] = fmaf(n, qr, yp[c]);
+            }
+        }
+        float* S = L.state + (size_t)hd * kDnD * kDnD;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            f32x4 o;
+            o.x = st[i][0]; o.y = st[i][1]; o.z = st[i][2]; o.w = st[i][3];
+            *reinterpret_cast<f32x4*>(S + (size_t)(8 * rc + i) * kDnD + 4 * cq) = o;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) yp[c] += shfl_xor(yp[c], 32);
+    }
+    wg_sync();   // Sk partials consumed
+    if (holder && lane < 32) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) red[wave * kDnD + 4 * cq + c] = yp[c];
+    }
+    wg_sync();
+    if (active && wave == kCtl) {
+        float y[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) t += red[w * kDnD + u * 64 + lane];
+            y[u] = t;
+        }
+        float* out = L.core_out + (size_t)hd * kDnD;
+        if (L.dn_flags & ANELM_DN_GATED_NORM) {
+            const float ss = wave_sum(y[0] * y[0] + y[1] * y[1]);
+            const float inv = 1.0f / sqrtf(ss / (float)kDnD + 1e-6f);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float zi = s[512 + u * 64 + lane];
+                float o = (y[u] * inv) * s[640 + u * 64 + lane];
+                o = o / (1.0f + expf(-zi));
+                out[u * 64 + lane] = o * zi;
+            }
+        } else {
+            out[lane] = y[0];
+            out[64 + lane] = y[1];
+        }
+    }
+}
+
+constexpr int kMergeOff = 131072;           // merge weights [4][64] + M[4], L[4]
+
+// Two-level split combine (all threads; after the split record is stored):
+// the last split of each group of 8 merges its group, the last group merges
+// the head and writes the gated output.  Counters are per (layer, kv head).
+__device__ void attn_combine(const PArgs& a, const PLayer& L, int layer, char* lds, int tid) {
+    const int wg = blockIdx.x;
+    const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
+    if (kvh >= a.Hkv) return;
+    int* ctl = reinterpret_cast<int*>(lds + kLdsCtl);
+    const int spg = a.splits / kSplitGroups, sg = sp / spg;
+    const int rec = kAttnG * (kAttnD + 2);
+    if (tid == 0) {
+        unsigned* gc = a.sync + kGcOff + (((long)layer * kMaxKvh + kvh) * kSplitGroups + sg) * kPad;
+        ctl[1] = add_sc(gc, 1u) == (unsigned)spg - 1u;
+    }
+    wg_sync();
+    if (!ctl[1]) return;
+    float* grec = a.gpart + ((size_t)kvh * kSplitGroups + sg) * rec;
+    attn_merge<kSplitsPerGroup>(a.part + ((size_t)kvh * a.splits + sg * spg) * rec, rec, grec, false, L, kvh,
+                                reinterpret_cast<float*>(lds + kMergeOff), tid);
+    vm_drain();
+    wg_sync();
+    if (tid == 0) {
+        unsigned* hc = a.sync + kHcOff + ((long)layer * kMaxKvh + kvh) * kPad;
+        ctl[2] = add_sc(hc, 1u) == (unsigned)kSplitGroups - 1u;
+    }
+    wg_sync();
+    if (!ctl[2]) return;
+    attn_merge<kSplitGroups>(a.gpart + (size_t)kvh * kSplitGroups * rec, rec, nullptr, true, L, kvh,
+                             reinterpret_cast<float*>(lds + kMergeOff), tid);
+    vm_drain();
+}
+
+// Control wave: x (fp32, coherent loads) and the FFN norm weight, 5 loads of
+// each per batch; x is parked in LDS (misc, fp32) and the weight in the upper
+// part of xs until the sum of squares is known, then RMSNorm
+// (core/cpu_ops.cpp:24-30) -> fp16 pairs into xs[k*C + chunk].
+template <int JH>
+__device__ __forceinline__ void stage_x(const PArgs& a, const float* nw, int C, int lane, char* lds) {
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)(a.H * 4));
+    const __amdgpu_buffer_rsrc_t rw = rsrc(nw, (uint32_t)(a.H * 4));
+    f32x4* xpark = reinterpret_cast<f32x4*>(lds + kLdsMisc);
+    f32x4* wpark = reinterpret_cast<f32x4*>(lds + kLdsXs + 8192);
+    constexpr int B = 5;
+    float ss = 0.f;
+#pragma unroll
+    for (int j0 = 0; j0 < JH; j0 += B) {
+        f32x4 xv[B], wv[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            if (j0 + j < JH) {
+                xv[j] = ld4_sc(rx, (lane + 64 * (j0 + j)) * 16);
+                wv[j] = ld4(rw, (lane + 64 * (j0 + j)) * 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            if (j0 + j < JH) {
+                ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+                xpark[lane + 64 * (j0 + j)] = xv[j];
+                wpark[lane + 64 * (j0 + j)] = wv[j];
+            }
+        }
+        cbar();
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
+#pragma unroll
+    for (int j = 0; j < JH; j++) {
+        const f32x4 xv = xpark[lane + 64 * j], wv = wpark[lane + 64 * j];
+        const int i0 = 4 * (lane + 64 * j);
+        const int c = i0 >> 4, k = (i0 & 15) >> 1;
+        xs[k * C + c] = pack_h2((xv.x * inv) * wv.x, (xv.y * inv) * wv.y);
+        xs[(k + 1) * C + c] = pack_h2((xv.z * inv) * wv.z, (xv.w * inv) * wv.w);
+    }
+}
+
+// Control wave: h as fp16 pairs (written by the gate/up epilogue) -> xs;
+// 4 pairs per load.
+template <int JI>
+__device__ __forceinline__ void stage_h(const PArgs& a, int C, int lane, char* lds) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(a.h, (uint32_t)(a.I * 2));
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
+    constexpr int B = 12;   // loads in flight per batch
+#pragma unroll
+    for (int j0 = 0; j0 < JI; j0 += B) {
+        u32x4 hv[B];
+#pragma unroll
+        for (int j = 0; j < B; j++)
+            if (j0 + j < JI) hv[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (lane + 64 * (j0 + j)) * 16, 0, kSc1);
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            if (j0 + j < JI) {
+                const int i0 = 4 * (lane + 64 * (j0 + j));   // pair index
+                const int c = i0 >> 3, k = i0 & 7;
+                xs[k * C + c] = hv[j].x;
+                xs[(k + 1) * C + c] = hv[j].y;
+                xs[(k + 2) * C + c] = hv[j].z;
+                xs[(k + 3) * C + c] = hv[j].w;
+            }
+        }
+        cbar();
+    }
+}
+
+__device__ __forceinline__ int* ctl_ints(char* lds) { return reinterpret_cast<int*>(lds + kLdsCtl); }
+
+// Control-wave end of a phase: arrive (after its stores) and, if another
+// phase follows, wait for the barrier.  Returns false on abort.
+__device__ __forceinline__ bool ctl_arrive_wait(const PArgs& a, int p, bool wait, int ln) {
+    vm_drain();
+    if (ln == 0) bar_arrive(a.sync, p);
+    if (!wait) return true;
+    int okw = 1;
+    if (ln == 0) okw = bar_wait(a.sync, p);
+    return __shfl(okw, 0, 64) != 0;
+}
+
+enum : int { kDN = 0, kATT = 1, kNONE = 2 };
+
+// One layer: core (KIND), gate/up, down; the end of the down phase prefetches
+// the next layer's core (NEXT).  core_buf holds this layer's prefetched core
+// data; next_buf receives the next layer's.  Returns false on abort.
+template <int KIND, int NEXT, int NIG, int NID, int NKJ, int JH, int JI, class BC, class BN>
+__device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& next_buf, int wave,
+                                          int lane, char* lds) {
+    CArgs* ap = opaque_args(pa);
+    const PArgs a = *ap;
+    CLayer* layers = (CLayer*)a.layers;
+    const PLayer L = layers[l];
+    int* ctl = ctl_ints(lds);
+    int ln = opaque(lane);
+    // ------------------------------------------------------------ core
+    if constexpr (KIND == kATT) {
+        attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
+        vm_drain();
+        wg_sync();
+        attn_combine(a, L, l, lds, wave * 64 + ln);
+    } else {
+        dn_compute(core_buf, a, L, wave, ln, lds);
+        vm_drain();
+    }
+    wg_sync();
+    const int p0 = 3 * l;
+    const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
+    Buf<3 * NIG> gb;
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        const int okw = ctl_arrive_wait(a, p0, true, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) stage_x<JH>(a, L.ffn_norm_w, gu.C, ln, lds);
+    } else {
+        const uint8_t* const W[2] = {L.w[0], L.w[1]};
+        const uint16_t* const LU[2] = {L.lut[0], L.lut[1]};
+        gemv_prefetch<NIG>(gb, gu, W, LU, 2, wave, ln, lds);
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    // --------------------------------------------------------- gate/up
+    ln = opaque(lane);
+    gemv_compute<NIG>(gb, gu, 2, wave, ln, lds);
+    wg_sync();
+    const GemvGeo dg = gemv_geo(a.d_C, a.d_P, a.d_RP, a.d_rows, a.H);
+    Buf<3 * NID> db;
+    float x_old = 0.f;
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        // h = silu(g) * u for this workgroup's rows, published as fp16 pairs
+        float hv = 0.f;
+        if (ln < gu.nrows) {
+            const float g = gemv_row_sum<NIG>(gu, 0, ln, lds);
+            const float u = gemv_row_sum<NIG>(gu, 1, ln, lds);
+            hv = (g / (1.0f + expf(-g))) * u;
+        }
+        const float hn = __shfl_down(hv, 1, 64);
+        if (ln < gu.nrows && (ln & 1) == 0)
+            st_sc(reinterpret_cast<unsigned*>(a.h) + ((gu.R0 + ln) >> 1), pack_h2(hv, hn));
+        const int okw = ctl_arrive_wait(a, p0 + 1, true, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            stage_h<JI>(a, dg.C, ln, lds);
+            if (ln < dg.nrows) x_old = ldf_sc(a.x + dg.R0 + ln);
+        }
+    } else {
+        const uint8_t* const W[2] = {L.w[2], L.w[2]};
+        const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
+        gemv_prefetch<NID>(db, dg, W, LU, 1, wave, ln, lds);
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    // ------------------------------------------------------------ down
+    ln = opaque(lane);
+    gemv_compute<NID>(db, dg, 1, wave, ln, lds);
+    wg_sync();
+    ln = opaque(lane);
+    constexpr bool more = NEXT != kNONE;
+    const PLayer Ln = layers[more ? l + 1 : l];
+    if (wave == kCtl) {
+        if (ln < dg.nrows) stf_sc(a.x + dg.R0 + ln, x_old + gemv_row_sum<NID>(dg, 0, ln, lds));
+        const int okw = ctl_arrive_wait(a, p0 + 2, more, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (more && okw) {
+            if constexpr (NEXT == kATT) attn_stage(a, Ln, ln, lds);
+            else dn_stage(a, Ln, ln, lds);
+        }
+    } else if constexpr (more) {
+        if constexpr (NEXT == kATT) attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
+        else dn_prefetch(next_buf, a, Ln, wave, ln);
+    }
+    if constexpr (more) {
+        wg_sync();
+        if (!ctl[0]) return false;
+    }
+    return true;
+}
+
+// NIG / NID: GEMV instructions per wave for gate/up and down; NKJ: key
+// slots per attention lane; JH = H/256, JI = I/512 (fp16 pairs / 4 per load).
+// Layer pattern: groups of 3 DeltaNet layers and 1 full-attention layer
+// (models/llm/qwen3_5.cpp:64-71: layer i is full attention iff (i+1) % 4 == 0).
+template <int NIG, int NID, int NKJ, int JH, int JI>
+__global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ gpa) {
+    CArgs* pa = (CArgs*)gpa;
+    const PArgs a = *pa;
+    const PLayer L0 = ((CLayer*)a.layers)[0];
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int* ctl = ctl_ints(lds);
+    Buf<kDnBuf> cdn;
+    Buf<4 * NKJ> cat;
+    // phase 0: core of layer 0 (inputs are ready at launch)
+    dn_prefetch(cdn, a, L0, wave, lane);
+    if (wave == kCtl) dn_stage(a, L0, lane, lds);
+    if (tid == 0) ctl[0] = 1;
+    wg_sync();
+    const int groups = a.n_layers / 4;
+    for (int gr = 0; gr < groups; gr++) {
+        const int l0 = 4 * gr;
+        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0, cdn, cdn, wave, lane, lds)) break;
+        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 1, cdn, cdn, wave, lane, lds)) break;
+        if (!run_layer<kDN, kATT, NIG, NID, NKJ, JH, JI>(pa, l0 + 2, cdn, cat, wave, lane, lds)) break;
+        if (gr + 1 < groups) {
+            if (!run_layer<kATT, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, wave, lane, lds)) break;
+        } else {
+            run_layer<kATT, kNONE, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, wave, lane, lds);
+        }
+    }
+    // ------------------------------------------------------------ finish
+    vm_drain();
+    wg_sync();
+    if (tid == 0) ctl[3] = add_sc(a.sync + kFinOff, 1u) == gridDim.x - 1u;
+    wg_sync();
+    if (ctl[3]) {
+        // last workgroup out: every other one has finished all sync accesses
+        const int np = 3 * a.n_layers;
+        for (int i = tid; i < np * (2 * kNG + 1); i += kNT) {
+            const int p = i / (2 * kNG + 1), k = i - p * (2 * kNG + 1);
+            if (k < kNG) st_sc(a.sync + kGrpOff + ((long)p * kNG + k) * kPad, 0u);
+            else if (k < 2 * kNG) st_sc(a.sync + kRelOff + ((long)p * kNG + (k - kNG)) * kPad, 0u);
+            else st_sc(a.sync + kRootOff + (long)p * kPad, 0u);
+        }
+        for (int i = tid; i < a.n_layers * kMaxKvh * (kSplitGroups + 1); i += kNT) {
+            const int lk = i / (kSplitGroups + 1), k = i - lk * (kSplitGroups + 1);
+            if (k < kSplitGroups) st_sc(a.sync + kGcOff + ((long)lk * kSplitGroups + k) * kPad, 0u);
+            else st_sc(a.sync + kHcOff + (long)lk * kPad, 0u);
+        }
+        if (tid == 0) {
+            st_sc(a.sync + kFinOff, 0u);
+            st_sc(a.sync + kAbortOff, 0u);
+        }
+        vm_drain();
+    }
+}
+
+}  // namespace pk
+}  // namespace anelm
+
+// ============================================================== host side
+namespace anelm {
+
+struct PersistentStep {
+    pk::PArgs args{};
+    std::vector<pk::PLayer> host_layers;
+    std::vector<int> pos;              // per layer (attention): position of the new token
+    std::vector<int> start, len;       // per layer ring state BEFORE the step
+    int cap = 0, rot = 0;
+    float theta = 0.f;
+    pk::PLayer* d_layers = nullptr;
+    pk::PArgs* d_args = nullptr;
+    float* d_rope = nullptr;           // [n_layers][rot] (cos rot/2, sin rot/2)
+    void (*kernel)(const pk::PArgs*) = nullptr;
+    int grid = 0;
+};
+
+namespace {
+
+template <int NIG, int NID, int NKJ, int JH, int JI>
+void* kernel_ptr() {
+    return reinterpret_cast<void*>(&pk::step_kernel<NIG, NID, NKJ, JH, JI>);
+}
+
+// Geometry of a LUT6 GEMV with in_dim K for the persistent kernel: C chunks
+// per row (multiple of 32), P waves per matrix, RP rows per instruction group.
+bool geo(int K, int& C, int& P, int& RP) {
+    if (K % 512 != 0) return false;
+    C = K / 16;
+    int gc = 64;
+    while (C % gc) gc >>= 1;
+    P = C / gc;
+    RP = 64 / gc;
+    return true;
+}
+
+// Fills the per-step ring fields (after the append) and RoPE rows.
+void plan_positions(PersistentStep* s, std::vector<float>& rope_host) {
+    const int n = (int)s->host_layers.size();
+    rope_host.assign((size_t)n * s->rot, 0.f);
+    for (int i = 0; i < n; i++) {
+        pk::PLayer& L = s->host_layers[i];
+        if (L.kind != ANELM_LAYER_ATTENTION) continue;
+        int start = s->start[i], len = s->len[i], slot;
+        if (len < s->cap) {
+            slot = start + len;
+            if (slot >= s->cap) slot -= s->cap;
+            len++;
+        } else {
+            slot = start;
+            start++;
+            if (start >= s->cap) start = 0;
+        }
+        L.ring_start = start;
+        L.ring_len = len;
+        L.slot = slot;
+        rope_row(&rope_host[(size_t)i * s->rot], &rope_host[(size_t)i * s->rot + s->rot / 2], s->rot,
+                 s->pos[i], s->theta);
+    }
+}
+
+int upload(PersistentStep* s, hipStream_t st) {
+    std::vector<float> rope;
+    plan_positions(s, rope);
+    ANELM_HIP(hipMemcpy(s->d_rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice));
+    ANELM_HIP(hipMemcpy(s->d_layers, s->host_layers.data(), s->host_layers.size() * sizeof(pk::PLayer),
+                        hipMemcpyHostToDevice));
+    (void)st;
+    return ANELM_OK;
+}
+
+}  // namespace
+
+void persistent_destroy(PersistentStep* s) {
+    if (!s) return;
+    if (s->d_layers) (void)hipFree(s->d_layers);
+    if (s->d_args) (void)hipFree(s->d_args);
+    if (s->d_rope) (void)hipFree(s->d_rope);
+    if (s->args.part) (void)hipFree(s->args.part);
+    if (s->args.gpart) (void)hipFree(s->args.gpart);
+    if (s->args.sync) (void)hipFree(s->args.sync);
+    delete s;
+}
+
+int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const anelm_hybrid_layer* layers,
+                      int n_layers, float* x, float* h, hipStream_t st) {
+    *out = nullptr;
+    Device* dev = device();
+    if (!dev) return ANELM_EHIP;
+    const int nwg = dev->num_cus;
+    int gC, gP, gRP, dC, dP, dRP;
+    ANELM_REQUIRE(n_layers >= 1 && n_layers <= pk::kMaxLayers, "persistent step: %d layers (max %d)",
+                  n_layers, pk::kMaxLayers);
+    ANELM_REQUIRE(geo(d->hidden, gC, gP, gRP) && geo(d->inter, dC, dP, dRP),
+                  "persistent step: hidden %d / inter %d must be multiples of 512", d->hidden, d->inter);
+    ANELM_REQUIRE(2 * gP <= pk::kCW && dP <= pk::kCW && dC <= 768,
+                  "persistent step: GEMV geometry (P %d, %d) exceeds the workgroup", gP, dP);
+    ANELM_REQUIRE(d->inter % nwg == 0 && d->hidden % nwg == 0,
+                  "persistent step: inter %d and hidden %d must divide over %d workgroups", d->inter,
+                  d->hidden, nwg);
+    const int gu_rows = d->inter / nwg, d_rows = d->hidden / nwg;
+    ANELM_REQUIRE(gu_rows % gRP == 0 && gu_rows % 2 == 0 && d_rows % dRP == 0 && gu_rows <= 64 && d_rows <= 64,
+                  "persistent step: rows per workgroup %d / %d do not fit the tile geometry", gu_rows, d_rows);
+    const int nig = gu_rows / gRP, nid = d_rows / dRP;
+    ANELM_REQUIRE(n_layers % 4 == 0, "persistent step: %d layers (groups of 4 needed)", n_layers);
+    for (int i = 0; i < n_layers; i++)
+        ANELM_REQUIRE(layers[i].kind == ((i + 1) % 4 == 0 ? ANELM_LAYER_ATTENTION : ANELM_LAYER_DELTANET),
+                      "persistent step: layer %d breaks the 3 DeltaNet : 1 attention pattern", i);
+    int n_attn = 0, cap = 0;
+    for (int i = 0; i < n_layers; i++) {
+        if (layers[i].kind == ANELM_LAYER_ATTENTION) {
+            n_attn++;
+            ANELM_REQUIRE(cap == 0 || layers[i].cache_capacity == cap,
+                          "persistent step: attention layers need one cache capacity");
+            cap = layers[i].cache_capacity;
+            ANELM_REQUIRE(layers[i].cache_len >= 0 && layers[i].cache_len <= cap && layers[i].cache_start >= 0 &&
+                              layers[i].cache_start < cap,
+                          "persistent step: layer %d ring inconsistent", i);
+        } else {
+            ANELM_REQUIRE((layers[i].dn_flags & ~7) == 0, "persistent step: layer %d flags 0x%x", i,
+                          layers[i].dn_flags);
+        }
+    }
+    int splits = 0, kps = 0, nkj = 0;
+    if (n_attn) {
+        ANELM_REQUIRE(d->head_dim == pk::kAttnD && d->n_heads == pk::kAttnG * d->n_kv_heads &&
+                          d->n_kv_heads <= pk::kMaxKvh && nwg % d->n_kv_heads == 0,
+                      "persistent step: attention needs head_dim 256 and 4 q heads per kv head");
+        splits = nwg / d->n_kv_heads;
+        ANELM_REQUIRE(splits == pk::kSplitGroups * pk::kSplitsPerGroup,
+                      "persistent step: %d splits per kv head", splits);
+        kps = (cap + splits - 1) / splits;
+        nkj = (kps + 19) / 20;
+        ANELM_REQUIRE(nkj <= 7, "persistent step: cache capacity %d beyond %d keys", cap, splits * 140);
+        ANELM_REQUIRE(d->rot_dim % 2 == 0 && d->rot_dim <= pk::kAttnD && d->rot_dim / 2 <= 64,
+                      "persistent step: rot_dim %d", d->rot_dim);
+        ANELM_REQUIRE(d->rope_mode == ANELM_ROPE_INTERLEAVED || d->rope_mode == ANELM_ROPE_HALF_SPLIT,
+                      "persistent step: rope_mode %d", d->rope_mode);
+    }
+    if (n_attn < n_layers) {
+        ANELM_REQUIRE(d->lin_dim == pk::kDnD && d->lin_v_heads <= nwg && d->lin_k_heads > 0 &&
+                          d->lin_v_heads % d->lin_k_heads == 0,
+                      "persistent step: DeltaNet needs 128-dim heads, Hv <= %d", nwg);
+    }
+    // Supported instantiation: the Qwen3.5-4B shape on a 256-CU device.
+    void* kp = nullptr;
+    const int jh = d->hidden / 256, ji = d->inter / 512;
+    if (nig == 18 && nid == 10 && jh == 10 && ji == 18 && (n_attn == 0 || nkj == 7))
+        kp = kernel_ptr<18, 10, 7, 10, 18>();
+    ANELM_REQUIRE(kp != nullptr,
+                  "persistent step: no kernel for this shape (gate/up %d, down %d instructions, %d key slots)",
+                  nig, nid, nkj);
+
+    auto* s = new PersistentStep();
+    s->cap = cap;
+    s->rot = d->rot_dim;
+    s->theta = d->theta;
+    s->grid = nwg;
+    s->kernel = reinterpret_cast<void (*)(const pk::PArgs*)>(kp);
+    s->host_layers.resize(n_layers);
+    s->pos.resize(n_layers);
+    s->start.resize(n_layers);
+    s->len.resize(n_layers);
+    hipError_t e = hipMalloc(&s->d_layers, sizeof(pk::PLayer) * n_layers);
+    if (e == hipSuccess) e = hipMalloc(&s->d_args, sizeof(pk::PArgs));
+    if (e == hipSuccess) e = hipMalloc(&s->d_rope, sizeof(float) * (size_t)n_layers * (s->rot > 0 ? s->rot : 2));
+    const size_t rec = (size_t)pk::kAttnG * (pk::kAttnD + 2);
+    if (e == hipSuccess) e = hipMalloc(&s->args.part, sizeof(float) * rec * (n_attn ? d->n_kv_heads * splits : 1));
+    if (e == hipSuccess) e = hipMalloc(&s->args.gpart, sizeof(float) * rec * (n_attn ? d->n_kv_heads * pk::kSplitGroups : 1));
+    if (e == hipSuccess) e = hipMalloc(&s->args.sync, sizeof(unsigned) * pk::kSyncWords);
+    if (e == hipSuccess) e = hipMemset(s->args.sync, 0, sizeof(unsigned) * pk::kSyncWords);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, pk::kLdsBytes);
+    // every workgroup must be resident at once (they wait on each other)
+    int per_cu = 0;
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kp, pk::kNT, pk::kLdsBytes);
+    if (e != hipSuccess) {
+        persistent_destroy(s);
+        return hip_fail(e, "persistent step setup");
+    }
+    if (per_cu < 1) {
+        persistent_destroy(s);
+        return set_error(ANELM_EINVAL, "persistent step: a workgroup does not fit one CU");
+    }
+    for (int i = 0; i < n_layers; i++) {
+        const anelm_hybrid_layer& S = layers[i];
+        pk::PLayer& L = s->host_layers[i];
+        memset(&L, 0, sizeof(L));
+        L.kind = S.kind;
+        L.q_gate = S.q_gate;
+        L.k = S.k;
+        L.v = S.v;
+        L.k_cache = S.k_cache;
+        L.v_cache = S.v_cache;
+        L.q_norm_w = S.q_norm_w;
+        L.k_norm_w = S.k_norm_w;
+        L.rope = s->d_rope + (size_t)i * s->rot;
+        L.state = S.state;
+        L.dn_q = S.dn_q;
+        L.dn_k = S.dn_k;
+        L.dn_v = S.dn_v;
+        L.dn_a = S.dn_a;
+        L.dn_b = S.dn_b;
+        L.dn_A = S.dn_A;
+        L.dn_dt_bias = S.dn_dt_bias;
+        L.dn_z = S.dn_z;
+        L.dn_norm_w = S.dn_norm_w;
+        L.dn_flags = S.dn_flags;
+        L.core_out = S.core_out;
+        L.ffn_norm_w = S.ffn_norm_w;
+        L.w[0] = S.gate_w;
+        L.w[1] = S.up_w;
+        L.w[2] = S.down_w;
+        L.lut[0] = S.gate_lut;
+        L.lut[1] = S.up_lut;
+        L.lut[2] = S.down_lut;
+        s->pos[i] = S.pos;
+        s->start[i] = S.cache_start;
+        s->len[i] = S.cache_len;
+    }
+    pk::PArgs& a = s->args;
+    a.layers = s->d_layers;
+    a.n_layers = n_layers;
+    a.x = x;
+    a.h = h;
+    a.H = d->hidden;
+    a.I = d->inter;
+    a.gu_C = gC;
+    a.gu_P = gP;
+    a.gu_RP = gRP;
+    a.gu_rows = gu_rows;
+    a.d_C = dC;
+    a.d_P = dP;
+    a.d_RP = dRP;
+    a.d_rows = d_rows;
+    a.Hkv = d->n_kv_heads;
+    a.splits = splits;
+    a.kps = kps;
+    a.rot_pairs = d->rot_dim / 2;
+    a.rope_mode = d->rope_mode;
+    a.cap = cap;
+    a.eps = d->eps;
+    a.scale = 1.0f / sqrtf((float)d->head_dim);
+    a.Hk = d->lin_k_heads;
+    a.Hv = d->lin_v_heads;
+    int rc = upload(s, st);
+    if (rc == ANELM_OK) {
+        const hipError_t e2 = hipMemcpy(s->d_args, &s->args, sizeof(pk::PArgs), hipMemcpyHostToDevice);
+        if (e2 != hipSuccess) rc = hip_fail(e2, "hipMemcpy(step args)");
+    }
+    if (rc) {
+        persistent_destroy(s);
+        return rc;
+    }
+    *out = s;
+    return ANELM_OK;
+}
+
+// One step.  With `advance`, every attention ring and position moves one
+// token forward afterwards (the host KVCache bookkeeping of qwen3_5.cpp:973-983)
+// and the descriptors are re-uploaded before the next launch.
+int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
+    hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st,
+                       (const pk::PArgs*)s->d_args);
+    ANELM_LAUNCHED("step_kernel");
+    if (advance) {
+        for (size_t i = 0; i < s->host_layers.size(); i++) {
+            if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) continue;
+            s->start[i] = s->host_layers[i].ring_start;
+            s->len[i] = s->host_layers[i].ring_len;
+            s->pos[i]++;
+        }
+        // the next launch may only see new descriptors after this one has read them
+        ANELM_HIP(hipStreamSynchronize(st));
+        return upload(s, st);
+    }
+    return ANELM_OK;
+}
+
+int persistent_status(PersistentStep* s, int* status) {
+    unsigned v = 0;
+    ANELM_HIP(hipMemcpy(&v, s->args.sync + pk::kStatusOff, sizeof(v), hipMemcpyDeviceToHost));
+    *status = (int)v;
+    if (v) {
+        const unsigned z = 0;
+        ANELM_HIP(hipMemcpy(s->args.sync + pk::kStatusOff, &z, sizeof(z), hipMemcpyHostToDevice));
+    }
+    return ANELM_OK;
+}
+
+}  // namespace anelm

@@ -10,7 +10,8 @@ Per step (models/llm/qwen3_5.cpp:1278-1356 with the projections left out):
     the gated-RMSNorm epilogue;
   * 32 LUT6 SwiGLU FFN blocks 2560 -> 9216 -> 2560 with RMSNorm and residual.
 Inputs are synthetic (seeded), resident in HBM before timing; the step runs as
-one HIP-graph replay.  Prints ONE JSON line.
+one persistent-kernel launch (falls back to a HIP-graph replay of the eager
+launch sequence where the persistent step does not fit).  Prints ONE JSON line.
 """
 from __future__ import annotations
 
@@ -29,6 +30,11 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "µs per decode step (attn+DeltaNet+LUT6, 4B shape); HBM GB/s as % of peak"
 HBM_PEAK_GBPS = 8000.0
+MODE_NAMES = {0: "eager launches", 1: "hip graph replay", 6: "persistent kernel, one launch per step"}
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled
+# by the factor a plain copy kernel of known size reads (filled in from the
+# committed profiles; None until measured)
+TRAFFIC = {}
 
 CFG = dict(hidden=2560, inter=9216, layers=32, n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64,
            theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=32, lin_dim=128, ctx=8192)
@@ -60,7 +66,7 @@ def gateup_bytes(c=CFG):
     return 2 * (I * H * 3 // 4 + (I // 32) * 64 * 2) + 2 * H * 4 + 2 * I * 4
 
 
-def build_step(anelm, torch, dev, seed=0, use_graph=True):
+def build_step(anelm, torch, dev, seed=0, mode=None):
     """Allocates the synthetic 4B-shaped model state and returns (step, keep, x)."""
     c = CFG
     g = torch.Generator(device=dev)
@@ -123,13 +129,20 @@ def build_step(anelm, torch, dev, seed=0, use_graph=True):
     keep.append({"x": x, "h": h})
     dims = anelm.HybridDims(H, I, Hq, Hkv, D, c["rot_dim"], 0, c["theta"], c["eps"], Hk, Hv, dl)
     torch.cuda.synchronize()
-    handle = ctypes.c_void_p()
     stream = torch.cuda.current_stream()
-    anelm.call("anelm_hybrid_step_create", ctypes.byref(handle), ctypes.byref(dims), layers,
-               c["layers"], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(h.data_ptr()),
-               1 if use_graph else 0, ctypes.c_void_p(stream.cuda_stream))
+    modes = [mode] if mode is not None else [anelm.STEP_PERSISTENT | anelm.STEP_STATIC, anelm.STEP_GRAPH]
+    for md in modes:
+        handle = ctypes.c_void_p()
+        rc = anelm.status("anelm_hybrid_step_create", ctypes.byref(handle), ctypes.byref(dims), layers,
+                          c["layers"], ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(h.data_ptr()), md,
+                          ctypes.c_void_p(stream.cuda_stream))
+        if rc == 0:
+            break
+        print(f"step mode {md} unavailable: {anelm.last_error()}", file=sys.stderr)
+    else:
+        raise RuntimeError("no decode-step mode could be created")
     keep.append((layers, dims))
-    return handle, keep, x
+    return handle, keep, x, md
 
 
 def time_gateup(anelm, torch, keep, n=50):
@@ -236,7 +249,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a graph replay")
+    ap.add_argument("--mode", choices=["persistent", "graph", "eager"], default=None,
+                    help="decode-step execution (default: persistent, else graph)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--skip-cpu", action="store_true")
     args = ap.parse_args()
@@ -252,7 +266,9 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        handle, keep, x = build_step(anelm, torch, dev, use_graph=not args.no_graph)
+        md = {"persistent": anelm.STEP_PERSISTENT | anelm.STEP_STATIC, "graph": anelm.STEP_GRAPH,
+              "eager": anelm.STEP_EAGER, None: None}[args.mode]
+        handle, keep, x, mode = build_step(anelm, torch, dev, mode=md)
         s = ctypes.c_void_p(stream.cuda_stream)
         for _ in range(args.warmup):
             anelm.call("anelm_hybrid_step_run", handle, s)
@@ -269,8 +285,12 @@ def main():
         ms_total = e0.elapsed_time(e1)
         us_step = ms_total * 1e3 / args.steps
         assert torch.isfinite(x).all(), "non-finite hidden state"
+        st = ctypes.c_int(0)
+        anelm.call("anelm_hybrid_step_status", handle, ctypes.byref(st))
+        assert st.value == 0, "a grid barrier of the persistent step timed out"
         gu_avg, gu_med = time_gateup(anelm, torch, keep)
         anelm.call("anelm_hybrid_step_destroy", handle)
+        persistent = bool(mode & anelm.STEP_PERSISTENT)
 
     b = step_bytes()
     gbps = b["total"] / (us_step * 1e-6) / 1e9
@@ -294,17 +314,26 @@ def main():
                                "24 Gated-DeltaNet (16k/32v heads x128, fp32 state, gated norm), "
                                "32 LUT6 SwiGLU FFN 2560->9216->2560",
                    "batch": 1, "context": CFG["ctx"], "layers": CFG["layers"],
-                   "graph": not args.no_graph},
+                   "execution": MODE_NAMES.get(mode, str(mode))},
         "hbm_GBps": round(gbps, 1),
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes_per_step": b["total"],
         "wall_s": round(wall, 4),
-        "roofline": {"bound": "hbm", "kernel": "lut6_gemv_kernel (gate+up, 2 x 9216x2560)",
-                     "achieved": round(gu_gbps, 1),
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes_per_launch": gu_b, "avg_us": round(gu_avg, 3),
-                     "median_us": round(gu_med, 3)},
     }
+    if persistent:
+        # one kernel per step: its launch duration is the step time (HIP events
+        # on the stream it runs on), its algorithmic bytes are the step's
+        result["roofline"] = {"bound": "hbm", "kernel": "step_kernel (whole 32-layer decode step)",
+                              "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                              "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC.get("step_kernel"),
+                              "bytes_per_launch": b["total"], "avg_us": round(us_step, 3)}
+    else:
+        result["roofline"] = {"bound": "hbm", "kernel": "lut6_tile_kernel (gate+up, 2 x 9216x2560)",
+                              "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                              "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                              "bytes_per_launch": gu_b, "avg_us": round(gu_avg, 3)}
+    result["lut6_gate_up"] = {"avg_us": round(gu_avg, 3), "median_us": round(gu_med, 3),
+                              "GBps": round(gu_gbps, 1), "bytes_per_launch": gu_b}
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result))

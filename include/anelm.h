@@ -276,17 +276,37 @@ typedef struct {
 
 typedef struct anelm_hybrid_step anelm_hybrid_step;
 
+/* Execution modes of a step (the `mode` argument):
+ *   ANELM_STEP_EAGER       one launch per kernel; each run advances every
+ *                          attention ring and position by one token, as the
+ *                          model's decode loop does;
+ *   ANELM_STEP_GRAPH       the eager launches captured once into a HIP graph on
+ *                          `stream` (not the null stream) after one warm-up
+ *                          run; each run replays the same work (rings do not
+ *                          advance);
+ *   ANELM_STEP_PERSISTENT  the whole step as ONE kernel launch (one workgroup
+ *                          per compute unit, grid barriers between the
+ *                          layers' phases); advances rings like EAGER, or
+ *                          replays like GRAPH when combined with
+ *                          ANELM_STEP_STATIC.  Supported for hidden/inter
+ *                          sizes that tile over the device's compute units
+ *                          (the Qwen3.5-4B shape on 256 CUs); other shapes
+ *                          return ANELM_EINVAL from create. */
+#define ANELM_STEP_EAGER 0
+#define ANELM_STEP_GRAPH 1
+#define ANELM_STEP_PERSISTENT 2
+#define ANELM_STEP_STATIC 4
+
 /* Builds a step over n_layers descriptors (copied), x [hidden] and
- * h_scratch [2*inter] device buffers.  With use_graph, the step's launches are
- * captured once into a HIP graph on `stream` (which must not be the null
- * stream) after one eager warm-up run; each run then replays the same work
- * -- the attention rings do not advance between replays.  Without it, each
- * run launches eagerly and advances every attention ring and position by one
- * token, as the model's decode loop does. */
+ * h_scratch [2*inter] device buffers (the step's FFN scratch). */
 int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hybrid_dims* dims,
                              const anelm_hybrid_layer* layers, int n_layers, float* x,
-                             float* h_scratch, int use_graph, void* stream);
+                             float* h_scratch, int mode, void* stream);
 int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream);
+/* Synchronous: *status = 0 if every persistent run so far completed, 1 if a
+ * run gave up waiting at a grid barrier (its outputs are then invalid);
+ * clears the flag.  Always 0 for the eager and graph modes. */
+int anelm_hybrid_step_status(anelm_hybrid_step* step, int* status);
 int anelm_hybrid_step_destroy(anelm_hybrid_step* step);
 
 #ifdef __cplusplus

@@ -184,3 +184,85 @@ QWEN35_08B = dict(hidden=1024, inter=3584, layers=24, n_heads=8, n_kv_heads=2, h
 def layer_is_attention(i, interval=4):
     """models/llm/qwen3_5.cpp:64-71: layer i is full attention when (i+1) % interval == 0."""
     return (i + 1) % interval == 0
+
+
+# ------------------------------------------------- hybrid decode step model
+@dataclass
+class HybridModel:
+    """Seeded random-init weights and state of a Qwen3.5-shaped hybrid stack
+    (layer i is full attention iff (i+1) % 4 == 0), host copies in numpy."""
+    dims: dict
+    layers: list          # per layer dict of numpy arrays / ints
+    x: np.ndarray         # [hidden] fp32
+
+
+def hybrid_model(seed, n_layers, dims=QWEN35_4B, rings=None, cap=8192, lut_std=0.02):
+    """rings: per attention layer (start, len); default (0, 700).  Cached keys
+    and values are fp16 ~ N(0,1); weights as the benchmark describes."""
+    rng = np.random.default_rng(seed)
+    d = dims
+    H, I, D = d["hidden"], d["inter"], d["head_dim"]
+    Hq, Hkv, Hk, Hv, dl = d["n_heads"], d["n_kv_heads"], d["lin_k_heads"], d["lin_v_heads"], d["lin_dim"]
+    layers = []
+    n_attn = 0
+
+    def lut(rows):
+        return f16(lut_std * rng.standard_normal((rows // 32, 64)))
+
+    def lw(rows, cols):
+        return rng.integers(0, 256, (rows, cols * 3 // 4), dtype=np.uint8)
+
+    for i in range(n_layers):
+        L = {}
+        if layer_is_attention(i):
+            start, length = (rings[n_attn] if rings else (0, 700))
+            n_attn += 1
+            L["kind"] = 1
+            L["q_gate"] = rng.standard_normal((Hq, 2 * D)).astype(np.float32)
+            L["k"] = rng.standard_normal((Hkv, D)).astype(np.float32)
+            L["v"] = rng.standard_normal((Hkv, D)).astype(np.float32)
+            L["k_cache"] = f16(rng.standard_normal((cap, Hkv, D)))
+            L["v_cache"] = f16(rng.standard_normal((cap, Hkv, D)))
+            L["q_norm_w"] = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+            L["k_norm_w"] = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+            L["start"], L["len"], L["cap"], L["pos"] = start, length, cap, length
+        else:
+            dn = deltanet_case(int(rng.integers(1 << 30)), Hk=Hk, Hv=Hv, dk=dl, dv=dl)
+            L["kind"] = 0
+            L.update(state=dn.state, dn_q=dn.q, dn_k=dn.k, dn_v=dn.v, dn_a=dn.a, dn_b=dn.b,
+                     dn_A=dn.A, dn_dt_bias=dn.dt_bias, dn_z=dn.z, dn_norm_w=dn.norm_w)
+            L["dn_flags"] = 1 | 4
+        L["ffn_norm_w"] = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+        L["gate_w"], L["gate_lut"] = lw(I, H), lut(I)
+        L["up_w"], L["up_lut"] = lw(I, H), lut(I)
+        L["down_w"], L["down_lut"] = lw(H, I), lut(H)
+        layers.append(L)
+    return HybridModel(dict(d), layers, rng.standard_normal(H).astype(np.float32))
+
+
+def oracle_hybrid_step(orc, m: HybridModel):
+    """One decode step through the oracle (models/llm/qwen3_5.cpp:1278-1356 over
+    the cores): per layer the attention or DeltaNet core, then
+    x += lut6_ffn(rmsnorm(x)).  Updates m in place (x, states, caches, rings)
+    and returns the per-layer core outputs."""
+    d = m.dims
+    H, I, D = d["hidden"], d["inter"], d["head_dim"]
+    outs = []
+    for L in m.layers:
+        if L["kind"] == 1:
+            out, kc, vc, st, ln = orc.full_attn_decode(
+                L["q_gate"], L["k"], L["v"], L["k_cache"], L["v_cache"], L["q_norm_w"], L["k_norm_w"],
+                d["n_heads"], d["n_kv_heads"], D, d["rot_dim"], L["pos"], d["theta"], d["eps"], 0, True,
+                L["start"], L["len"], L["cap"])
+            L["k_cache"], L["v_cache"], L["start"], L["len"] = kc, vc, st, ln
+            L["pos"] += 1
+            outs.append(out.reshape(-1))
+        else:
+            y, S = orc.deltanet_decode(L["state"], L["dn_q"], L["dn_k"], L["dn_v"], L["dn_a"], L["dn_b"],
+                                       L["dn_A"], L["dn_dt_bias"], L["dn_flags"], L["dn_z"], L["dn_norm_w"])
+            L["state"] = S
+            outs.append(y.reshape(-1))
+        n = orc.rmsnorm(m.x, L["ffn_norm_w"], d["eps"])
+        m.x = (m.x + orc.lut6_ffn(n, (L["gate_w"], L["gate_lut"]), (L["up_w"], L["up_lut"]),
+                                  (L["down_w"], L["down_lut"]), H, I)).astype(np.float32)
+    return outs
