@@ -110,13 +110,16 @@ __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
 
 // RMSNorm (cpu_ops.cpp:24-30) + RoPE (cpu_ops.cpp:40-63) of one D-vector held
 // in shared memory, in place.  All threads participate.
+// A NULL weight skips the norm (callers whose q/k arrive normalised).
 template <int D>
 __device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p, float* red) {
-    float ss = 0.f;
-    for (int d = threadIdx.x; d < D; d += kNT) ss += row[d] * row[d];
-    ss = block_sum<kNT>(ss, red);
-    const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
-    for (int d = threadIdx.x; d < D; d += kNT) row[d] = (row[d] * inv) * w[d];
+    if (w != nullptr) {
+        float ss = 0.f;
+        for (int d = threadIdx.x; d < D; d += kNT) ss += row[d] * row[d];
+        ss = block_sum<kNT>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+        for (int d = threadIdx.x; d < D; d += kNT) row[d] = (row[d] * inv) * w[d];
+    }
     __syncthreads();
     for (int j = threadIdx.x; j < p.rot_pairs; j += kNT) {
         const int i0 = p.rope_mode == 0 ? 2 * j : j;
@@ -525,8 +528,8 @@ extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const flo
     ANELM_NONNULL(v);
     ANELM_NONNULL(k_cache);
     ANELM_NONNULL(v_cache);
-    ANELM_NONNULL(q_norm_w);
-    ANELM_NONNULL(k_norm_w);
+    ANELM_REQUIRE((q_norm_w == nullptr) == (k_norm_w == nullptr),
+                  "q_norm_w and k_norm_w must both be given or both be NULL");
     ANELM_NONNULL(cache_start);
     ANELM_NONNULL(cache_len);
     int rc = check_heads(n_heads, n_kv_heads, head_dim);

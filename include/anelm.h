@@ -111,6 +111,8 @@ int anelm_gqa_attention(float* out, const float* q, const void* k_cache, const v
  *   q_norm_w / k_norm_w (:952-959); RoPE (:961-971); fp16 ring append of k, v
  *   (:973-986); gqa_attention (:989-991); sigmoid output gate when `gate`
  *   (:993-1000).
+ * q_norm_w and k_norm_w may both be NULL: no q/k RMSNorm, for callers that
+ * receive normalised q/k (scripts/serve_hybrid.py:89-107 applies RoPE only).
  * q_gate [n_heads][2*head_dim], k/v [n_kv_heads][head_dim] are read only.
  * *cache_start / *cache_len are HOST ints advanced as the KVCache ring does.
  * cos_row/sin_row: HOST, as for anelm_apply_rope. */

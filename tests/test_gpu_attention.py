@@ -177,3 +177,26 @@ def test_prefill_4096_rows(anelm, orc, dev):
     got16 = widen(to_host(anelm.ops.attn_prefill(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev),
                                                  torch.float16)))
     assert_close(got16, got, what="fp16 output")
+
+
+def test_full_attn_decode_without_norms(anelm, orc, dev):
+    """q/k arriving normalised (scripts/serve_hybrid.py:89-107: half-split RoPE,
+    cache append, attention, sigmoid gate, no q/k RMSNorm): NULL norm weights,
+    checked against the oracle's RoPE, fp16 append and gqa_attention."""
+    c = attn_decode_case(321, n_heads=16, n_kv_heads=4, head_dim=256, cached=300, capacity=4096)
+    D, G = c.head_dim, c.n_heads
+    dk, dv = to_dev(c.k_cache, dev), to_dev(c.v_cache, dev)
+    ring = anelm.ops.KVRing(c.capacity, c.start, c.length)
+    out = anelm.ops.full_attn_decode(to_dev(c.q_gate, dev), to_dev(c.k, dev), to_dev(c.v, dev), dk, dv,
+                                     None, None, ring, G, c.n_kv_heads, D, c.rot_dim, c.pos, c.theta,
+                                     c.eps, rope_mode=1, gate=True)
+    q, k = orc.apply_rope(c.q_gate, c.k, G, c.n_kv_heads, D, 2 * D, D, c.rot_dim, c.pos, c.theta, mode=1)
+    slot = (c.start + c.length) % c.capacity
+    kc, vc = c.k_cache.copy(), c.v_cache.copy()
+    kc[slot], vc[slot] = f16(k), f16(c.v)
+    want = orc.gqa_attention(q, widen(kc), widen(vc), G, c.n_kv_heads, D, 2 * D, c.start, c.length + 1,
+                             c.capacity)
+    want = orc.mul_sigmoid(want, c.q_gate[:, D:])
+    assert (ring.start.value, ring.len.value) == (c.start, c.length + 1)
+    assert_close(to_host(out), want, what="decode without norms")
+    assert np.array_equal(to_host(dk)[slot], kc[slot]) and np.array_equal(to_host(dv)[slot], vc[slot])
