@@ -244,12 +244,22 @@ __device__ void bar_arrive(unsigned* sync, int p) {
         }
     }
 }
+// Scalar load that bypasses the scalar cache (glc): it takes the scalar path
+// to L2, not the vector-memory queue where this CU's bulk loads wait.
+__device__ __forceinline__ unsigned scalar_word(const unsigned* p) {
+    const unsigned long long pa = (unsigned long long)p;
+    const unsigned long long sa = ((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned)(pa >> 32)) << 32) |
+                                  (unsigned)__builtin_amdgcn_readfirstlane((unsigned)pa);
+    unsigned v;
+    asm volatile("s_load_dword %0, %1, 0x0 glc\n s_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(sa) : "memory");
+    return v;
+}
 __device__ bool bar_wait(unsigned* sync, int p) {
     const unsigned* f = sync + kRelOff + ((long)p * kNG + (blockIdx.x % kNG)) * kPad;
     for (int it = 0; it < kSpinLimit; it++) {
-        if (ld_sc(f)) return true;
-        if ((it & 255) == 255 && ld_sc(sync + kAbortOff)) return false;
-        __builtin_amdgcn_s_sleep(1);
+        if (scalar_word(f)) return true;
+        if ((it & 255) == 255 && scalar_word(sync + kAbortOff)) return false;
+        __builtin_amdgcn_s_sleep(2);
     }
     st_sc(sync + kAbortOff, 1u);
     st_sc(sync + kStatusOff, 1u);
@@ -1012,12 +1022,17 @@ __device__ __forceinline__ void stage_h(const PArgs& a, int C, int lane, char* l
 
 __device__ __forceinline__ int* ctl_ints(char* lds) { return reinterpret_cast<int*>(lds + kLdsCtl); }
 
-// Control-wave end of a phase: arrive (after its stores) and, if another
-// phase follows, wait for the barrier.  Returns false on abort.
-__device__ __forceinline__ bool ctl_arrive_wait(const PArgs& a, int p, bool wait, int ln) {
-    vm_drain();
+// Control wave: arrive at barrier p (after this wave's stores completed when
+// `drain`: the phase published data other workgroups read).  The arrival's
+// atomics complete before the caller releases the compute waves, so they are
+// not queued behind the next phase's bulk loads.
+__device__ __forceinline__ void ctl_arrive(const PArgs& a, int p, int ln, bool drain) {
+    if (drain) vm_drain();
     if (ln == 0) bar_arrive(a.sync, p);
-    if (!wait) return true;
+    vm_drain();
+}
+// Control wave: wait for barrier p.  Returns false on abort.
+__device__ __forceinline__ bool ctl_wait(const PArgs& a, int p, int ln) {
     int okw = 1;
     if (ln == 0) okw = bar_wait(a.sync, p);
     return __shfl(okw, 0, 64) != 0;
@@ -1045,15 +1060,17 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         attn_combine(a, L, l, lds, wave * 64 + ln);
     } else {
         dn_compute(core_buf, a, L, wave, ln, lds);
-        vm_drain();
     }
+    // core outputs and DeltaNet states are read after the launch only: no drain
     wg_sync();
     const int p0 = 3 * l;
+    if (wave == kCtl) ctl_arrive(a, p0, opaque(lane), false);
+    wg_sync();   // the bulk loads below queue behind the arrival
     const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
     Buf<3 * NIG> gb;
     ln = opaque(lane);
     if (wave == kCtl) {
-        const int okw = ctl_arrive_wait(a, p0, true, ln);
+        const int okw = ctl_wait(a, p0, ln);
         if (ln == 0) ctl[0] = okw;
         if (okw) stage_x<JH>(a, L.ffn_norm_w, gu.C, ln, lds);
     } else {
@@ -1082,7 +1099,12 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         const float hn = __shfl_down(hv, 1, 64);
         if (ln < gu.nrows && (ln & 1) == 0)
             st_sc(reinterpret_cast<unsigned*>(a.h) + ((gu.R0 + ln) >> 1), pack_h2(hv, hn));
-        const int okw = ctl_arrive_wait(a, p0 + 1, true, ln);
+        ctl_arrive(a, p0 + 1, ln, true);
+    }
+    wg_sync();   // the bulk loads below queue behind the arrival
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        const int okw = ctl_wait(a, p0 + 1, ln);
         if (ln == 0) ctl[0] = okw;
         if (okw) {
             stage_h<JI>(a, dg.C, ln, lds);
@@ -1092,6 +1114,10 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         const uint8_t* const W[2] = {L.w[2], L.w[2]};
         const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
         gemv_prefetch<NID>(db, dg, W, LU, 1, wave, ln, lds);
+        // the next DeltaNet layer's state (not produced by this launch) streams in
+        // during the down phase, so the core inputs staged after the barrier do
+        // not queue behind it
+        if constexpr (NEXT == kDN) dn_prefetch(next_buf, a, layers[l + 1], wave, ln);
     }
     wg_sync();
     if (!ctl[0]) return false;
@@ -1104,15 +1130,19 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     const PLayer Ln = layers[more ? l + 1 : l];
     if (wave == kCtl) {
         if (ln < dg.nrows) stf_sc(a.x + dg.R0 + ln, x_old + gemv_row_sum<NID>(dg, 0, ln, lds));
-        const int okw = ctl_arrive_wait(a, p0 + 2, more, ln);
+        ctl_arrive(a, p0 + 2, ln, true);
+    }
+    if constexpr (more) wg_sync();   // the bulk loads below queue behind the arrival
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        const int okw = more ? (int)ctl_wait(a, p0 + 2, ln) : 1;
         if (ln == 0) ctl[0] = okw;
         if (more && okw) {
             if constexpr (NEXT == kATT) attn_stage(a, Ln, ln, lds);
             else dn_stage(a, Ln, ln, lds);
         }
-    } else if constexpr (more) {
-        if constexpr (NEXT == kATT) attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
-        else dn_prefetch(next_buf, a, Ln, wave, ln);
+    } else if constexpr (NEXT == kATT) {
+        attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
     }
     if constexpr (more) {
         wg_sync();
