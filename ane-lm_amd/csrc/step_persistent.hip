@@ -51,6 +51,7 @@ constexpr int kCtl = kCW;             // control wave index
 constexpr int kW3 = 0x00020000;       // raw buffer descriptor word 3 (gfx9 class)
 constexpr int kSc1 = 16;              // buffer-load cache policy: device-scope coherent
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -121,6 +122,7 @@ struct PArgs {
     float* x;                         // [H]
     float* h;                         // [I]
     float* part;                      // [Hkv][splits][G][D+2]
+    float* dnss;                      // [Hv][8] DeltaNet slab sums of squares
     float* gpart;                     // [Hkv][8][G][D+2]
     unsigned* sync;
     int H, I;
@@ -294,14 +296,30 @@ __device__ __forceinline__ GemvGeo gemv_geo(int C, int P, int RP, int rows_per_w
     return q;
 }
 
-// Issues the LUT loads and the weight stream of this wave, then builds the
-// pair tables (after the LUT values arrive; the weights stay in flight).
-template <int NI>
+// Weight stream of this wave in two parts: PART 0 issues the LUT loads and
+// instructions m < NA, then builds the pair tables (after the LUT values
+// arrive; the weights stay in flight); PART 1 issues m >= NA.  Splitting lets
+// the phase's staging loads, issued between the parts, overtake half of the
+// stream.
+template <int NI, int NA, int PART>
 __device__ __forceinline__ void gemv_prefetch(Buf<3 * NI>& b, const GemvGeo& q, const uint8_t* const (&W)[2],
                                               const uint16_t* const (&LUT)[2], int n_mat, int wave,
                                               int lane, char* lds) {
     if (wave >= n_mat * q.P || q.nrows <= 0) return;
     const int mt = wave / q.P, wl = wave - mt * q.P;
+    if constexpr (PART == 1) {
+        const uint8_t* Wt = (mt ? W[1] : W[0]) + (size_t)q.R0 * q.C * 12;
+        const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
+        const int voff = (wl * 64 + lane) * 12;
+#pragma unroll
+        for (int m = NA; m < NI; m++) {
+            const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, m * q.P * 768, 0);
+            b.v[3 * m] = t.x;
+            b.v[3 * m + 1] = t.y;
+            b.v[3 * m + 2] = t.z;
+        }
+        return;
+    }
     const uint16_t* lut = mt ? LUT[1] : LUT[0];
     uint32_t lv0 = 0u, lv1 = 0u, lv2 = 0u;
     lv0 = lut[(size_t)q.g0 * 64 + lane];
@@ -311,7 +329,7 @@ __device__ __forceinline__ void gemv_prefetch(Buf<3 * NI>& b, const GemvGeo& q, 
     const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
     const int voff = (wl * 64 + lane) * 12;
 #pragma unroll
-    for (int m = 0; m < NI; m++) {
+    for (int m = 0; m < NA; m++) {
         const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, m * q.P * 768, 0);
         b.v[3 * m] = t.x;
         b.v[3 * m + 1] = t.y;
@@ -350,10 +368,9 @@ __device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const GemvGeo
     const int mt = wave / q.P, wl = wave - mt * q.P;
     const int g = 64 * wl + lane;
     const int pos = g % q.C;
-    const uint32_t* xs = reinterpret_cast<const uint32_t*>(lds + kLdsXs);
-    uint32_t xh[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) xh[k] = xs[k * q.C + pos];
+    const u32x4* xs = reinterpret_cast<const u32x4*>(lds + kLdsXs);
+    const u32x4 x0 = xs[2 * pos], x1 = xs[2 * pos + 1];
+    const uint32_t xh[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     float* red = reinterpret_cast<float*>(lds + kLdsMisc);
     const int hw = wl * 2 + (lane >> 5);
 #pragma unroll
@@ -388,44 +405,6 @@ __device__ __forceinline__ float gemv_row_sum(const GemvGeo& q, int mt, int r, c
     float s = 0.f;
     for (int hw = d * per; hw < (d + 1) * per; hw++) s += red[(mt * NI + m) * 32 + hw];
     return s;
-}
-
-// Control wave: stages an input vector (fp32, n floats, n % 256 == 0) as fp16
-// pairs xs[k*C + chunk] into LDS; optional RMSNorm with weight nw (already
-// loaded per lane in nwv).  Reads the vector with device-coherent loads.
-template <int J>
-__device__ __forceinline__ void stage_vec(const float* v, int n, int C, bool norm, const f32x4 (&nwv)[J],
-                                          float eps, int lane, char* lds) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(v, (uint32_t)(n * 4));
-    f32x4 xv[J];
-#pragma unroll
-    for (int j = 0; j < J; j++) xv[j] = ld4_sc(r, (lane + 64 * j) * 16);
-    float inv = 1.0f;
-    if (norm) {
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < J; j++)
-            ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-        ss = wave_sum(ss);
-        inv = 1.0f / sqrtf(ss / (float)n + eps);
-    }
-    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-        const int i0 = 4 * (lane + 64 * j);
-        if (i0 < n) {
-            f32x4 t = xv[j];
-            if (norm) {
-                t.x = (t.x * inv) * nwv[j].x;
-                t.y = (t.y * inv) * nwv[j].y;
-                t.z = (t.z * inv) * nwv[j].z;
-                t.w = (t.w * inv) * nwv[j].w;
-            }
-            const int c = i0 >> 4, k = (i0 & 15) >> 1;
-            xs[k * C + c] = pack_h2(t.x, t.y);
-            xs[(k + 1) * C + c] = pack_h2(t.z, t.w);
-        }
-    }
 }
 
 // ================================================================ attention
@@ -755,34 +734,36 @@ __device__ void attn_merge(const float* recs, int rstride, float* out_rec, bool 
 }
 
 // ================================================================= DeltaNet
-// Workgroup h < Hv owns value head h; compute waves 0..7 hold the state as
-// lane (column quad cq = L & 31, row chunk rc = L >> 5): rows 8rc..8rc+7,
-// columns 4cq..4cq+3.
-constexpr int kDnBuf = 32;
+// Eight workgroups per value head: workgroup w owns head hd = w / 8 and state
+// columns [16c, 16c + 16), c = w % 8 -- columns are independent in the
+// recurrence, so every workgroup moves the same 8 KB of state each way.
+// Compute waves 0..7 hold the slab as lane L = 64*wave + lane: row r = L >> 2,
+// columns 16c + 4*(L & 3) + 0..3.
+constexpr int kDnSlabs = 8;
+constexpr int kDnCols = kDnD / kDnSlabs;     // 16
+constexpr int kDnBuf = 4;
 __device__ __forceinline__ void dn_prefetch(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane) {
-    const int hd = blockIdx.x;
+    const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
     if (hd >= a.Hv || wave >= 8) return;
-    const int Lg = wave * 64 + lane, cq = Lg & 31, rc = Lg >> 5;
-    const __amdgpu_buffer_rsrc_t r = rsrc(L.state + (size_t)hd * kDnD * kDnD, kDnD * kDnD * 4);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, ((8 * rc + i) * kDnD + 4 * cq) * 4, 0, 0);
-        b.v[4 * i] = t.x; b.v[4 * i + 1] = t.y; b.v[4 * i + 2] = t.z; b.v[4 * i + 3] = t.w;
-    }
+    const int Lg = wave * 64 + lane, r = Lg >> 2, cq = Lg & 3;
+    const __amdgpu_buffer_rsrc_t rs = rsrc(L.state + (size_t)hd * kDnD * kDnD, kDnD * kDnD * 4);
+    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, (r * kDnD + kDnCols * c + 4 * cq) * 4, 0, 0);
+    b.v[0] = t.x; b.v[1] = t.y; b.v[2] = t.z; b.v[3] = t.w;
 }
 
-constexpr int kDqOff = kLdsMisc;            // q[128] k[128] v[128] beta decay ... z[128] nw[128]
-constexpr int kDredOff = kLdsMisc + 4096;   // [8][128] partials
+constexpr int kDqOff = kLdsMisc;            // q[128] k[128] v[16] ... beta decay at 384
+constexpr int kDredOff = kLdsMisc + 4096;   // [8][16] partials
 
 // Control wave: l2 norm of q, k (cpu_ops.cpp:82-87), q scale (qwen3_5.cpp:879-887),
-// beta and decay (qwen3_5.cpp:896-898); z and the gated-norm weight.
+// beta and decay (qwen3_5.cpp:896-898), and this slab's v columns.
 __device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
-    const int hd = blockIdx.x;
+    const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
     if (hd >= a.Hv) return;
     const int kh = hd / (a.Hv / a.Hk);
     float* s = reinterpret_cast<float*>(lds + kDqOff);
     float q0 = L.dn_q[(size_t)kh * kDnD + lane], q1 = L.dn_q[(size_t)kh * kDnD + 64 + lane];
     float k0 = L.dn_k[(size_t)kh * kDnD + lane], k1 = L.dn_k[(size_t)kh * kDnD + 64 + lane];
+    const float vj = lane < kDnCols ? L.dn_v[(size_t)hd * kDnD + kDnCols * c + lane] : 0.f;
     if (L.dn_flags & ANELM_DN_L2NORM) {
         const float sq = wave_sum(q0 * q0 + q1 * q1);
         const float sk = wave_sum(k0 * k0 + k1 * k1);
@@ -794,14 +775,7 @@ __device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
     s[64 + lane] = q1 * qsc;
     s[128 + lane] = k0;
     s[192 + lane] = k1;
-    s[256 + lane] = L.dn_v[(size_t)hd * kDnD + lane];
-    s[320 + lane] = L.dn_v[(size_t)hd * kDnD + 64 + lane];
-    if (L.dn_flags & ANELM_DN_GATED_NORM) {
-        s[512 + lane] = L.dn_z[(size_t)hd * kDnD + lane];
-        s[576 + lane] = L.dn_z[(size_t)hd * kDnD + 64 + lane];
-        s[640 + lane] = L.dn_norm_w[lane];
-        s[704 + lane] = L.dn_norm_w[64 + lane];
-    }
+    if (lane < kDnCols) s[256 + lane] = vj;
     if (lane == 0) {
         const float beta = 1.0f / (1.0f + expf(-L.dn_b[hd]));
         const float sp = logf(1.0f + expf(L.dn_a[hd] + L.dn_dt_bias[hd]));
@@ -810,106 +784,107 @@ __device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
     }
 }
 
+// Sum over the 16 lanes of a wave that share lane & 3 (the slab rows held by
+// the wave for one column quad).
+__device__ __forceinline__ float sum_rows16(float v) {
+    v += shfl_xor(v, 4);
+    v += shfl_xor(v, 8);
+    v += shfl_xor(v, 16);
+    v += shfl_xor(v, 32);
+    return v;
+}
+
 // Recurrence (core/cpu_ops.cpp:131-146, or the decay-first order) on the
-// register-held state, state write-back, and the output with the optional
-// gated RMSNorm (core/cpu_ops.cpp:32-38, models/llm/qwen3_5.cpp:902-908).
-__device__ void dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds) {
-    const int hd = blockIdx.x;
+// register-held slab, state write-back, and the slab's 16 outputs.  Without
+// the gated norm they go to core_out; with it the slab's sum of squares is
+// published (dnss) and the control wave returns y (lane j: column 16c + j)
+// for dn_finish after the next barrier.
+__device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds) {
+    const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
     const bool active = hd < a.Hv;
     const float* s = reinterpret_cast<const float*>(lds + kDqOff);
     float* red = reinterpret_cast<float*>(lds + kDredOff);
     const bool tf = (L.dn_flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
-    const int Lg = wave * 64 + lane, cq = Lg & 31, rc = Lg >> 5;
+    const int Lg = wave * 64 + lane, r = Lg >> 2, cq = Lg & 3;
     const bool holder = active && wave < 8;
-    float st[8][4];
+    float st[4] = {0.f, 0.f, 0.f, 0.f};
     float yp[4] = {0.f, 0.f, 0.f, 0.f};
-    float beta = 0.f, decay = 0.f;
+    float beta = 0.f, decay = 0.f, kr = 0.f;
     if (holder) {
         beta = s[384];
         decay = s[385];
+        kr = s[128 + r];
+        float skp[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) st[i][c] = __builtin_bit_cast(float, b.v[4 * i + c]);
-        // Sk = S^T k over this lane's 8 rows (the decay-first order decays first)
-        float skp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float kr = s[128 + 8 * rc + i];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                if (tf) st[i][c] = decay * st[i][c];
-                skp[c] = fmaf(st[i][c], kr, skp[c]);
-            }
+        for (int j = 0; j < 4; j++) {
+            st[j] = __builtin_bit_cast(float, b.v[j]);
+            if (tf) st[j] = decay * st[j];   // decay-first: Sk from the decayed state
+            skp[j] = sum_rows16(st[j] * kr);
         }
+        if (lane < 4) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) skp[c] += shfl_xor(skp[c], 32);
-        if (lane < 32) {
-#pragma unroll
-            for (int c = 0; c < 4; c++) red[wave * kDnD + 4 * cq + c] = skp[c];
+            for (int j = 0; j < 4; j++) red[wave * kDnCols + 4 * cq + j] = skp[j];
         }
     }
     wg_sync();
     if (holder) {
-        float delta[4];
+        const float qr = s[r];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int j = 0; j < 4; j++) {
             float sk = 0.f;
 #pragma unroll
-            for (int w = 0; w < 8; w++) sk += red[w * kDnD + 4 * cq + c];
-            const float vj = s[256 + 4 * cq + c];
-            delta[c] = tf ? (vj - sk) * beta : vj - sk;
+            for (int w = 0; w < 8; w++) sk += red[w * kDnCols + 4 * cq + j];
+            const float vj = s[256 + 4 * cq + j];
+            const float delta = tf ? (vj - sk) * beta : vj - sk;
+            const float n = tf ? fmaf(kr, delta, st[j]) : fmaf(beta * kr, delta, decay * st[j]);
+            st[j] = n;
+            yp[j] = sum_rows16(n * qr);
         }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float kr = s[128 + 8 * rc + i], qr = s[8 * rc + i];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const float n = tf ? fmaf(kr, delta[c], st[i][c]) : fmaf(beta * kr, delta[c], decay * st[i][c]);
-                st[i][c] = n;
-                yp[c] = fmaf(n, qr, yp[c]);
-            }
-        }
-        float* S = L.state + (size_t)hd * kDnD * kDnD;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            f32x4 o;
-            o.x = st[i][0]; o.y = st[i][1]; o.z = st[i][2]; o.w = st[i][3];
-            *reinterpret_cast<f32x4*>(S + (size_t)(8 * rc + i) * kDnD + 4 * cq) = o;
-        }
-#pragma unroll
-        for (int c = 0; c < 4; c++) yp[c] += shfl_xor(yp[c], 32);
+        f32x4 o;
+        o.x = st[0]; o.y = st[1]; o.z = st[2]; o.w = st[3];
+        *reinterpret_cast<f32x4*>(L.state + (size_t)hd * kDnD * kDnD + (size_t)r * kDnD + kDnCols * c + 4 * cq) = o;
     }
     wg_sync();   // Sk partials consumed
-    if (holder && lane < 32) {
+    if (holder && lane < 4) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) red[wave * kDnD + 4 * cq + c] = yp[c];
+        for (int j = 0; j < 4; j++) red[wave * kDnCols + 4 * cq + j] = yp[j];
     }
     wg_sync();
+    float y = 0.f;
     if (active && wave == kCtl) {
-        float y[2];
+        if (lane < kDnCols) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            float t = 0.f;
-#pragma unroll
-            for (int w = 0; w < 8; w++) t += red[w * kDnD + u * 64 + lane];
-            y[u] = t;
+            for (int w = 0; w < 8; w++) y += red[w * kDnCols + lane];
         }
-        float* out = L.core_out + (size_t)hd * kDnD;
         if (L.dn_flags & ANELM_DN_GATED_NORM) {
-            const float ss = wave_sum(y[0] * y[0] + y[1] * y[1]);
-            const float inv = 1.0f / sqrtf(ss / (float)kDnD + 1e-6f);
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const float zi = s[512 + u * 64 + lane];
-                float o = (y[u] * inv) * s[640 + u * 64 + lane];
-                o = o / (1.0f + expf(-zi));
-                out[u * 64 + lane] = o * zi;
-            }
-        } else {
-            out[lane] = y[0];
-            out[64 + lane] = y[1];
+            const float ss = wave_sum(lane < kDnCols ? y * y : 0.f);
+            if (lane == 0) stf_sc(a.dnss + hd * kDnSlabs + c, ss);
+        } else if (lane < kDnCols) {
+            L.core_out[(size_t)hd * kDnD + kDnCols * c + lane] = y;
         }
+    }
+    return y;
+}
+
+// Control wave, after the barrier that follows a gated DeltaNet core: the
+// head's sum of squares from its eight slabs, then rmsnorm_gated
+// (core/cpu_ops.cpp:32-38, qwen3_5.cpp:902-908, eps 1e-6) of this slab's 16
+// outputs y (lane j: column 16c + j).
+__device__ void dn_finish(const PArgs& a, const PLayer& L, float y, int lane) {
+    const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
+    if (hd >= a.Hv || !(L.dn_flags & ANELM_DN_GATED_NORM)) return;
+    const float part = lane < kDnSlabs ? ldf_sc(a.dnss + hd * kDnSlabs + lane) : 0.f;
+    float z = 0.f, w = 0.f;
+    if (lane < kDnCols) {
+        z = L.dn_z[(size_t)hd * kDnD + kDnCols * c + lane];
+        w = L.dn_norm_w[kDnCols * c + lane];
+    }
+    const float ss = wave_sum(part);
+    const float inv = 1.0f / sqrtf(ss / (float)kDnD + 1e-6f);
+    if (lane < kDnCols) {
+        float o = (y * inv) * w;
+        o = o / (1.0f + expf(-z));
+        L.core_out[(size_t)hd * kDnD + kDnCols * c + lane] = o * z;
     }
 }
 
@@ -947,77 +922,59 @@ __device__ void attn_combine(const PArgs& a, const PLayer& L, int layer, char* l
     vm_drain();
 }
 
-// Control wave: x (fp32, coherent loads) and the FFN norm weight, 5 loads of
-// each per batch; x is parked in LDS (misc, fp32) and the weight in the upper
-// part of xs until the sum of squares is known, then RMSNorm
-// (core/cpu_ops.cpp:24-30) -> fp16 pairs into xs[k*C + chunk].
+// Control wave: GEMV input staging.  LDS holds the input as fp16 pairs in
+// natural order (pair i = inputs 2i, 2i+1 at dword i of xs), so chunk `pos`
+// owns dwords 8*pos .. 8*pos + 7.  All staging loads go straight to LDS
+// (buffer loads with an LDS destination, 1 KiB per wave instruction), so no
+// registers are held while they are in flight.
+//   stage_w       FFN norm weight (a model constant), fp32 -> wpark, before the barrier;
+//   stage_x_load  x (fp32, device-coherent) -> xpark, after the barrier;
+//   stage_x_fin   RMSNorm (core/cpu_ops.cpp:24-30) of xpark * wpark -> fp16 pairs in xs;
+//   stage_h_load  h (already fp16 pairs, device-coherent) -> xs.
+constexpr int kWparkOff = kLdsXs + 8192;   // fp32 [H], above the input pairs of the gate/up GEMV
+constexpr int kXparkOff = kLdsMisc;        // fp32 [H]
+template <int J, int AUX>
+__device__ __forceinline__ void lds_fill(const void* src, uint32_t bytes, char* lds, int off, int lane) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(src, bytes);
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds + off + j * 1024),
+                                                 16, (lane + 64 * j) * 16, 0, 0, AUX);
+}
 template <int JH>
-__device__ __forceinline__ void stage_x(const PArgs& a, const float* nw, int C, int lane, char* lds) {
-    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)(a.H * 4));
-    const __amdgpu_buffer_rsrc_t rw = rsrc(nw, (uint32_t)(a.H * 4));
-    f32x4* xpark = reinterpret_cast<f32x4*>(lds + kLdsMisc);
-    f32x4* wpark = reinterpret_cast<f32x4*>(lds + kLdsXs + 8192);
-    constexpr int B = 5;
+__device__ __forceinline__ void stage_w(const PArgs& a, const float* nw, int lane, char* lds) {
+    lds_fill<JH, 0>(nw, (uint32_t)(a.H * 4), lds, kWparkOff, lane);
+}
+template <int JH>
+__device__ __forceinline__ void stage_x_load(const PArgs& a, int lane, char* lds) {
+    lds_fill<JH, kSc1>(a.x, (uint32_t)(a.H * 4), lds, kXparkOff, lane);
+}
+template <int JH>
+__device__ __forceinline__ void stage_x_fin(const PArgs& a, int lane, char* lds) {
+    vm_drain();   // xpark and wpark have landed
+    const f32x4* xpark = reinterpret_cast<const f32x4*>(lds + kXparkOff);
+    const f32x4* wpark = reinterpret_cast<const f32x4*>(lds + kWparkOff);
     float ss = 0.f;
 #pragma unroll
-    for (int j0 = 0; j0 < JH; j0 += B) {
-        f32x4 xv[B], wv[B];
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            if (j0 + j < JH) {
-                xv[j] = ld4_sc(rx, (lane + 64 * (j0 + j)) * 16);
-                wv[j] = ld4(rw, (lane + 64 * (j0 + j)) * 16);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            if (j0 + j < JH) {
-                ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-                xpark[lane + 64 * (j0 + j)] = xv[j];
-                wpark[lane + 64 * (j0 + j)] = wv[j];
-            }
-        }
-        cbar();
+    for (int j = 0; j < JH; j++) {
+        const f32x4 xv = xpark[lane + 64 * j];
+        ss += xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w;
     }
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)a.H + a.eps);
-    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
+    u32x2* xs = reinterpret_cast<u32x2*>(lds + kLdsXs);
 #pragma unroll
     for (int j = 0; j < JH; j++) {
         const f32x4 xv = xpark[lane + 64 * j], wv = wpark[lane + 64 * j];
-        const int i0 = 4 * (lane + 64 * j);
-        const int c = i0 >> 4, k = (i0 & 15) >> 1;
-        xs[k * C + c] = pack_h2((xv.x * inv) * wv.x, (xv.y * inv) * wv.y);
-        xs[(k + 1) * C + c] = pack_h2((xv.z * inv) * wv.z, (xv.w * inv) * wv.w);
+        u32x2 o;
+        o.x = pack_h2((xv.x * inv) * wv.x, (xv.y * inv) * wv.y);
+        o.y = pack_h2((xv.z * inv) * wv.z, (xv.w * inv) * wv.w);
+        xs[lane + 64 * j] = o;
     }
 }
-
-// Control wave: h as fp16 pairs (written by the gate/up epilogue) -> xs;
-// 4 pairs per load.
 template <int JI>
-__device__ __forceinline__ void stage_h(const PArgs& a, int C, int lane, char* lds) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(a.h, (uint32_t)(a.I * 2));
-    uint32_t* xs = reinterpret_cast<uint32_t*>(lds + kLdsXs);
-    constexpr int B = 12;   // loads in flight per batch
-#pragma unroll
-    for (int j0 = 0; j0 < JI; j0 += B) {
-        u32x4 hv[B];
-#pragma unroll
-        for (int j = 0; j < B; j++)
-            if (j0 + j < JI) hv[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (lane + 64 * (j0 + j)) * 16, 0, kSc1);
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            if (j0 + j < JI) {
-                const int i0 = 4 * (lane + 64 * (j0 + j));   // pair index
-                const int c = i0 >> 3, k = i0 & 7;
-                xs[k * C + c] = hv[j].x;
-                xs[(k + 1) * C + c] = hv[j].y;
-                xs[(k + 2) * C + c] = hv[j].z;
-                xs[(k + 3) * C + c] = hv[j].w;
-            }
-        }
-        cbar();
-    }
+__device__ __forceinline__ void stage_h_load(const PArgs& a, int lane, char* lds) {
+    lds_fill<JI, kSc1>(a.h, (uint32_t)(a.I * 2), lds, kLdsXs, lane);
 }
 
 __device__ __forceinline__ int* ctl_ints(char* lds) { return reinterpret_cast<int*>(lds + kLdsCtl); }
@@ -1052,6 +1009,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     const PLayer L = layers[l];
     int* ctl = ctl_ints(lds);
     int ln = opaque(lane);
+    float ydn = 0.f;
     // ------------------------------------------------------------ core
     if constexpr (KIND == kATT) {
         attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
@@ -1059,30 +1017,50 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         wg_sync();
         attn_combine(a, L, l, lds, wave * 64 + ln);
     } else {
-        dn_compute(core_buf, a, L, wave, ln, lds);
+        ydn = dn_compute(core_buf, a, L, wave, ln, lds);
     }
-    // core outputs and DeltaNet states are read after the launch only: no drain
+    // core outputs and DeltaNet states are read after the launch only; the
+    // DeltaNet slab sums of squares are read after the barrier
     wg_sync();
     const int p0 = 3 * l;
-    if (wave == kCtl) ctl_arrive(a, p0, opaque(lane), false);
+    if (wave == kCtl) {
+        ln = opaque(lane);
+        ctl_arrive(a, p0, ln, KIND == kDN);
+        stage_w<JH>(a, L.ffn_norm_w, ln, lds);
+    }
     wg_sync();   // the bulk loads below queue behind the arrival
     const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
     Buf<3 * NIG> gb;
+    constexpr int NAG = NIG / 2;
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0, ln);
         if (ln == 0) ctl[0] = okw;
-        if (okw) stage_x<JH>(a, L.ffn_norm_w, gu.C, ln, lds);
+        if (okw) stage_x_load<JH>(a, ln, lds);
     } else {
         const uint8_t* const W[2] = {L.w[0], L.w[1]};
         const uint16_t* const LU[2] = {L.lut[0], L.lut[1]};
-        gemv_prefetch<NIG>(gb, gu, W, LU, 2, wave, ln, lds);
+        gemv_prefetch<NIG, NAG, 0>(gb, gu, W, LU, 2, wave, ln, lds);
+    }
+    wg_sync();   // the x loads were issued ahead of the second half of the weights
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        if (ctl[0]) stage_x_fin<JH>(a, ln, lds);
+    } else {
+        const uint8_t* const W[2] = {L.w[0], L.w[1]};
+        const uint16_t* const LU[2] = {L.lut[0], L.lut[1]};
+        gemv_prefetch<NIG, NAG, 1>(gb, gu, W, LU, 2, wave, ln, lds);
     }
     wg_sync();
     if (!ctl[0]) return false;
     // --------------------------------------------------------- gate/up
     ln = opaque(lane);
     gemv_compute<NIG>(gb, gu, 2, wave, ln, lds);
+    // the control wave is idle during the gate/up products: finish the
+    // DeltaNet outputs there, off the staging path
+    if constexpr (KIND == kDN) {
+        if (wave == kCtl) dn_finish(a, L, ydn, ln);
+    }
     wg_sync();
     const GemvGeo dg = gemv_geo(a.d_C, a.d_P, a.d_RP, a.d_rows, a.H);
     Buf<3 * NID> db;
@@ -1102,18 +1080,28 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         ctl_arrive(a, p0 + 1, ln, true);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
+    constexpr int NAD = NID / 2;
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0 + 1, ln);
         if (ln == 0) ctl[0] = okw;
         if (okw) {
-            stage_h<JI>(a, dg.C, ln, lds);
+            stage_h_load<JI>(a, ln, lds);
             if (ln < dg.nrows) x_old = ldf_sc(a.x + dg.R0 + ln);
         }
     } else {
         const uint8_t* const W[2] = {L.w[2], L.w[2]};
         const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
-        gemv_prefetch<NID>(db, dg, W, LU, 1, wave, ln, lds);
+        gemv_prefetch<NID, NAD, 0>(db, dg, W, LU, 1, wave, ln, lds);
+    }
+    wg_sync();   // the h loads were issued ahead of the second half of the weights
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        vm_drain();   // h has landed in LDS
+    } else {
+        const uint8_t* const W[2] = {L.w[2], L.w[2]};
+        const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
+        gemv_prefetch<NID, NAD, 1>(db, dg, W, LU, 1, wave, ln, lds);
         // the next DeltaNet layer's state (not produced by this launch) streams in
         // during the down phase, so the core inputs staged after the barrier do
         // not queue behind it
@@ -1293,6 +1281,7 @@ void persistent_destroy(PersistentStep* s) {
     if (s->d_rope) (void)hipFree(s->d_rope);
     if (s->args.part) (void)hipFree(s->args.part);
     if (s->args.gpart) (void)hipFree(s->args.gpart);
+    if (s->args.dnss) (void)hipFree(s->args.dnss);
     if (s->args.sync) (void)hipFree(s->args.sync);
     delete s;
 }
@@ -1353,9 +1342,10 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
                       "persistent step: rope_mode %d", d->rope_mode);
     }
     if (n_attn < n_layers) {
-        ANELM_REQUIRE(d->lin_dim == pk::kDnD && d->lin_v_heads <= nwg && d->lin_k_heads > 0 &&
+        ANELM_REQUIRE(d->lin_dim == pk::kDnD && d->lin_v_heads * pk::kDnSlabs == nwg && d->lin_k_heads > 0 &&
                           d->lin_v_heads % d->lin_k_heads == 0,
-                      "persistent step: DeltaNet needs 128-dim heads, Hv <= %d", nwg);
+                      "persistent step: DeltaNet needs 128-dim heads and %d value heads (8 workgroups each)",
+                      nwg / pk::kDnSlabs);
     }
     // Supported instantiation: the Qwen3.5-4B shape on a 256-CU device.
     void* kp = nullptr;
@@ -1382,6 +1372,7 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     const size_t rec = (size_t)pk::kAttnG * (pk::kAttnD + 2);
     if (e == hipSuccess) e = hipMalloc(&s->args.part, sizeof(float) * rec * (n_attn ? d->n_kv_heads * splits : 1));
     if (e == hipSuccess) e = hipMalloc(&s->args.gpart, sizeof(float) * rec * (n_attn ? d->n_kv_heads * pk::kSplitGroups : 1));
+    if (e == hipSuccess) e = hipMalloc(&s->args.dnss, sizeof(float) * (size_t)nwg);
     if (e == hipSuccess) e = hipMalloc(&s->args.sync, sizeof(unsigned) * pk::kSyncWords);
     if (e == hipSuccess) e = hipMemset(s->args.sync, 0, sizeof(unsigned) * pk::kSyncWords);
     if (e == hipSuccess)
