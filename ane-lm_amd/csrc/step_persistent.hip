@@ -177,8 +177,19 @@ __device__ __forceinline__ CArgs* opaque_args(CArgs* p) {
 }
 // Waits until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-// Workgroup barrier; LDS writes are complete first.  Bulk loads stay in flight.
-__device__ __forceinline__ void wg_sync() { __syncthreads(); }
+// Workgroup barrier for LDS exchange: this wave's LDS operations complete
+// first (lgkmcnt(0), vmcnt and expcnt left open), then s_barrier.  Unlike
+// __syncthreads() it carries no release fence for global memory, which would
+// wait for every vector memory operation (vmcnt(0)) once a store is pending --
+// including the bulk loads kept in flight across the barrier.  Global data
+// handed between workgroups is drained explicitly (vm_drain) before its
+// barrier arrival.
+__device__ __forceinline__ void wg_sync() {
+    cbar();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    cbar();
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, kW3);
@@ -216,9 +227,9 @@ __device__ __forceinline__ uint32_t pair_addr(uint32_t w0, uint32_t w1, uint32_t
 __device__ __forceinline__ uint32_t lds_u32(const char* base, uint32_t off) {
     return *reinterpret_cast<const uint32_t*>(base + off);
 }
-__device__ __forceinline__ float chunk_dot(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1,
-                                           uint32_t w2, const uint32_t (&xh)[8]) {
-    uint32_t p[8];
+// The 8 fp16 weight pairs of one 96-bit chunk (pair k: weights 2k, 2k+1).
+__device__ __forceinline__ void chunk_pairs(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1, uint32_t w2,
+                                            uint32_t (&p)[8]) {
     p[0] = lds_u32(lds, pair_addr<0>(w0, w1, w2, tb));
     p[1] = lds_u32(lds, pair_addr<12>(w0, w1, w2, tb));
     p[2] = lds_u32(lds, pair_addr<24>(w0, w1, w2, tb));
@@ -227,6 +238,8 @@ __device__ __forceinline__ float chunk_dot(const char* lds, uint32_t tb, uint32_
     p[5] = lds_u32(lds, pair_addr<60>(w0, w1, w2, tb));
     p[6] = lds_u32(lds, pair_addr<72>(w0, w1, w2, tb));
     p[7] = lds_u32(lds, pair_addr<84>(w0, w1, w2, tb));
+}
+__device__ __forceinline__ float pairs_dot(const uint32_t (&p)[8], const uint32_t (&xh)[8]) {
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k += 2) {
@@ -234,6 +247,12 @@ __device__ __forceinline__ float chunk_dot(const char* lds, uint32_t tb, uint32_
         a1 = dot2(p[k + 1], xh[k + 1], a1);
     }
     return a0 + a1;
+}
+__device__ __forceinline__ float chunk_dot(const char* lds, uint32_t tb, uint32_t w0, uint32_t w1,
+                                           uint32_t w2, const uint32_t (&xh)[8]) {
+    uint32_t p[8];
+    chunk_pairs(lds, tb, w0, w1, w2, p);
+    return pairs_dot(p, xh);
 }
 
 // ----------------------------------------------------------------- barrier
@@ -296,53 +315,79 @@ __device__ __forceinline__ GemvGeo gemv_geo(int C, int P, int RP, int rows_per_w
     return q;
 }
 
-// Weight stream of this wave in two parts: PART 0 issues the LUT loads and
-// instructions m < NA, then builds the pair tables (after the LUT values
-// arrive; the weights stay in flight); PART 1 issues m >= NA.  Splitting lets
-// the phase's staging loads, issued between the parts, overtake half of the
-// stream.
-template <int NI, int NA, int PART>
-__device__ __forceinline__ void gemv_prefetch(Buf<3 * NI>& b, const GemvGeo& q, const uint8_t* const (&W)[2],
-                                              const uint16_t* const (&LUT)[2], int n_mat, int wave,
-                                              int lane, char* lds) {
+// Weight stream of this wave: gemv_issue issues instructions [LO, HI) (and,
+// with LUTS, this wave's LUT loads into lr); gemv_tables builds the pair
+// tables once the LUT values arrived (the weights stay in flight).  Issuing
+// the stream in parts lets the phase's staging loads overtake its second half.
+struct LutRegs {
+    uint32_t v[3];
+};
+// A wave without a share issues nothing (callers keep the control wave out).
+template <int NI, int LO, int HI, bool LUTS>
+__device__ __forceinline__ void gemv_issue(Buf<3 * NI>& b, LutRegs& lr, const GemvGeo& q,
+                                           const uint8_t* const (&W)[2], const uint16_t* const (&LUT)[2],
+                                           int n_mat, int wave, int lane) {
     if (wave >= n_mat * q.P || q.nrows <= 0) return;
     const int mt = wave / q.P, wl = wave - mt * q.P;
-    if constexpr (PART == 1) {
-        const uint8_t* Wt = (mt ? W[1] : W[0]) + (size_t)q.R0 * q.C * 12;
-        const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
-        const int voff = (wl * 64 + lane) * 12;
-#pragma unroll
-        for (int m = NA; m < NI; m++) {
-            const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, m * q.P * 768, 0);
-            b.v[3 * m] = t.x;
-            b.v[3 * m + 1] = t.y;
-            b.v[3 * m + 2] = t.z;
-        }
-        return;
+    if constexpr (LUTS) {
+        // buffer loads: generic (flat) loads would also count on the LDS wait
+        // counter and stall every LDS wait that follows until they return
+        const uint16_t* lut = (mt ? LUT[1] : LUT[0]) + (size_t)q.g0 * 64;
+        const __amdgpu_buffer_rsrc_t rl = rsrc(lut, (uint32_t)(q.ng * 128));
+        lr.v[0] = __builtin_amdgcn_raw_buffer_load_b16(rl, lane * 2, 0, 0);
+        lr.v[1] = __builtin_amdgcn_raw_buffer_load_b16(rl, (64 + lane) * 2, 0, 0);   // 0 past ng groups
+        lr.v[2] = __builtin_amdgcn_raw_buffer_load_b16(rl, (128 + lane) * 2, 0, 0);
     }
-    const uint16_t* lut = mt ? LUT[1] : LUT[0];
-    uint32_t lv0 = 0u, lv1 = 0u, lv2 = 0u;
-    lv0 = lut[(size_t)q.g0 * 64 + lane];
-    if (q.ng > 1) lv1 = lut[(size_t)(q.g0 + 1) * 64 + lane];
-    if (q.ng > 2) lv2 = lut[(size_t)(q.g0 + 2) * 64 + lane];
     const uint8_t* Wt = (mt ? W[1] : W[0]) + (size_t)q.R0 * q.C * 12;
     const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
     const int voff = (wl * 64 + lane) * 12;
 #pragma unroll
-    for (int m = 0; m < NA; m++) {
+    for (int m = LO; m < HI; m++) {
         const u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, m * q.P * 768, 0);
         b.v[3 * m] = t.x;
         b.v[3 * m + 1] = t.y;
         b.v[3 * m + 2] = t.z;
     }
+}
+__device__ __forceinline__ void gemv_tables(const LutRegs& lr, const GemvGeo& q, int n_mat, int wave, int lane,
+                                            char* lds, int* ctr, int target) {
+    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    const int mt = wave / q.P, wl = wave - mt * q.P;
     // pair tables (mt*3 + gi): rows i1 = wl, wl + P, ... of 64
     for (int gi = 0; gi < q.ng; gi++) {
-        const uint32_t mine = gi == 0 ? lv0 : (gi == 1 ? lv1 : lv2);
+        const uint32_t mine = gi == 0 ? lr.v[0] : (gi == 1 ? lr.v[1] : lr.v[2]);
         char* tab = lds + kLdsTab + (mt * 3 + gi) * 16384;
         for (int i1 = wl; i1 < 64; i1 += q.P) {
             const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)mine, i1);
             *reinterpret_cast<uint32_t*>(tab + i1 * 256 + lane * 4) = mine | (hi << 16);
         }
+    }
+    // the matrix's P waves each wrote rows of its tables: wait for all of them
+    // (LDS counter, grows by P per build; bounded spin)
+    int* c = ctr + mt;
+    if (lane == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int it = 0; it < (1 << 20); it++) {
+        if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Table lookups of instructions m < NA ahead of the input (they need only
+// the weights and the tables): decoded fp16 pairs into d.
+template <int NI, int NA>
+__device__ __forceinline__ void gemv_decode(const Buf<3 * NI>& b, Buf<8 * NA>& d, const GemvGeo& q, int n_mat,
+                                            int wave, int lane, char* lds) {
+    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    const int mt = wave / q.P;
+#pragma unroll
+    for (int m = 0; m < NA; m++) {
+        const int gi = ((q.R0 + q.RP * m) >> 5) - q.g0;
+        const uint32_t tb = (uint32_t)(kLdsTab + (mt * 3 + gi) * 16384);
+        uint32_t p[8];
+        chunk_pairs(lds, tb, b.v[3 * m], b.v[3 * m + 1], b.v[3 * m + 2], p);
+#pragma unroll
+        for (int k = 0; k < 8; k++) d.v[8 * m + k] = p[k];
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -361,9 +406,9 @@ __device__ __forceinline__ void half_sum8(float (&v)[8], int lane) {
 // Compute waves: dot products of the prefetched rows against the staged fp16
 // x pairs; per-half-wave row sums into LDS red[mt][m][hw] (hw = half-wave of
 // the matrix's waves), reduced 8 instructions at a time.
-template <int NI>
-__device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const GemvGeo& q, int n_mat, int wave,
-                                             int lane, char* lds) {
+template <int NI, int NA>
+__device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const Buf<8 * NA>& d, const GemvGeo& q,
+                                             int n_mat, int wave, int lane, char* lds) {
     if (wave >= n_mat * q.P || q.nrows <= 0) return;
     const int mt = wave / q.P, wl = wave - mt * q.P;
     const int g = 64 * wl + lane;
@@ -379,7 +424,11 @@ __device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const GemvGeo
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int m = m0 + j;
-            if (m < NI) {
+            if (m < NA) {
+                const uint32_t p[8] = {d.v[8 * m], d.v[8 * m + 1], d.v[8 * m + 2], d.v[8 * m + 3],
+                                       d.v[8 * m + 4], d.v[8 * m + 5], d.v[8 * m + 6], d.v[8 * m + 7]};
+                part[j] = pairs_dot(p, xh);
+            } else if (m < NI) {
                 const int gi = ((q.R0 + q.RP * m) >> 5) - q.g0;
                 const uint32_t tb = (uint32_t)(kLdsTab + (mt * 3 + gi) * 16384);
                 part[j] = chunk_dot(lds, tb, b.v[3 * m], b.v[3 * m + 1], b.v[3 * m + 2], xh);
@@ -699,7 +748,7 @@ __device__ void attn_merge(const float* recs, int rstride, float* out_rec, bool 
             tot[4 + g] = Ls;
         }
     }
-    __syncthreads();
+    wg_sync();
     constexpr int E = kAttnG * kAttnD;
     constexpr int PER = (E + kNT - 1) / kNT;
     float v[PER][N];
@@ -1010,6 +1059,13 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     int* ctl = ctl_ints(lds);
     int ln = opaque(lane);
     float ydn = 0.f;
+    const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
+    Buf<3 * NIG> gb;
+    LutRegs glr;
+    constexpr int NAG = NIG / 2;     // weights issued before the barrier
+    constexpr int NDG = 5;           // of them decoded before the input (registers)
+    const uint8_t* const GW[2] = {L.w[0], L.w[1]};
+    const uint16_t* const GLU[2] = {L.lut[0], L.lut[1]};
     // ------------------------------------------------------------ core
     if constexpr (KIND == kATT) {
         attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
@@ -1029,33 +1085,31 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         stage_w<JH>(a, L.ffn_norm_w, ln, lds);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
-    const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
-    Buf<3 * NIG> gb;
-    constexpr int NAG = NIG / 2;
+    Buf<8 * NDG> gd;
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0, ln);
         if (ln == 0) ctl[0] = okw;
         if (okw) stage_x_load<JH>(a, ln, lds);
     } else {
-        const uint8_t* const W[2] = {L.w[0], L.w[1]};
-        const uint16_t* const LU[2] = {L.lut[0], L.lut[1]};
-        gemv_prefetch<NIG, NAG, 0>(gb, gu, W, LU, 2, wave, ln, lds);
+        // first half of the weights, the tables, and their lookups while the
+        // barrier is pending
+        gemv_issue<NIG, 0, NAG, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        gemv_tables(glr, gu, 2, wave, ln, lds, ctl + 8, gu.P * (l + 1));
+        gemv_decode<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
     }
     wg_sync();   // the x loads were issued ahead of the second half of the weights
     ln = opaque(lane);
     if (wave == kCtl) {
         if (ctl[0]) stage_x_fin<JH>(a, ln, lds);
     } else {
-        const uint8_t* const W[2] = {L.w[0], L.w[1]};
-        const uint16_t* const LU[2] = {L.lut[0], L.lut[1]};
-        gemv_prefetch<NIG, NAG, 1>(gb, gu, W, LU, 2, wave, ln, lds);
+        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
     }
     wg_sync();
     if (!ctl[0]) return false;
     // --------------------------------------------------------- gate/up
     ln = opaque(lane);
-    gemv_compute<NIG>(gb, gu, 2, wave, ln, lds);
+    gemv_compute<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
     // the control wave is idle during the gate/up products: finish the
     // DeltaNet outputs there, off the staging path
     if constexpr (KIND == kDN) {
@@ -1080,7 +1134,9 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         ctl_arrive(a, p0 + 1, ln, true);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
-    constexpr int NAD = NID / 2;
+    constexpr int NAD = NID / 2;     // weights issued before the barrier
+    constexpr int NDD = 5;           // of them decoded before the input
+    Buf<8 * NDD> dd;
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0 + 1, ln);
@@ -1092,7 +1148,10 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     } else {
         const uint8_t* const W[2] = {L.w[2], L.w[2]};
         const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
-        gemv_prefetch<NID, NAD, 0>(db, dg, W, LU, 1, wave, ln, lds);
+        LutRegs dlr;
+        gemv_issue<NID, 0, NAD, true>(db, dlr, dg, W, LU, 1, wave, ln);
+        gemv_tables(dlr, dg, 1, wave, ln, lds, ctl + 10, dg.P * (l + 1));
+        gemv_decode<NID, NDD>(db, dd, dg, 1, wave, ln, lds);
     }
     wg_sync();   // the h loads were issued ahead of the second half of the weights
     ln = opaque(lane);
@@ -1101,7 +1160,8 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     } else {
         const uint8_t* const W[2] = {L.w[2], L.w[2]};
         const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
-        gemv_prefetch<NID, NAD, 1>(db, dg, W, LU, 1, wave, ln, lds);
+        LutRegs unused;
+        gemv_issue<NID, NAD, NID, false>(db, unused, dg, W, LU, 1, wave, ln);
         // the next DeltaNet layer's state (not produced by this launch) streams in
         // during the down phase, so the core inputs staged after the barrier do
         // not queue behind it
@@ -1111,7 +1171,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     if (!ctl[0]) return false;
     // ------------------------------------------------------------ down
     ln = opaque(lane);
-    gemv_compute<NID>(db, dg, 1, wave, ln, lds);
+    gemv_compute<NID, NDD>(db, dd, dg, 1, wave, ln, lds);
     wg_sync();
     ln = opaque(lane);
     constexpr bool more = NEXT != kNONE;
@@ -1157,7 +1217,10 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     // phase 0: core of layer 0 (inputs are ready at launch)
     dn_prefetch(cdn, a, L0, wave, lane);
     if (wave == kCtl) dn_stage(a, L0, lane, lds);
-    if (tid == 0) ctl[0] = 1;
+    if (tid == 0) {
+        ctl[0] = 1;
+        ctl[8] = ctl[9] = ctl[10] = 0;   // table-build counters (gate, up, down)
+    }
     wg_sync();
     const int groups = a.n_layers / 4;
     for (int gr = 0; gr < groups; gr++) {
