@@ -31,10 +31,11 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 METRIC = "µs per decode step (attn+DeltaNet+LUT6, 4B shape); HBM GB/s as % of peak"
 HBM_PEAK_GBPS = 8000.0
 MODE_NAMES = {0: "eager launches", 1: "hip graph replay", 6: "persistent kernel, one launch per step"}
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled
-# by the factor a plain copy kernel of known size reads (filled in from the
-# committed profiles; None until measured)
-TRAFFIC = {}
+# HBM bytes per launch of the step kernel from two rocprofv3 --pmc runs
+# (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the counter
+# reads for a 1 GiB device copy in the same run (fetch 524338 KiB -> factor
+# 1.99981; write 1048576 KiB -> factor 1.0): fetch 1040983 KiB, write 62939 KiB.
+TRAFFIC = {"step_kernel": 2196179422}
 
 CFG = dict(hidden=2560, inter=9216, layers=32, n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64,
            theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=32, lin_dim=128, ctx=8192)
@@ -253,6 +254,9 @@ def main():
                     help="decode-step execution (default: persistent, else graph)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="after the timed steps, copy MB MiB device-to-device once (a kernel of known "
+                         "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark measures one GPU; the decode step does not "
@@ -290,6 +294,13 @@ def main():
         assert st.value == 0, "a grid barrier of the persistent step timed out"
         gu_avg, gu_med = time_gateup(anelm, torch, keep)
         anelm.call("anelm_hybrid_step_destroy", handle)
+        if args.copy_probe:
+            src = torch.empty(args.copy_probe << 18, device=dev)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
         persistent = bool(mode & anelm.STEP_PERSISTENT)
 
     b = step_bytes()
