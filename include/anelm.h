@@ -171,7 +171,9 @@ int anelm_deltanet_decode(float* y, float* state, const float* q, const float* k
 /* Chunked DeltaNet prefill over S tokens (no reference kernel: the reference
  * runs ssm_step per token, qwen3_5.cpp:1204-1217).  q,k [S][Hk][dk],
  * v [S][Hv][dv], a,b [S][Hv]; y [S][Hv][dv]; state [Hv][dk][dv] updated to the
- * state after token S-1.  chunk = 64.  Flags as anelm_deltanet_decode minus
+ * state after token S-1.  chunk = 64: chunked closed form (per 64-token chunk
+ * the state-independent products in parallel, then the state carried through
+ * the chunks); chunk = 1: token-by-token scan.  Flags as anelm_deltanet_decode minus
  * GATED_NORM.  dk, dv = 128. */
 int anelm_deltanet_prefill(float* y, float* state, const float* q, const float* k, const float* v,
                            const float* a, const float* b, const float* A, const float* dt_bias,

@@ -79,3 +79,39 @@ def test_deltanet_prefill_matches_decode_chain(anelm, dev):
                                        d2["b"][t].contiguous(), d2["A"], d2["dt_bias"], 1)
         assert_close(to_host(yt), y[t], rel=1e-5, max_abs=1e-4)
     assert_close(to_host(d2["state"]), to_host(d["state"]), rel=1e-5, max_abs=1e-4)
+
+
+@pytest.mark.parametrize("S,flags", [(64, 1), (65, 3), (200, 1)])
+def test_deltanet_prefill_scan_path(anelm, orc, dev, S, flags):
+    """chunk=1 selects the token-by-token scan; it matches the oracle too."""
+    c = deltanet_case(560 + S, Hk=4, Hv=8, S=S)
+    d = _dev_case(c, dev)
+    y = anelm.ops.deltanet_prefill(d["state"], d["q"], d["k"], d["v"], d["a"], d["b"], d["A"],
+                                   d["dt_bias"], flags, chunk=1)
+    yw, Sw = orc.deltanet_prefill(c.state, c.q, c.k, c.v, c.a, c.b, c.A, c.dt_bias, flags)
+    assert_close(to_host(y), yw, what="y")
+    assert_close(to_host(d["state"]), Sw, what="state")
+
+
+@pytest.mark.parametrize("flags", [1, 3])
+def test_deltanet_prefill_chunked_matches_scan_4096(anelm, dev, flags):
+    """The prefill workload size (4096 tokens, 16 key / 32 value heads): the
+    chunked form (64-token chunks) against the token-by-token scan, both on the
+    GPU (the sequential oracle at this size takes minutes)."""
+    c = deltanet_case(570 + flags, Hk=16, Hv=32, S=4096)
+    d = _dev_case(c, dev)
+    y = to_host(anelm.ops.deltanet_prefill(d["state"], d["q"], d["k"], d["v"], d["a"], d["b"], d["A"],
+                                           d["dt_bias"], flags))
+    d2 = _dev_case(c, dev)
+    y2 = to_host(anelm.ops.deltanet_prefill(d2["state"], d2["q"], d2["k"], d2["v"], d2["a"], d2["b"],
+                                            d2["A"], d2["dt_bias"], flags, chunk=1))
+    assert_close(y, y2, rel=1e-4, max_abs=1e-3, what="y")
+    assert_close(to_host(d["state"]), to_host(d2["state"]), rel=1e-4, max_abs=1e-3, what="state")
+
+
+def test_deltanet_prefill_rejects_other_chunks(anelm, dev):
+    c = deltanet_case(580, Hk=2, Hv=4, S=8)
+    d = _dev_case(c, dev)
+    with pytest.raises(anelm.AnelmError):
+        anelm.ops.deltanet_prefill(d["state"], d["q"], d["k"], d["v"], d["a"], d["b"], d["A"],
+                                   d["dt_bias"], 1, chunk=32)
