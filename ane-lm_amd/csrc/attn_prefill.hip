@@ -148,6 +148,336 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Workload-balanced, pipelined kernel for head_dim 256 and 4 query heads per KV
+// head (the Qwen3.5 shapes).
+//
+// * Blocks of 64 query rows; a workgroup's 8 waves are 4 query heads x 2 row
+//   halves of 32 rows, and all of them consume ONE stream of 32-key tiles, so
+//   each K / V^T byte staged in LDS feeds 256 query rows.
+// * Balance: a unit is a KV head and a pair of blocks (a, nb-1-a) (or the
+//   middle block when nb is odd).  Its causal key tiles, a's then b's, are cut
+//   into two equal halves taken by two workgroups.  The block whose tiles are
+//   split is merged by whichever of the two finishes second: both write their
+//   partial (m, l, unnormalised O) with device-coherent stores, a relaxed
+//   device-scope counter tells the second which it is, and the second combines
+//   and writes the rows (and re-zeroes the counter for the next call).
+// * Stream: K tiles (32 keys x 256) and V^T tiles (256 dims x 32 keys, from the
+//   V^T copy made by vt_kernel) go straight to LDS with buffer loads (1 KiB per
+//   wave instruction) into a ring of 4 buffers, 3 tiles ahead of use.  K rows c
+//   and c+16 share a 1040-byte chunk (16 bytes of padding per chunk) so the
+//   MFMA operand reads are conflict-free with immediate offsets; V^T 16-byte
+//   granules are XOR-swizzled.
+// * Scores S^T = K Q^T (v_mfma_f32_32x32x16_f16).  The A-operand lane i reads
+//   key row pi(i) (bits 2 and 3 of i swapped): lane (r, h) of the accumulator
+//   then holds the scores of query row r for keys 8h..8h+7 and 16+8h..16+8h+7,
+//   exactly the B-operand keys of O^T += V^T P^T.
+// * Softmax in the log2 domain; the running maximum only moves when it grows
+//   by more than 8, so probabilities stay below 2^8 (fp16-exact range) and the
+//   128-register output rescale is rare.
+constexpr int kGKeys = 32;                       // keys per tile
+constexpr int kGKBytes = 16 * 1040;              // K tile: chunk c = rows c, c + 16
+constexpr int kGTile = kGKBytes + 16384;         // + V^T tile (256 x 32 fp16)
+constexpr int kGBuf = 4;                         // ring of tile buffers
+constexpr int kGLds = kGBuf * kGTile + 64;       // + the merge flag
+constexpr int kGSlotFloats = 8 * 128 * 64 + 8 * 128;   // partial: O (8 waves x 128 x 64 lanes), m, l
+constexpr int kGNT = 512;
+constexpr int kSc1 = 16;                         // buffer cache policy: device-scope coherent
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// V^T copy: vt[(kvh * D + d) * S_pad + key] (zero past S).
+__global__ __launch_bounds__(256) void vt_kernel(_Float16* vt, const _Float16* v, int S, int S_pad, int Hkv) {
+    constexpr int D = 256;
+    __shared__ __attribute__((aligned(16))) _Float16 tile[kGKeys][D + 8];
+    const int j0 = blockIdx.x * kGKeys, kvh = blockIdx.y, tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k, key = c / (D / 8), g = c % (D / 8);
+        uint4 val = make_uint4(0, 0, 0, 0);
+        if (j0 + key < S) val = *reinterpret_cast<const uint4*>(v + ((size_t)(j0 + key) * Hkv + kvh) * D + 8 * g);
+        *reinterpret_cast<uint4*>(&tile[key][8 * g]) = val;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k, d = c / 4, g = c % 4;
+        _Float16 e[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) e[i] = tile[8 * g + i][d];
+        *reinterpret_cast<uint4*>(vt + ((size_t)kvh * D + d) * S_pad + j0 + 8 * g) = *reinterpret_cast<const uint4*>(e);
+    }
+}
+
+__device__ __forceinline__ int key_perm(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// Key tiles needed by 64-row block blk: keys 0 .. min(64 blk + 63, S - 1).
+__device__ __forceinline__ int block_tiles(int blk, int S) { return (min(64 * blk + 64, S) + 31) / 32; }
+
+template <bool OUT16>
+__global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Float16* q, const _Float16* k,
+                                                           const _Float16* vt, float* part, uint32_t* ctr, int S,
+                                                           int S_pad, int Hq, int Hkv) {
+    constexpr int D = 256, KS = D / 16, DB = D / 32;
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hl = w & 3, rh = w >> 2;
+    const int nb = (S + 63) / 64, npair = nb / 2, upk = npair + (nb & 1);
+    // consecutive units on one XCD (workgroup id mod 8 selects the XCD): one KV head per L2
+    int L = blockIdx.x;
+    if (gridDim.x % 8 == 0) L = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+    const int unit = L >> 1, half_id = L & 1;
+    const int kvh = unit / upk, pu = unit % upk;
+    const int h = kvh * 4 + hl;
+    const int blk_a = pu < npair ? pu : -1, blk_b = pu < npair ? nb - 1 - pu : npair;
+    const int nta = blk_a >= 0 ? block_tiles(blk_a, S) : 0, ntb = block_tiles(blk_b, S);
+    const int half = (nta + ntb) / 2, nb0 = half - nta;   // tiles of b taken by the first workgroup
+    const bool split = nb0 > 0;
+    // this workgroup's segments (block, first key tile, tile count)
+    int blk0, t00, n0, blk1 = 0, t01 = 0, n1 = 0;
+    if (half_id == 0) {
+        if (nta > 0) {
+            blk0 = blk_a; t00 = 0; n0 = nta;
+            if (nb0 > 0) { blk1 = blk_b; t01 = 0; n1 = nb0; }
+        } else {
+            blk0 = blk_b; t00 = 0; n0 = nb0;
+        }
+    } else {
+        const int f = nb0 > 0 ? nb0 : 0;
+        blk0 = blk_b; t00 = f; n0 = ntb - f;
+    }
+    if (n0 <= 0) return;
+    const int nseg = n1 > 0 ? 2 : 1;
+    const int ntot = n0 + n1;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(k), 0, (int)min((size_t)S * Hkv * D * 2, (size_t)0x7fffffff), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(vt), 0, (int)min((size_t)Hkv * D * S_pad * 2, (size_t)0x7fffffff), 0x00020000);
+    const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;   // 1/sqrt(256) * log2(e)
+    auto key_tile = [&](int i) { return i < n0 ? t00 + i : t01 + (i - n0); };
+    // stream tile i -> buffer i % 4; wave w loads K chunks 2w, 2w+1 and V^T pieces 2w, 2w+1
+    auto issue = [&](int i) {
+        char* base = lds + (i % kGBuf) * kGTile;
+        const int j0 = key_tile(i) * kGKeys;
+        int ln = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln));   // lane offsets are recomputed here, not held across the loop
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            const int c = 2 * w + x, row = c + 16 * (ln >> 5), key = j0 + row;
+            const int off = key < S ? ((key * Hkv + kvh) * D + 8 * (ln & 31)) * 2 : 0x7fffffff;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(base + c * 1040), 16,
+                                                     off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            const int p = (2 * w + x) * 64 + ln, d = p >> 2, gs = p & 3, g = gs ^ ((d >> 2) & 3);
+            const int off = (((kvh * D + d) * S_pad) + j0 + 8 * g) * 2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void*)(base + kGKBytes + (2 * w + x) * 1024), 16, off, 0, 0, 0);
+        }
+    };
+    for (int i = 0; i < 3 && i < ntot; i++) issue(i);
+    int i = 0;
+    for (int sg = 0; sg < nseg; sg++) {
+        const int blk = sg == 0 ? blk0 : blk1;
+        const int row0 = 64 * blk + 32 * rh;
+        half8 qf[KS];
+        {
+            const int lane = threadIdx.x & 63, qrow = row0 + (lane & 31);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                if (qrow < S)
+                    qf[ks] = *reinterpret_cast<const half8*>(q + ((size_t)qrow * Hq + h) * D + 16 * ks + 8 * (lane >> 5));
+                else
+                    qf[ks] = half8{};
+            }
+        }
+        // the Q fragments complete here, so no wait for them remains inside the tile loop
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        float16_t o[DB];
+#pragma unroll
+        for (int db = 0; db < DB; db++) o[db] = float16_t{};
+        float m = -INFINITY, l = 0.f;
+        const int iend = sg == 0 ? n0 : ntot;
+        for (; i < iend; i++) {
+            // tile i has landed once at most the loads of tiles i+1, i+2 (4 per wave each) remain
+            const int left = ntot - 1 - i;
+            if (left >= 2) __builtin_amdgcn_s_waitcnt(0x0F78);
+            else if (left == 1) __builtin_amdgcn_s_waitcnt(0x0F74);
+            else __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();   // every wave's part of tile i landed; buffer (i+3)%4 (tile i-1) is free
+            if (i + 3 < ntot) issue(i + 3);
+            const int kt = key_tile(i), j0 = kt * kGKeys;
+            if (j0 > row0 + 31) continue;   // every key of this tile lies after this wave's rows
+            const char* base = lds + (i % kGBuf) * kGTile;
+            int ln = threadIdx.x & 63;
+            asm volatile("" : "+v"(ln));
+            // ---- S^T = K Q^T
+            float16_t sc = float16_t{};
+            {
+                const int krow = key_perm(ln & 31);
+                const char* kb = base + (krow & 15) * 1040 + (krow >> 4) * 512 + (ln >> 5) * 16;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + 32 * ks), qf[ks], sc,
+                                                                0, 0, 0);
+            }
+            // ---- online softmax; element e holds key j0 + (e < 8 ? 8 h + e : 16 + 8 h + e - 8)
+            if (j0 + 31 > row0) {
+                const int h2 = ln >> 5, qr = row0 + (ln & 31);
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int key = j0 + (e < 8 ? 8 * h2 + e : 16 + 8 * h2 + (e - 8));
+                    sc[e] = key <= qr ? sc[e] : -INFINITY;
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; e++) mx = fmaxf(mx, sc[e]);
+            mx = fmaxf(mx, shfl_xor(mx, 32)) * sl2;
+            if (__builtin_amdgcn_ballot_w64(mx > m + 8.0f) != 0) {
+                const float m_new = fmaxf(m, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+                l *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; db++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) o[db][e] *= alpha;
+                m = m_new;
+            }
+            half8 pf[2];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -m));
+                l += pe;
+                pf[e / 8][e % 8] = (_Float16)pe;
+            }
+            // ---- O^T += V^T P^T
+            {
+                const int rr = ln & 31, h2 = ln >> 5;
+                const char* vb0 = base + kGKBytes + rr * 64 + ((h2 ^ ((rr >> 2) & 3)) << 4);
+                const char* vb1 = base + kGKBytes + rr * 64 + (((2 + h2) ^ ((rr >> 2) & 3)) << 4);
+#pragma unroll
+                for (int db = 0; db < DB; db++) {
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(vb0 + 2048 * db),
+                                                                   pf[0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(vb1 + 2048 * db),
+                                                                   pf[1], o[db], 0, 0, 0);
+                }
+            }
+        }
+        l += shfl_xor(l, 32);
+        int ln = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln));   // the epilogue's addresses are computed here, not held through the loop
+        const int erow = row0 + (ln & 31), eh = ln >> 5;
+        float a0 = 1.f, a1 = 0.f, inv;
+        __amdgpu_buffer_rsrc_t rot = __builtin_amdgcn_make_buffer_rsrc(part, 0, 0, 0x00020000);
+        bool have_other = false;
+        if (split && blk == blk_b) {
+            // partial of the split block: publish, then the second finisher merges
+            const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+                part + (size_t)(unit * 2 + half_id) * kGSlotFloats, 0, kGSlotFloats * 4, 0x00020000);
+#pragma unroll
+            for (int db = 0; db < DB; db++)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const float4 v4 = make_float4(o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v4), rm,
+                                                           (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1);
+                }
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m), rm, (8 * 128 * 64 + w * 128 + ln) * 4,
+                                                  0, kSc1);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l), rm,
+                                                  (8 * 128 * 64 + w * 128 + 64 + ln) * 4, 0, kSc1);
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's partial is stored
+            __syncthreads();
+            uint32_t* flag = reinterpret_cast<uint32_t*>(lds + kGBuf * kGTile);
+            if (tid == 0) flag[0] = __hip_atomic_fetch_add(&ctr[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (flag[0] == 0) break;   // the other workgroup finishes this block (its segment is the last)
+            if (tid == 0) __hip_atomic_store(&ctr[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            rot = __builtin_amdgcn_make_buffer_rsrc(part + (size_t)(unit * 2 + (half_id ^ 1)) * kGSlotFloats, 0,
+                                                    kGSlotFloats * 4, 0x00020000);
+            have_other = true;
+            const float m1 = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rot, (8 * 128 * 64 + w * 128 + ln) * 4, 0, kSc1));
+            const float l1 = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rot, (8 * 128 * 64 + w * 128 + 64 + ln) * 4, 0, kSc1));
+            const float M = fmaxf(m, m1);
+            a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+            a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+            inv = 1.0f / (l * a0 + l1 * a1);
+        } else {
+            inv = 1.0f / l;
+        }
+        if (erow < S) {
+            // o[db][e] = output dim 32 db + 8 (e / 4) + 4 h + e % 4 of row erow
+#pragma unroll
+            for (int db = 0; db < DB; db++) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int dd = 32 * db + 8 * g4 + 4 * eh;
+                    const size_t off = ((size_t)erow * Hq + h) * D + dd;
+                    float4 ov = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (have_other)
+                        ov = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
+                    const float v0 = (o[db][4 * g4] * a0 + ov.x * a1) * inv;
+                    const float v1 = (o[db][4 * g4 + 1] * a0 + ov.y * a1) * inv;
+                    const float v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
+                    const float v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
+                    if (OUT16) {
+                        half4 hv = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+                        *reinterpret_cast<half4*>(static_cast<_Float16*>(out) + off) = hv;
+                    } else {
+                        *reinterpret_cast<float4*>(static_cast<float*>(out) + off) = make_float4(v0, v1, v2, v3);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // stores retired before the stream's counted waits resume
+    }
+}
+
+int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const void* v, int S, int Hq, int Hkv,
+                      hipStream_t st) {
+    constexpr int D = 256;
+    const int S_pad = (S + kGKeys - 1) / kGKeys * kGKeys;
+    ANELM_REQUIRE((size_t)S * Hkv * D * 2 < 0x7fffffffu && (size_t)Hkv * D * S_pad * 2 < 0x7fffffffu,
+                  "prefill: %d tokens exceed the 2 GiB buffer range", S);
+    const int nb = (S + 63) / 64, upk = nb / 2 + (nb & 1), units = Hkv * upk;
+    const size_t vt_bytes = ((size_t)Hkv * D * S_pad * 2 + 255) & ~(size_t)255;
+    const size_t part_bytes = (size_t)2 * units * kGSlotFloats * sizeof(float);
+    char* ws = static_cast<char*>(workspace(vt_bytes + part_bytes, st));
+    if (!ws) return ANELM_ENOMEM;
+    uint32_t* ctr = counters(units);   // zeroed; each call leaves them zeroed
+    if (!ctr) return ANELM_ERANGE;
+    _Float16* vt = reinterpret_cast<_Float16*>(ws);
+    float* part = reinterpret_cast<float*>(ws + vt_bytes);
+    hipLaunchKernelGGL(vt_kernel, dim3(S_pad / kGKeys, Hkv), dim3(256), 0, st, vt, static_cast<const _Float16*>(v), S,
+                       S_pad, Hkv);
+    ANELM_LAUNCHED("vt_kernel");
+    static bool attr_set = false;
+    if (!attr_set) {
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_g4_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGLds));
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_g4_kernel<false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGLds));
+        attr_set = true;
+    }
+    const _Float16* qh = static_cast<const _Float16*>(q);
+    const _Float16* kh = static_cast<const _Float16*>(k);
+    const dim3 grid(2 * units);
+    if (out16)
+        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, S_pad,
+                           Hq, Hkv);
+    else
+        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, S_pad,
+                           Hq, Hkv);
+    ANELM_LAUNCHED("prefill_g4_kernel");
+    return ANELM_OK;
+}
+
 template <int D, int HB, int RB>
 int launch_prefill(void* out, bool out16, const void* q, const void* k, const void* v, int S, int Hq,
                    int Hkv, hipStream_t st) {
@@ -168,7 +498,9 @@ int dispatch_g(void* out, bool out16, const void* q, const void* k, const void* 
     switch (Hq / Hkv) {
         case 1: return launch_prefill<D, 1, 8>(out, out16, q, k, v, S, Hq, Hkv, st);
         case 2: return launch_prefill<D, 2, 4>(out, out16, q, k, v, S, Hq, Hkv, st);
-        case 4: return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, Hq, Hkv, st);
+        case 4:
+            if (D == 256) return launch_prefill_g4(out, out16, q, k, v, S, Hq, Hkv, st);
+            return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, Hq, Hkv, st);
         case 8: return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, Hq, Hkv, st);
         default: return set_error(ANELM_EINVAL, "prefill: n_heads/n_kv_heads = %d unsupported", Hq / Hkv);
     }

@@ -154,7 +154,8 @@ def test_paged_decode(anelm, orc, dev):
 
 # ---------------------------------------------------------------- prefill
 @pytest.mark.parametrize("S,Hq,Hkv,D", [(100, 4, 1, 256), (77, 8, 2, 128), (64, 2, 2, 256),
-                                        (130, 16, 2, 128)])
+                                        (130, 16, 2, 128), (1, 4, 1, 256), (95, 8, 2, 256),
+                                        (257, 16, 4, 256)])
 def test_prefill_small(anelm, orc, dev, S, Hq, Hkv, D):
     q, k, v = prefill_inputs(400 + S, S, Hq, Hkv, D)
     got = to_host(anelm.ops.attn_prefill(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)))
@@ -177,6 +178,22 @@ def test_prefill_4096_rows(anelm, orc, dev):
     got16 = widen(to_host(anelm.ops.attn_prefill(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev),
                                                  torch.float16)))
     assert_close(got16, got, what="fp16 output")
+
+
+def test_prefill_repeated_calls_are_identical(anelm, orc, dev):
+    """Split blocks are merged through per-call counters that each call leaves
+    zeroed: back-to-back calls of different sizes (odd block count, middle
+    unit, split pairs) give bit-identical rows, and match the oracle."""
+    runs = {}
+    for S in (700, 130, 700, 64, 700):
+        q, k, v = prefill_inputs(990 + S, S, 16, 4, 256)
+        got = to_host(anelm.ops.attn_prefill(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)))
+        if S in runs:
+            assert np.array_equal(got, runs[S]), f"S={S}: repeated call differs"
+        else:
+            runs[S] = got
+            for t in (0, S // 3, S - 1):
+                assert_close(got[t], orc.prefill_attention(q, k, v, t, t + 1)[0], what=f"S{S} row {t}")
 
 
 def test_full_attn_decode_without_norms(anelm, orc, dev):
