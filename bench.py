@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import platform
 import statistics
@@ -180,6 +181,151 @@ def time_gateup(anelm, torch, keep, n=50):
     return statistics.mean(ms) * 1e3, statistics.median(ms) * 1e3
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
+
+
+def _gpu_us(torch, fn, reps, warm=2):
+    """Average GPU time of fn() on the current stream, HIP events around `reps`
+    calls queued behind a GPU-side sleep, so host launch gaps are not timed."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.0e9 * 40e-6 * reps))
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def _hbm(us, nbytes):
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbps, 1),
+            "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def measure_cores(anelm, torch, dev, seed=11):
+    """The other workloads of the path, each timed alone on one GPU with its
+    roofline: decode attention (0.8B shape), DeltaNet decode, causal prefill
+    attention and chunked DeltaNet prefill at 4096 tokens, and the pieces of the
+    32-sequence batched decode (paged attention, batched DeltaNet, LUT6 LM head
+    top-32)."""
+    import numpy as np
+    from workloads import attn_decode_case
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def randn(*shape, std=1.0, dtype=torch.float32):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(dtype)
+
+    def l2n(t):
+        return t / t.norm(dim=-1, keepdim=True)
+
+    res = {}
+    # decode attention, 8 q / 2 kv heads, D 256, 512 cached keys + the new one
+    c = attn_decode_case(seed)
+    cap = 1024
+    kc = torch.zeros(cap, 2, 256, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    kc[:c.length].copy_(torch.from_numpy(c.k_cache[:c.length].view(np.float16)))
+    vc[:c.length].copy_(torch.from_numpy(c.v_cache[:c.length].view(np.float16)))
+    qg, k1, v1 = (torch.from_numpy(a).to(dev) for a in (c.q_gate, c.k, c.v))
+    qn, kn = torch.from_numpy(c.q_norm_w).to(dev), torch.from_numpy(c.k_norm_w).to(dev)
+    out = torch.empty(8, 256, device=dev)
+
+    def c1():
+        anelm.ops.full_attn_decode(qg, k1, v1, kc, vc, qn, kn, anelm.ops.KVRing(cap, 0, c.length), 8, 2, 256,
+                                   64, c.length, out=out)
+    res["decode_attention_0.8b"] = dict(_hbm(_gpu_us(torch, c1, 200), 1079296), keys=c.length + 1)
+
+    # DeltaNet decode, 16 heads x 128 x 128 fp32 state
+    H = 16
+    st = randn(H, 128, 128, std=0.1)
+    dq, dk = l2n(randn(H, 128)), l2n(randn(H, 128))
+    dv = randn(H, 128)
+    da, db, ddt = randn(H), randn(H), randn(H)
+    dA = torch.exp(torch.rand(H, generator=g, device=dev) * math.log(16.0))
+    y = torch.empty(H, 128, device=dev)
+
+    def c2():
+        anelm.ops.deltanet_decode(st, dq, dk, dv, da, db, dA, ddt, 0, out=y)
+    res["deltanet_decode"] = _hbm(_gpu_us(torch, c2, 200), 2129920)
+
+    # causal prefill attention, S 4096, 16 q / 4 kv heads, D 256
+    S = 4096
+    q = randn(S, 16, 256, dtype=torch.float16)
+    k = randn(S, 4, 256, dtype=torch.float16)
+    v = randn(S, 4, 256, dtype=torch.float16)
+    us = _gpu_us(torch, lambda: anelm.ops.attn_prefill(q, k, v), 20)
+    flops = 4 * 256 * 16 * S * (S + 1) // 2
+    tf = flops / (us * 1e-6) / 1e12
+    res["prefill_attention_4096"] = {"us": round(us, 2), "flops": flops, "TFLOPs": round(tf, 1),
+                                     "frac_mfma": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    del q, k, v
+
+    # chunked DeltaNet prefill, S 4096, 16 key / 32 value heads, chunk 64
+    Hk, Hv = 16, 32
+    st = randn(Hv, 128, 128, std=0.1)
+    pq, pk = l2n(randn(S, Hk, 128)), l2n(randn(S, Hk, 128))
+    pv = randn(S, Hv, 128)
+    pa, pb = randn(S, Hv), randn(S, Hv)
+    pdt = randn(Hv)
+    pA = torch.exp(torch.rand(Hv, generator=g, device=dev) * math.log(16.0))
+    us = _gpu_us(torch, lambda: anelm.ops.deltanet_prefill(st, pq, pk, pv, pa, pb, pA, pdt, 1), 10)
+    r = _hbm(us, 206569472)
+    r["GFLOPs_recurrent_form"] = round(15.03e9 / (us * 1e-6) / 1e9, 1)
+    res["deltanet_prefill_4096"] = r
+    del pq, pk, pv, pa, pb
+
+    # 32-sequence batched decode, per layer: paged attention over ragged
+    # lengths U[256, 16384] (16-token pages, shuffled page table) ...
+    rng = np.random.default_rng(seed)
+    n_seq, P = 32, 16
+    lens = rng.integers(256, 16385, n_seq).astype(np.int32)
+    npg = (lens + P - 1) // P
+    n_pages = int(npg.sum())
+    perm = rng.permutation(n_pages).astype(np.int32)
+    table = np.zeros((n_seq, int(npg.max())), np.int32)
+    off = 0
+    for s in range(n_seq):
+        table[s, :npg[s]] = perm[off:off + npg[s]]
+        off += npg[s]
+    kp = randn(n_pages, 4, P, 256, dtype=torch.float16)
+    vp = randn(n_pages, 4, P, 256, dtype=torch.float16)
+    qb = randn(n_seq, 16, 256)
+    tb = torch.from_numpy(table).to(dev)
+    lb = torch.from_numpy(lens).to(dev)
+    ob = torch.empty(n_seq, 16, 256, device=dev)
+    us = _gpu_us(torch, lambda: anelm.ops.attn_decode_paged(qb, kp, vp, tb, lb, int(lens.max()), 16, 4, 256, P,
+                                                            out=ob), 10)
+    r = _hbm(us, int(lens.sum()) * 4 * 256 * 2 * 2)
+    r["sum_len"] = int(lens.sum())
+    res["batch32_paged_attention_layer"] = r
+    del kp, vp
+    # ... DeltaNet decode of all 32 sequences in one launch (1024 value heads) ...
+    Hk, Hv = 16 * n_seq, 32 * n_seq
+    st = randn(Hv, 128, 128, std=0.1)
+    bq, bk = l2n(randn(Hk, 128)), l2n(randn(Hk, 128))
+    bv = randn(Hv, 128)
+    ba, bb, bdt = randn(Hv), randn(Hv), randn(Hv)
+    bA = torch.exp(torch.rand(Hv, generator=g, device=dev) * math.log(16.0))
+    by = torch.empty(Hv, 128, device=dev)
+    us = _gpu_us(torch, lambda: anelm.ops.deltanet_decode(st, bq, bk, bv, ba, bb, bA, bdt, 1, out=by), 20)
+    res["batch32_deltanet_layer"] = _hbm(us, Hv * 128 * 128 * 4 * 2 + (2 * Hk + 2 * Hv) * 128 * 4)
+    del st
+    # ... and the LM head: top-32 of a [262144][2560] LUT6 matrix for 32 fp16-valued inputs
+    V, D = 262144, 2560
+    w = torch.randint(0, 256, (V, D * 3 // 4), generator=g, device=dev, dtype=torch.uint8)
+    lut = randn(V // 32, 64, std=0.02, dtype=torch.float16)
+    hx = randn(n_seq, D, dtype=torch.float16).float()
+    us = _gpu_us(torch, lambda: anelm.ops.lut6_topk(w, lut, hx, V, D, 32), 10)
+    res["batch32_lm_head_top32"] = _hbm(us, V * D * 3 // 4 + (V // 32) * 128 + n_seq * D * 4)
+    return res
+
+
 def cpu_baseline(seconds=12.0):
     """The oracle (a single-threaded C restatement of the reference cpu_ops
     path) on a bounded sample of the same step: one block of four layers
@@ -254,6 +400,8 @@ def main():
                     help="decode-step execution (default: persistent, else graph)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-cores", action="store_true",
+                    help="do not time the other workloads (decode/prefill attention, DeltaNet, batched decode)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="after the timed steps, copy MB MiB device-to-device once (a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -302,6 +450,9 @@ def main():
             torch.cuda.synchronize()
             del src, dst
         persistent = bool(mode & anelm.STEP_PERSISTENT)
+        del keep
+        torch.cuda.empty_cache()
+        cores = None if args.skip_cores else measure_cores(anelm, torch, dev)
 
     b = step_bytes()
     gbps = b["total"] / (us_step * 1e-6) / 1e9
@@ -345,6 +496,8 @@ def main():
                               "bytes_per_launch": gu_b, "avg_us": round(gu_avg, 3)}
     result["lut6_gate_up"] = {"avg_us": round(gu_avg, 3), "median_us": round(gu_med, 3),
                               "GBps": round(gu_gbps, 1), "bytes_per_launch": gu_b}
+    if cores is not None:
+        result["cores"] = cores
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result))
