@@ -60,6 +60,12 @@ Device* device();
 // sync + free + malloc).  Returns nullptr on failure with the error recorded.
 void* workspace(size_t bytes, hipStream_t stream);
 
+// Batched LUT6 GEMM on MFMA (lut6_mfma.hip): column split for in_dim, and the
+// launch for batch <= 32 inputs.
+bool lut6_gemm_geometry(int in_dim, int& np, int& waves);
+int lut6_gemm_launch(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                     int in_dim, hipStream_t st);
+
 // `n` zeroed counters on the current device; nullptr if n exceeds the pool.
 uint32_t* counters(size_t n);
 

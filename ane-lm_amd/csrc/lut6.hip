@@ -487,66 +487,93 @@ __device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
     return va > vb || (va == vb && ia < ib);
 }
 
-constexpr int kTopkChunk = 2048;   // logits per selection workgroup
+constexpr int kTopkChunk = 8192;   // logits per selection workgroup (4 waves x 2048)
 
-// Bitonic sort of n (power of two) (value, index) pairs in shared memory,
-// best first.
-__device__ void bitonic_sort(float* v, int* id, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
-            for (int t = threadIdx.x; t < n / 2; t += kNT) {
-                const int lo = 2 * t - (t & (stride - 1));
-                const int hi = lo + stride;
-                const bool desc = ((lo & size) == 0);
-                const bool swap = desc ? before(v[hi], id[hi], v[lo], id[lo])
-                                       : before(v[lo], id[lo], v[hi], id[hi]);
-                if (swap) {
-                    const float tv = v[lo]; v[lo] = v[hi]; v[hi] = tv;
-                    const int ti = id[lo]; id[lo] = id[hi]; id[hi] = ti;
-                }
-            }
-        }
-    }
-    __syncthreads();
+// Wave-resident selection: lane i holds the i-th best (value, index) of the
+// wave's list, best first under `before`; lanes past the list hold (-inf, max).
+struct Cand {
+    float v;
+    int i;
+};
+__device__ __forceinline__ Cand xchg(Cand c, int mask) {
+    return Cand{__shfl_xor(c.v, mask, 64), __shfl_xor(c.i, mask, 64)};
+}
+// One compare-exchange stage of a bitonic network over the 64 lanes: lanes
+// lane and lane ^ stride form a pair; in blocks where (lane & size) == 0 the
+// better element goes to the lower lane, in the others to the upper one.
+__device__ __forceinline__ Cand bitonic_step(Cand c, int lane, int size, int stride) {
+    const Cand p = xchg(c, stride);
+    const bool lower = (lane & stride) == 0;
+    const bool desc = (lane & size) == 0;
+    const bool mine = before(c.v, c.i, p.v, p.i);
+    return (lower == desc) == mine ? c : p;
+}
+// Sorts the 64 lanes' candidates best first.
+__device__ __forceinline__ Cand wave_sort(Cand c, int lane) {
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) c = bitonic_step(c, lane, size, stride);
+    return c;
+}
+// Top 64 of two lists sorted best first: the lane-wise better of L[i] and
+// N[63 - i] is bitonic; a half-cleaner cascade sorts it.
+__device__ __forceinline__ Cand wave_merge(Cand L, Cand N, int lane) {
+    const Cand r = Cand{__shfl(N.v, 63 - lane, 64), __shfl(N.i, 63 - lane, 64)};
+    Cand c = before(L.v, L.i, r.v, r.i) ? L : r;
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) c = bitonic_step(c, lane, 64, stride);
+    return c;
+}
+// Adds 64 unsorted candidates (one per lane) to the list L holding the best k;
+// skipped when none beats the list's k-th entry.
+__device__ __forceinline__ Cand wave_offer(Cand L, Cand c, int lane, int k) {
+    const float tv = __shfl(L.v, k - 1, 64);
+    const int ti = __shfl(L.i, k - 1, 64);
+    if (!__any(before(c.v, c.i, tv, ti))) return L;
+    return wave_merge(L, wave_sort(c, lane), lane);
 }
 
-// Stage 1: each workgroup sorts one chunk of one batch row's logits and keeps
-// the best k as candidates [batch][n_chunks][k].
-__global__ __launch_bounds__(kNT) void topk_stage1(const float* logits, int n, int k, int n_chunks,
+// Stage 1: each workgroup selects the best k of one chunk of one batch row's
+// logits -- every wave keeps a running list over its quarter, then wave 0
+// merges the four lists -- into candidates [batch][n_chunks][k].
+__global__ __launch_bounds__(256) void topk_stage1(const float* logits, int n, int k, int n_chunks,
                                                    float* cv, int* ci) {
-    __shared__ float v[kTopkChunk];
-    __shared__ int id[kTopkChunk];
+    __shared__ Cand lists[4][64];
     const int chunk = blockIdx.x, b = blockIdx.y;
-    const int base = chunk * kTopkChunk;
-    for (int t = threadIdx.x; t < kTopkChunk; t += kNT) {
-        const int r = base + t;
-        v[t] = (r < n) ? logits[(size_t)b * n + r] : -INFINITY;
-        id[t] = (r < n) ? r : 0x7fffffff;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float* row = logits + (size_t)b * n;
+    Cand L{-INFINITY, 0x7fffffff};
+    const int base = chunk * kTopkChunk + w * (kTopkChunk / 4);
+    for (int j = 0; j < kTopkChunk / 4; j += 64) {
+        const int r = base + j + lane;
+        const Cand c = r < n ? Cand{row[r], r} : Cand{-INFINITY, 0x7fffffff};
+        L = wave_offer(L, c, lane, k);
     }
-    bitonic_sort(v, id, kTopkChunk);
-    for (int t = threadIdx.x; t < k; t += kNT) {
-        cv[((size_t)b * n_chunks + chunk) * k + t] = v[t];
-        ci[((size_t)b * n_chunks + chunk) * k + t] = id[t];
+    lists[w][lane] = L;
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int o = 1; o < 4; o++) L = wave_merge(L, lists[o][lane], lane);
+    if (lane < k) {
+        cv[((size_t)b * n_chunks + chunk) * k + lane] = L.v;
+        ci[((size_t)b * n_chunks + chunk) * k + lane] = L.i;
     }
 }
 
-// Stage 2: one workgroup per batch row sorts all candidates (padded to a
-// power of two) and writes the best k.
-__global__ __launch_bounds__(kNT) void topk_stage2(const float* cv, const int* ci, int n_cand, int np2,
-                                                   int k, int32_t* out_idx, float* out_val) {
-    extern __shared__ float sm[];
-    float* v = sm;
-    int* id = reinterpret_cast<int*>(sm + np2);
-    const int b = blockIdx.x;
-    for (int t = threadIdx.x; t < np2; t += kNT) {
-        v[t] = (t < n_cand) ? cv[(size_t)b * n_cand + t] : -INFINITY;
-        id[t] = (t < n_cand) ? ci[(size_t)b * n_cand + t] : 0x7fffffff;
+// Stage 2: one wave per batch row merges the rows' chunk candidates.
+__global__ __launch_bounds__(64) void topk_stage2(const float* cv, const int* ci, int n_chunks, int k,
+                                                  int32_t* out_idx, float* out_val) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    Cand L{-INFINITY, 0x7fffffff};
+    for (int c = 0; c < n_chunks; c++) {
+        const size_t o = ((size_t)b * n_chunks + c) * k;
+        const Cand n = lane < k ? Cand{cv[o + lane], ci[o + lane]} : Cand{-INFINITY, 0x7fffffff};
+        L = wave_merge(L, n, lane);   // chunk lists arrive sorted
     }
-    bitonic_sort(v, id, np2);
-    for (int t = threadIdx.x; t < k; t += kNT) {
-        out_idx[(size_t)b * k + t] = id[t];
-        out_val[(size_t)b * k + t] = v[t];
+    if (lane < k) {
+        out_idx[(size_t)b * k + lane] = L.i;
+        out_val[(size_t)b * k + lane] = L.v;
     }
 }
 
@@ -662,6 +689,28 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
     return gemv_dispatch<kStageCopy>(a, 1, st);
 }
 
+// Y[b] = W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs where the
+// column count fits its register-resident window, else one GEMV per input.
+int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                 int in_dim, hipStream_t st) {
+    int np = 0, waves = 0;
+    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (aligned && lut6_gemm_geometry(in_dim, np, waves)) {
+        for (int b0 = 0; b0 < batch; b0 += 32) {
+            const int nb = batch - b0 < 32 ? batch - b0 : 32;
+            const int rc = lut6_gemm_launch(y + (size_t)b0 * out_dim, w, lut, x + (size_t)b0 * in_dim, nb, out_dim,
+                                            in_dim, st);
+            if (rc) return rc;
+        }
+        return ANELM_OK;
+    }
+    for (int b = 0; b < batch; b++) {
+        const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, 0, st);
+        if (rc) return rc;
+    }
+    return ANELM_OK;
+}
+
 }  // namespace
 }  // namespace anelm
 
@@ -747,6 +796,18 @@ int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
     return gemv(x, down_w, down_lut, h, hidden, inter, 1, st);
 }
 
+int anelm_lut6_gemm(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                    int in_dim, void* stream) {
+    ANELM_NONNULL(y);
+    ANELM_NONNULL(w);
+    ANELM_NONNULL(lut);
+    ANELM_NONNULL(x);
+    int rc = check_shape(out_dim, in_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(batch > 0, "lut6_gemm: batch %d", batch);
+    return batched_gemv(y, w, lut, x, batch, out_dim, in_dim, as_stream(stream));
+}
+
 int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
                     const float* x, int batch, int out_dim, int in_dim, int k, void* stream) {
     ANELM_NONNULL(out_idx);
@@ -761,9 +822,6 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     hipStream_t st = as_stream(stream);
     const int n_chunks = (out_dim + kTopkChunk - 1) / kTopkChunk;
     const int n_cand = n_chunks * k;
-    int np2 = 1;
-    while (np2 < n_cand) np2 <<= 1;
-    ANELM_REQUIRE(np2 <= 8192, "lut6_topk: %d candidates exceed the merge limit", n_cand);
     const size_t logits_bytes = (size_t)batch * out_dim * sizeof(float);
     const size_t cand_bytes = (size_t)batch * n_cand * (sizeof(float) + sizeof(int));
     char* ws = static_cast<char*>(workspace(logits_bytes + cand_bytes, st));
@@ -771,15 +829,12 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     float* logits = reinterpret_cast<float*>(ws);
     float* cv = reinterpret_cast<float*>(ws + logits_bytes);
     int* ci = reinterpret_cast<int*>(ws + logits_bytes + (size_t)batch * n_cand * sizeof(float));
-    for (int b = 0; b < batch; b++) {
-        rc = gemv(logits + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, 0, st);
-        if (rc) return rc;
-    }
-    hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(kNT), 0, st, logits, out_dim, k,
+    rc = batched_gemv(logits, w, lut, x, batch, out_dim, in_dim, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(256), 0, st, logits, out_dim, k,
                        n_chunks, cv, ci);
     ANELM_LAUNCHED("topk_stage1");
-    hipLaunchKernelGGL(topk_stage2, dim3(batch), dim3(kNT), (size_t)np2 * 8, st, cv, ci, n_cand,
-                       np2, k, out_idx, out_val);
+    hipLaunchKernelGGL(topk_stage2, dim3(batch), dim3(64), 0, st, cv, ci, n_chunks, k, out_idx, out_val);
     ANELM_LAUNCHED("topk_stage2");
     return ANELM_OK;
 }

@@ -1,0 +1,301 @@
+// Batched LUT6 GEMM on fp16 MFMA: Y[b][r] = sum_c W[r][c] * X[b][c] for up to
+// 32 input vectors at once, each 32-row LUT group of W decoded ONCE for all of
+// them.  Used by the LM head (top-k over the logits of a batch of hidden
+// states, scripts/export_hybrid_chunks.py:409-421) and by batched LUT6
+// projections; a batch of one goes through the same path.
+//
+// Mapping (v_mfma_f32_32x32x16_f16, A = 32 weight rows x 16 columns, B = 16
+// columns x 32 batch vectors, C = 32 rows x 32 vectors):
+//   * a workgroup walks 32-row groups g (one LUT per group); its NW waves split
+//     the columns: wave w owns the window [w*128*NP, (w+1)*128*NP);
+//   * lane l = (m, hh), m = l % 32, hh = l / 32, feeds weight row m and batch
+//     vector m; MFMA step t of the wave contracts columns
+//     w*128*NP + hh*64*NP + 8t + j (j < 8).  The contraction order over the
+//     columns is permuted identically in A and B, so each lane's weights are
+//     one contiguous 48*NP-byte stretch of its row;
+//   * the wave's X window sits in registers for the whole launch (fp16, as the
+//     LUT6 path takes its activations); weights are double-buffered in
+//     registers one group ahead; each 12-bit field (two indices) dequantises
+//     through a 4096-entry pair table T[(i1 << 6) | i0] = (lut[i0], lut[i1])
+//     built per group in LDS (double-buffered);
+//   * the NW partial 32x32 tiles are summed through LDS and written as fp32.
+// Reference math: matvec (core/cpu_ops.cpp:77-80) on the dequantised weights.
+#include "anelm_internal.hpp"
+
+namespace anelm {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxWaves = 16;
+constexpr int kTabBytes = 4096 * 4;
+constexpr int kLutSlots = 64;                          // LUTs staged per round
+constexpr int kLutOff = 2 * kTabBytes;                 // staged LUTs [kLutSlots][64] u16
+constexpr int kRedOff = kLutOff + kLutSlots * 128;     // partial tiles [NW][16][kRedRow] f32
+// Partial-tile row: lane l of accumulator e sits at (l % 32) + 33 * (l / 32)
+// of a 66-float row, so the reduction's reads (32 threads of one vector n:
+// all 16 e x 2 half-waves) fall on 32 distinct banks, and so do the writes.
+constexpr int kRedRow = 66;
+__device__ __forceinline__ int red_pos(int e, int l) { return e * kRedRow + (l & 31) + 33 * (l >> 5); }
+
+struct GemmArgs {
+    float* y;              // [batch][out_dim]
+    const uint8_t* w;      // [out_dim][in_dim * 3 / 4]
+    const uint16_t* lut;   // [out_dim / 32][64]
+    const float* x;        // [batch][in_dim]
+    int batch, out_dim, in_dim;
+};
+
+// Pair-table byte offset of pair p (indices 2p, 2p + 1: the 12-bit field at
+// bit 12p of the lane's weight words), OR-ed with the table base tb.  p is a
+// compile-time constant after unrolling, so the shifts and word picks fold.
+template <int NWD>
+__device__ __forceinline__ uint32_t pair_off(const uint32_t (&wd)[NWD], int p, uint32_t tb) {
+    const int s = 12 * p - 2;                  // field lands at bit 2 (4 bytes per entry)
+    uint32_t v;
+    if (s < 0) {
+        v = wd[0] << 2;
+    } else {
+        const int d = s >> 5, sh = s & 31;
+        if (sh + 14 <= 32 || d + 1 >= NWD) v = wd[d] >> sh;
+        else v = __builtin_amdgcn_alignbit(wd[d + 1], wd[d], sh);
+    }
+    return (v & 0x3FFCu) | tb;
+}
+
+template <int NP>
+__device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w,
+                                             int lane) {
+    const int m = lane & 31, hh = lane >> 5;
+    const size_t row_bytes = (size_t)a.in_dim * 3 / 4;
+    const u32x4* p = reinterpret_cast<const u32x4*>(a.w + ((size_t)g * 32 + m) * row_bytes +
+                                                    (size_t)w * 96 * NP + hh * 48 * NP);
+#pragma unroll
+    for (int i = 0; i < 3 * NP; i++) {
+        const u32x4 v = __builtin_nontemporal_load(p + i);
+        wd[4 * i] = v.x;
+        wd[4 * i + 1] = v.y;
+        wd[4 * i + 2] = v.z;
+        wd[4 * i + 3] = v.w;
+    }
+}
+
+// Dequantise this lane's 64*NP indices through the pair table at byte offset
+// tb and accumulate the wave's 8*NP MFMA steps into c.
+template <int NP>
+__device__ __forceinline__ void group_mfma(float16_t& c, const uint32_t (&wd)[12 * NP],
+                                           const half8 (&xb)[8 * NP], const char* lds, uint32_t tb) {
+#pragma unroll
+    for (int t = 0; t < 8 * NP; t++) {
+        u32x4 av;
+        av.x = *reinterpret_cast<const uint32_t*>(lds + pair_off(wd, 4 * t + 0, tb));
+        av.y = *reinterpret_cast<const uint32_t*>(lds + pair_off(wd, 4 * t + 1, tb));
+        av.z = *reinterpret_cast<const uint32_t*>(lds + pair_off(wd, 4 * t + 2, tb));
+        av.w = *reinterpret_cast<const uint32_t*>(lds + pair_off(wd, 4 * t + 3, tb));
+        c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av), xb[t], c, 0, 0, 0);
+    }
+}
+
+// Workgroup barrier for LDS exchange only: this wave's LDS operations
+// complete, then s_barrier.  __syncthreads() would also wait for every vector
+// memory load in flight -- the next group's weights, prefetched one group
+// ahead -- at each of the two barriers per group.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Builds the pair table of the workgroup's j-th group (LUT staged in LDS at
+// kLutOff) into table `slot`: wave w writes rows i1 = w, w + nw, ... of 64
+// entries, lane i0 holding lut[i0].
+__device__ __forceinline__ void build_table(char* lds, int slot, int j, int w, int nw, int lane) {
+    const uint16_t* l = reinterpret_cast<const uint16_t*>(lds + kLutOff) + (j & (kLutSlots - 1)) * 64;
+    uint32_t* tab = reinterpret_cast<uint32_t*>(lds + slot * kTabBytes);
+    const uint32_t mine = l[lane];
+    for (int i1 = w; i1 < 64; i1 += nw) tab[i1 * 64 + lane] = mine | ((uint32_t)l[i1] << 16);
+}
+
+// Stages the LUTs of the workgroup's groups j0 .. j0 + kLutSlots - 1 (group
+// index blockIdx.x + j * gridDim.x, clamped) into LDS.  Called with every
+// wave between two barriers.
+__device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0, int tid, int nt) {
+    uint16_t* l = reinterpret_cast<uint16_t*>(lds + kLutOff);
+    const int last = a.out_dim / 32 - 1;
+    for (int e = tid; e < kLutSlots * 64; e += nt) {
+        const int g = min((int)blockIdx.x + (j0 + (e >> 6)) * (int)gridDim.x, last);
+        l[e] = a.lut[(size_t)g * 64 + (e & 63)];
+    }
+}
+
+// Sums the NW partial tiles of group g and writes Y[n][32g + m] for n < batch.
+// Thread t handles (n = t / 32, m = t % 32): consecutive threads write
+// consecutive rows of one output vector.
+// The trip count is a compile-time constant, so every thread issues the same
+// number of stores per group: the compiler can then count the vector-memory
+// events between a weight prefetch and its use (stores count too) and leave
+// the prefetch in flight.
+// Stores are raw buffer stores over y: an element outside the batch gets an
+// offset past the buffer's end, which the hardware drops, so the store is
+// issued by every thread without a branch.
+template <int NW>
+__device__ __forceinline__ void reduce_store(const GemmArgs& a, int g, const char* lds, int tid) {
+    constexpr int NT = NW * 64;
+    const float* red = reinterpret_cast<const float*>(lds + kRedOff);
+    const uint32_t bytes = (uint32_t)a.batch * (uint32_t)a.out_dim * 4u;
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, (int)bytes, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < (1024 + NT - 1) / NT; k++) {
+        const int t = tid + k * NT;
+        const int n = t >> 5, m = t & 31;
+        // C layout: accumulator e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, vector l%32
+        const int hh = (m >> 2) & 1, e = 4 * (m >> 3) + (m & 3), l = (n & 31) + 32 * hh;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) s += red[w * 16 * kRedRow + red_pos(e, l)];
+        const uint32_t off = (t < 1024 && n < a.batch) ? ((uint32_t)n * (uint32_t)a.out_dim + (uint32_t)g * 32u +
+                                                            (uint32_t)m) * 4u
+                                                         : bytes;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s), ry, (int)off, 0, 0);
+    }
+}
+
+// NP = 2: 64 registers of X per lane; NP = 1: 32.
+template <int NP, int NW>
+__global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    constexpr int nt = NW * 64, nw = NW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = tid >> 6;
+    const int n_groups = a.out_dim / 32;
+    int g = blockIdx.x;
+    if (g >= n_groups) return;
+
+    // the wave's X window as MFMA B operands (fp16), zero for vectors >= batch
+    half8 xb[8 * NP];
+    {
+        const int n = lane & 31, hh = lane >> 5;
+        const float* xr = a.x + (size_t)n * a.in_dim + (size_t)w * 128 * NP + hh * 64 * NP;
+#pragma unroll
+        for (int t = 0; t < 8 * NP; t++) {
+            half8 v = half8{};
+            if (n < a.batch) {
+                const float4 lo = *reinterpret_cast<const float4*>(xr + 8 * t);
+                const float4 hi = *reinterpret_cast<const float4*>(xr + 8 * t + 4);
+                v = half8{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                          (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+            }
+            xb[t] = v;
+        }
+    }
+    // Software pipeline, one group ahead: while group g is multiplied from
+    // registers wa (table slot 0), group gn's LUT and weights are in flight
+    // into lr / wb, its table is built into slot 1 after the products, and the
+    // roles swap for the next group.  The LUT load is issued before the
+    // weights, so waiting for it never waits for them; loads past the last
+    // group repeat the last group (clamped, never used).
+    const int stride = gridDim.x, last = n_groups - 1;
+    uint32_t wa[12 * NP], wb[12 * NP];
+    load_weights<NP>(wa, a, g, w, lane);
+    stage_luts(a, lds, 0, tid, nt);
+    lds_barrier();
+    build_table(lds, 0, 0, w, nw, lane);
+    load_weights<NP>(wb, a, min(g + stride, last), w, lane);
+    float* red = reinterpret_cast<float*>(lds + kRedOff);
+    // j counts the workgroup's groups; LUTs are restaged every kLutSlots groups
+    for (int j = 0;; j += 2) {
+        lds_barrier();                                 // table 0 ready; red free
+        {
+            float16_t c = float16_t{};
+            group_mfma<NP>(c, wa, xb, lds, 0u);
+#pragma unroll
+            for (int e = 0; e < 16; e++) red[w * 16 * kRedRow + red_pos(e, lane)] = c[e];
+        }
+        build_table(lds, 1, j + 1, w, nw, lane);      // next group (table 1 is free since the last barrier)
+        lds_barrier();                                 // partial tiles and table 1 complete
+        reduce_store<NW>(a, g, lds, tid);
+        g += stride;
+        if (g >= n_groups) break;
+        load_weights<NP>(wa, a, min(g + stride, last), w, lane);
+        lds_barrier();                                 // table 1 ready; red free
+        {
+            float16_t c = float16_t{};
+            group_mfma<NP>(c, wb, xb, lds, (uint32_t)kTabBytes);
+#pragma unroll
+            for (int e = 0; e < 16; e++) red[w * 16 * kRedRow + red_pos(e, lane)] = c[e];
+        }
+        if (((j + 2) & (kLutSlots - 1)) == 0) {
+            // restage the next kLutSlots LUTs (every 64 groups of this workgroup)
+            lds_barrier();
+            stage_luts(a, lds, j + 2, tid, nt);
+            lds_barrier();
+        }
+        build_table(lds, 0, j + 2, w, nw, lane);
+        lds_barrier();
+        reduce_store<NW>(a, g, lds, tid);
+        g += stride;
+        if (g >= n_groups) break;
+        load_weights<NP>(wb, a, min(g + stride, last), w, lane);
+    }
+}
+
+}  // namespace
+
+// Column split for the GEMM: NP (1 or 2) and the wave count in_dim / (128 NP).
+// NP = 2 (256 columns per wave) up to 10 waves; otherwise NP = 1 (128 columns
+// per wave, an odd number of waves up to 15).
+bool lut6_gemm_geometry(int in_dim, int& np, int& waves) {
+    if (in_dim % 256 == 0 && in_dim / 256 <= 10) {
+        np = 2;
+        waves = in_dim / 256;
+        return true;
+    }
+    if (in_dim % 128 == 0 && (in_dim / 128) % 2 == 1 && in_dim / 128 <= 15) {
+        np = 1;
+        waves = in_dim / 128;
+        return true;
+    }
+    return false;
+}
+
+// Y[b][r] for b < batch (batch <= 32), out_dim % 32 == 0, in_dim accepted by
+// lut6_gemm_geometry.  Shapes are validated by the caller.
+int lut6_gemm_launch(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                     int in_dim, hipStream_t st) {
+    int np = 0, waves = 0;
+    if (!lut6_gemm_geometry(in_dim, np, waves) || batch < 1 || batch > 32 || out_dim % 32 ||
+        (long long)batch * out_dim * 4 >= (1LL << 31))
+        return set_error(ANELM_EINVAL, "lut6_gemm: unsupported shape batch %d out %d in %d", batch, out_dim,
+                         in_dim);
+    Device* dev = device();
+    if (!dev) return ANELM_EHIP;
+    GemmArgs a{y, w, lut, x, batch, out_dim, in_dim};
+    const int n_groups = out_dim / 32;
+    const int grid = n_groups < dev->num_cus ? n_groups : dev->num_cus;
+    const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float);
+    using K = void (*)(GemmArgs);
+    static const K k2[11] = {nullptr, lut6_gemm_kernel<2, 1>, lut6_gemm_kernel<2, 2>, lut6_gemm_kernel<2, 3>,
+                             lut6_gemm_kernel<2, 4>, lut6_gemm_kernel<2, 5>, lut6_gemm_kernel<2, 6>,
+                             lut6_gemm_kernel<2, 7>, lut6_gemm_kernel<2, 8>, lut6_gemm_kernel<2, 9>,
+                             lut6_gemm_kernel<2, 10>};
+    static const K k1[16] = {nullptr, lut6_gemm_kernel<1, 1>, nullptr, lut6_gemm_kernel<1, 3>, nullptr,
+                             lut6_gemm_kernel<1, 5>, nullptr, lut6_gemm_kernel<1, 7>, nullptr,
+                             lut6_gemm_kernel<1, 9>, nullptr, lut6_gemm_kernel<1, 11>, nullptr,
+                             lut6_gemm_kernel<1, 13>, nullptr, lut6_gemm_kernel<1, 15>};
+    const K kp = np == 2 ? k2[waves] : k1[waves];
+    if (!kp) return set_error(ANELM_EINVAL, "lut6_gemm: no kernel for %d waves (np %d)", waves, np);
+    static bool attr_set[2][16] = {};
+    if (!attr_set[np - 1][waves]) {
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kp), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lds));
+        attr_set[np - 1][waves] = true;
+    }
+    hipLaunchKernelGGL(kp, dim3(grid), dim3(waves * 64), lds, st, a);
+    ANELM_LAUNCHED("lut6_gemm_kernel");
+    return ANELM_OK;
+}
+
+}  // namespace anelm

@@ -228,6 +228,14 @@ def lut6_gate_up(x, norm_w, eps, gate, up, hidden, inter):
     return g, u
 
 
+def lut6_gemm(w, lut, x, out_dim, in_dim, out=None):
+    """y[b] = W x[b] for a batch x [batch][in_dim] (weights dequantised once per 32 inputs)."""
+    batch = x.shape[0]
+    out = torch.empty(batch, out_dim, device=x.device, dtype=_F32) if out is None else out
+    call("anelm_lut6_gemm", _p(out), _p(w), _p(lut), _p(x), batch, out_dim, in_dim, _s())
+    return out
+
+
 def lut6_topk(w, lut, x, out_dim, in_dim, k):
     batch = x.shape[0] if x.dim() == 2 else 1
     idx = torch.empty(batch, k, device=x.device, dtype=torch.int32)

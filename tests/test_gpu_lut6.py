@@ -50,6 +50,24 @@ def test_ffn_block(anelm, orc, dev, hidden, inter):
     assert_close(to_host(xd), x + orc.lut6_ffn(x, g[:2], u[:2], d[:2], hidden, inter))
 
 
+@pytest.mark.parametrize("out_dim,in_dim,batch", [(9216, 2560, 32), (2560, 2560, 1), (4096, 1024, 5),
+                                                  (512, 1280, 33), (256, 128, 7), (1024, 2048, 64),
+                                                  (96, 2176, 3)])
+def test_gemm_batched(anelm, orc, dev, out_dim, in_dim, batch):
+    """Batched projection y[b] = W x[b]: the MFMA path (column windows of 128 or
+    256 per wave, tiles of 32 inputs, ragged last tile) and the per-input
+    fallback (2176 columns do not fit the register-resident window)."""
+    packed, lut, _ = lut6_matrix(640 + in_dim, out_dim, in_dim)
+    x = np.random.default_rng(641 + batch).standard_normal((batch, in_dim)).astype(np.float32)
+    got = to_host(anelm.ops.lut6_gemm(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim, in_dim))
+    for b in sorted({0, batch // 2, batch - 1}):
+        want = orc.lut6_matvec(packed, lut, x[b], out_dim, in_dim)
+        assert_close(got[b], want, what=f"{out_dim}x{in_dim} input {b}")
+    # repeated call: same bits (no state carried between launches)
+    again = to_host(anelm.ops.lut6_gemm(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim, in_dim))
+    assert np.array_equal(got, again)
+
+
 def _check_topk(orc, idx, val, logits, k):
     """Indices bit-exact against the oracle's top-k of the oracle logits
     wherever neighbouring values are separated by more than the fp32
@@ -69,14 +87,14 @@ def _check_topk(orc, idx, val, logits, k):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,batch,k", [(262144, 2560, 2, 32), (4096, 1024, 3, 64),
-                                                    (8192, 2560, 1, 1)])
+                                                    (8192, 2560, 1, 1), (262144, 2560, 32, 32)])
 def test_topk(anelm, orc, dev, out_dim, in_dim, batch, k):
     packed, lut, _ = lut6_matrix(620 + k, out_dim, in_dim)
     x = np.random.default_rng(621).standard_normal((batch, in_dim)).astype(np.float32)
     idx, val = anelm.ops.lut6_topk(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim,
                                    in_dim, k)
     idx, val = to_host(idx), to_host(val)
-    for b in range(batch):
+    for b in (range(batch) if batch <= 3 else (0, batch // 2, batch - 1)):
         logits = orc.lut6_matvec(packed, lut, x[b], out_dim, in_dim)
         _check_topk(orc, idx[b], val[b], logits, k)
         if k == 1:
