@@ -60,6 +60,18 @@ Device* device();
 // sync + free + malloc).  Returns nullptr on failure with the error recorded.
 void* workspace(size_t bytes, hipStream_t stream);
 
+// Workgroup barrier for LDS exchange only: this wave's LDS operations
+// complete, then s_barrier.  __syncthreads() also carries a release fence that
+// makes the compiler wait for every vector-memory operation of the wave
+// (vmcnt(0)), which drains any global prefetch issued before the barrier.
+// Use this one where the barrier only orders LDS accesses.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Batched LUT6 GEMM on MFMA (lut6_mfma.hip): column split for in_dim, and the
 // launch for batch <= 32 inputs.
 bool lut6_gemm_geometry(int in_dim, int& np, int& waves);

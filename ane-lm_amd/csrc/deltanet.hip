@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kSeqNT) void dn_chunk_seq_kernel(float* __restrict_
         }
         // ---- U = Ut - Wm S0
         dn_seq_park(M[buf], nxt, tid);
-        __syncthreads();
+        lds_barrier();
         dn_seq_fetch(nxt, rc + 3 * kCMat, tid);                 // Qh
         dn_seq_rowdot(part, M[buf], s, rb);
         if (lead) {
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(kSeqNT) void dn_chunk_seq_kernel(float* __restrict_
         }
         buf ^= 1;
         dn_seq_park(M[buf], nxt, tid);
-        __syncthreads();
+        lds_barrier();
         dn_seq_fetch(nxt, rc + 4 * kCMat, tid);                 // Kh
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -490,14 +490,14 @@ __global__ __launch_bounds__(kSeqNT) void dn_chunk_seq_kernel(float* __restrict_
         }
         // ---- y = Op + Qh S0
         dn_seq_rowdot(part, M[buf], s, rb);
-        __syncthreads();   // red consumed by the U rows above
+        lds_barrier();   // red consumed by the U rows above
         if (lead) {
 #pragma unroll
             for (int t = 0; t < kChunk; t++) red[w][t][c] = part[t];
         }
         buf ^= 1;
         dn_seq_park(M[buf], nxt, tid);
-        __syncthreads();
+        lds_barrier();
         if (ch + 1 < n_chunks) dn_seq_fetch(nxt, rc + (size_t)Hv * kCRec + kCMat, tid);   // next Wm
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(kSeqNT) void dn_chunk_seq_kernel(float* __restrict_
             s[0] = fmaf(k0.x, uv, s[0]); s[1] = fmaf(k0.y, uv, s[1]); s[2] = fmaf(k0.z, uv, s[2]); s[3] = fmaf(k0.w, uv, s[3]);
             s[4] = fmaf(k1.x, uv, s[4]); s[5] = fmaf(k1.y, uv, s[5]); s[6] = fmaf(k1.z, uv, s[6]); s[7] = fmaf(k1.w, uv, s[7]);
         }
-        __syncthreads();   // Ul, red and M[buf] are rewritten in the next chunk
+        lds_barrier();   // Ul, red and M[buf] are rewritten in the next chunk
         buf ^= 1;
     }
 #pragma unroll

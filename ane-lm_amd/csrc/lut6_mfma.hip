@@ -98,17 +98,6 @@ __device__ __forceinline__ void group_mfma(float16_t& c, const uint32_t (&wd)[12
     }
 }
 
-// Workgroup barrier for LDS exchange only: this wave's LDS operations
-// complete, then s_barrier.  __syncthreads() would also wait for every vector
-// memory load in flight -- the next group's weights, prefetched one group
-// ahead -- at each of the two barriers per group.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt unchanged
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // Builds the pair table of the workgroup's j-th group (LUT staged in LDS at
 // kLutOff) into table `slot`: wave w writes rows i1 = w, w + nw, ... of 64
 // entries, lane i0 holding lut[i0].

@@ -81,7 +81,8 @@ constexpr int kLdsTab = 0;            // 6 pair tables x 16 KiB (GEMV); attentio
 constexpr int kLdsXs = 98304;         // fp16 x pairs [8][C], C <= 768
 constexpr int kLdsMisc = 122880;      // 16 KiB of per-phase small buffers
 constexpr int kLdsCtl = 139008;       // control ints (last 256 bytes)
-constexpr int kLdsBytes = 139264;
+constexpr int kLdsXpark = 139264;    // fp32 x [H <= 2560] staged for the next gate/up GEMV
+constexpr int kLdsBytes = kLdsXpark + 10240;
 
 constexpr int kAttnD = 256;           // head_dim of the persistent attention core
 constexpr int kAttnG = 4;             // q heads per kv head
@@ -510,9 +511,38 @@ __device__ __forceinline__ float h16(uint32_t w, int hi) {
     return (float)__builtin_bit_cast(half2_t, w)[hi];
 }
 
-// Control wave: q norm + RoPE for the kv head's 4 q heads; if this split holds
-// the newest key, k norm + RoPE and the fp16 ring append of k and v.
-__device__ void attn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
+// Control wave, two parts.  attn_stage_load reads this step's inputs of the
+// kv head (4 q rows, the new k and v, the norm weights and this lane's RoPE
+// pair) into registers -- constants of the step, so they are issued before
+// the barrier the core waits on.  attn_stage_fin, after the barrier: q norm +
+// RoPE for the 4 q heads; if this split holds the newest key, k norm + RoPE
+// and the fp16 ring append of k and v.
+struct AttnStage {
+    float q[kAttnG][4];
+    float k[4], v[4], qw[4], kw[4];
+    float cs, sn;
+};
+__device__ __forceinline__ void attn_stage_load(const PArgs& a, const PLayer& L, int lane, AttnStage& r) {
+    const int kvh = blockIdx.x / a.splits;
+    if (kvh >= a.Hkv) return;
+#pragma unroll
+    for (int g = 0; g < kAttnG; g++) {
+        const float4 t = *reinterpret_cast<const float4*>(L.q_gate + (size_t)(kvh * kAttnG + g) * 2 * kAttnD + 4 * lane);
+        r.q[g][0] = t.x; r.q[g][1] = t.y; r.q[g][2] = t.z; r.q[g][3] = t.w;
+    }
+    const float4 k = *reinterpret_cast<const float4*>(L.k + (size_t)kvh * kAttnD + 4 * lane);
+    const float4 v = *reinterpret_cast<const float4*>(L.v + (size_t)kvh * kAttnD + 4 * lane);
+    const float4 qw = *reinterpret_cast<const float4*>(L.q_norm_w + 4 * lane);
+    const float4 kw = *reinterpret_cast<const float4*>(L.k_norm_w + 4 * lane);
+    r.k[0] = k.x; r.k[1] = k.y; r.k[2] = k.z; r.k[3] = k.w;
+    r.v[0] = v.x; r.v[1] = v.y; r.v[2] = v.z; r.v[3] = v.w;
+    r.qw[0] = qw.x; r.qw[1] = qw.y; r.qw[2] = qw.z; r.qw[3] = qw.w;
+    r.kw[0] = kw.x; r.kw[1] = kw.y; r.kw[2] = kw.z; r.kw[3] = kw.w;
+    const int j = lane < a.rot_pairs ? lane : 0;
+    r.cs = L.rope[j];
+    r.sn = L.rope[a.rot_pairs + j];
+}
+__device__ void attn_stage_fin(const PArgs& a, const PLayer& L, int lane, char* lds, const AttnStage& r) {
     const int wg = blockIdx.x;
     const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
     int* flags = reinterpret_cast<int*>(lds + kAflagOff);
@@ -521,33 +551,32 @@ __device__ void attn_stage(const PArgs& a, const PLayer& L, int lane, char* lds)
     const bool owner = t_new >= 0 && t_new < a.kps;
     if (lane == 0) flags[0] = owner ? t_new : -1;
     float* qs = reinterpret_cast<float*>(lds + kAqOff);
-    const float* cs = L.rope;
-    const float* sn = L.rope + a.rot_pairs;
     // rows: 4 q heads, then (owner) the new key
-    for (int row = 0; row < kAttnG + (owner ? 1 : 0); row++) {
+#pragma unroll
+    for (int row = 0; row <= kAttnG; row++) {
         const bool isk = row == kAttnG;
-        const float* src = isk ? L.k + (size_t)kvh * kAttnD
-                               : L.q_gate + (size_t)(kvh * kAttnG + row) * 2 * kAttnD;
-        const float* w = isk ? L.k_norm_w : L.q_norm_w;
-        float v[4];
+        if (isk && !owner) break;
+        float v[4], w[4];
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            v[i] = src[4 * lane + i];
+            v[i] = isk ? r.k[i] : r.q[row < kAttnG ? row : 0][i];
+            w[i] = isk ? r.kw[i] : r.qw[i];
             ss += v[i] * v[i];
         }
         ss = wave_sum(ss);
         const float inv = 1.0f / sqrtf(ss / (float)kAttnD + a.eps);
         float* dst = isk ? reinterpret_cast<float*>(lds + kAscOff) : qs + row * kAttnD;  // k temp in sc
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[4 * lane + i] = (v[i] * inv) * w[4 * lane + i];
+        for (int i = 0; i < 4; i++) dst[4 * lane + i] = (v[i] * inv) * w[i];
         // RoPE pairs (core/cpu_ops.cpp:40-63): interleaved (2j, 2j+1) or half-split (j, j+rot/2)
-        for (int j = lane; j < a.rot_pairs; j += 64) {
+        if (lane < a.rot_pairs) {
+            const int j = lane;
             const int i0 = a.rope_mode == 0 ? 2 * j : j;
             const int i1 = a.rope_mode == 0 ? 2 * j + 1 : j + a.rot_pairs;
             const float v0 = dst[i0], v1 = dst[i1];
             float o0, o1;
-            rotate_pair(o0, o1, v0, v1, cs[j], sn[j]);
+            rotate_pair(o0, o1, v0, v1, r.cs, r.sn);
             dst[i0] = o0;
             dst[i1] = o1;
         }
@@ -561,7 +590,7 @@ __device__ void attn_stage(const PArgs& a, const PLayer& L, int lane, char* lds)
             for (int i = 0; i < 4; i++) {
                 const int d = 4 * lane + i;
                 const uint16_t kh = f2h(dst[d]);
-                const uint16_t vh = f2h(L.v[(size_t)kvh * kAttnD + d]);
+                const uint16_t vh = f2h(r.v[i]);
                 kn[d] = kh;
                 vn[d] = vh;
                 kc[d] = kh;
@@ -803,16 +832,33 @@ __device__ __forceinline__ void dn_prefetch(Buf<kDnBuf>& b, const PArgs& a, cons
 constexpr int kDqOff = kLdsMisc;            // q[128] k[128] v[16] ... beta decay at 384
 constexpr int kDredOff = kLdsMisc + 4096;   // [8][16] partials
 
-// Control wave: l2 norm of q, k (cpu_ops.cpp:82-87), q scale (qwen3_5.cpp:879-887),
-// beta and decay (qwen3_5.cpp:896-898), and this slab's v columns.
-__device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
+// Control wave, two parts.  dn_stage_load reads this step's inputs of the
+// slab (q and k of its key head, its 16 v columns, the gate inputs) into
+// registers before the barrier the core waits on; dn_stage_fin, after it:
+// l2 norm of q, k (cpu_ops.cpp:82-87), q scale (qwen3_5.cpp:879-887), beta and
+// decay (qwen3_5.cpp:896-898) into LDS.
+struct DnStage {
+    float q0, q1, k0, k1, vj, b, av, dt, A;
+};
+__device__ __forceinline__ void dn_stage_load(const PArgs& a, const PLayer& L, int lane, DnStage& r) {
     const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
     if (hd >= a.Hv) return;
     const int kh = hd / (a.Hv / a.Hk);
+    r.q0 = L.dn_q[(size_t)kh * kDnD + lane];
+    r.q1 = L.dn_q[(size_t)kh * kDnD + 64 + lane];
+    r.k0 = L.dn_k[(size_t)kh * kDnD + lane];
+    r.k1 = L.dn_k[(size_t)kh * kDnD + 64 + lane];
+    r.vj = L.dn_v[(size_t)hd * kDnD + kDnCols * c + (lane & (kDnCols - 1))];
+    r.b = L.dn_b[hd];
+    r.av = L.dn_a[hd];
+    r.dt = L.dn_dt_bias[hd];
+    r.A = L.dn_A[hd];
+}
+__device__ void dn_stage_fin(const PArgs& a, const PLayer& L, int lane, char* lds, const DnStage& r) {
+    const int hd = blockIdx.x / kDnSlabs;
+    if (hd >= a.Hv) return;
     float* s = reinterpret_cast<float*>(lds + kDqOff);
-    float q0 = L.dn_q[(size_t)kh * kDnD + lane], q1 = L.dn_q[(size_t)kh * kDnD + 64 + lane];
-    float k0 = L.dn_k[(size_t)kh * kDnD + lane], k1 = L.dn_k[(size_t)kh * kDnD + 64 + lane];
-    const float vj = lane < kDnCols ? L.dn_v[(size_t)hd * kDnD + kDnCols * c + lane] : 0.f;
+    float q0 = r.q0, q1 = r.q1, k0 = r.k0, k1 = r.k1;
     if (L.dn_flags & ANELM_DN_L2NORM) {
         const float sq = wave_sum(q0 * q0 + q1 * q1);
         const float sk = wave_sum(k0 * k0 + k1 * k1);
@@ -824,12 +870,12 @@ __device__ void dn_stage(const PArgs& a, const PLayer& L, int lane, char* lds) {
     s[64 + lane] = q1 * qsc;
     s[128 + lane] = k0;
     s[192 + lane] = k1;
-    if (lane < kDnCols) s[256 + lane] = vj;
+    if (lane < kDnCols) s[256 + lane] = r.vj;
     if (lane == 0) {
-        const float beta = 1.0f / (1.0f + expf(-L.dn_b[hd]));
-        const float sp = logf(1.0f + expf(L.dn_a[hd] + L.dn_dt_bias[hd]));
+        const float beta = 1.0f / (1.0f + expf(-r.b));
+        const float sp = logf(1.0f + expf(r.av + r.dt));
         s[384] = beta;
-        s[385] = expf(-L.dn_A[hd] * sp);
+        s[385] = expf(-r.A * sp);
     }
 }
 
@@ -976,12 +1022,13 @@ __device__ void attn_combine(const PArgs& a, const PLayer& L, int layer, char* l
 // owns dwords 8*pos .. 8*pos + 7.  All staging loads go straight to LDS
 // (buffer loads with an LDS destination, 1 KiB per wave instruction), so no
 // registers are held while they are in flight.
-//   stage_w       FFN norm weight (a model constant), fp32 -> wpark, before the barrier;
-//   stage_x_load  x (fp32, device-coherent) -> xpark, after the barrier;
+//   stage_w       FFN norm weight (a model constant), fp32 -> wpark;
+//   stage_x_load  x (fp32, device-coherent) -> xpark, as soon as the previous
+//                 down phase has completed (the barrier the core waits on);
 //   stage_x_fin   RMSNorm (core/cpu_ops.cpp:24-30) of xpark * wpark -> fp16 pairs in xs;
 //   stage_h_load  h (already fp16 pairs, device-coherent) -> xs.
 constexpr int kWparkOff = kLdsXs + 8192;   // fp32 [H], above the input pairs of the gate/up GEMV
-constexpr int kXparkOff = kLdsMisc;        // fp32 [H]
+constexpr int kXparkOff = kLdsXpark;       // fp32 [H], free during the core phases
 template <int J, int AUX>
 __device__ __forceinline__ void lds_fill(const void* src, uint32_t bytes, char* lds, int off, int lane) {
     const __amdgpu_buffer_rsrc_t r = rsrc(src, bytes);
@@ -1082,7 +1129,10 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     if (wave == kCtl) {
         ln = opaque(lane);
         ctl_arrive(a, p0, ln, KIND == kDN);
-        stage_w<JH>(a, L.ffn_norm_w, ln, lds);
+        // x and the norm weight were staged while the core ran (their loads
+        // completed with the arrival's drain): the normalised input is ready
+        // before the barrier resolves
+        stage_x_fin<JH>(a, ln, lds);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
     Buf<8 * NDG> gd;
@@ -1090,7 +1140,6 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0, ln);
         if (ln == 0) ctl[0] = okw;
-        if (okw) stage_x_load<JH>(a, ln, lds);
     } else {
         // first half of the weights, the tables, and their lookups while the
         // barrier is pending
@@ -1098,13 +1147,9 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         gemv_tables(glr, gu, 2, wave, ln, lds, ctl + 8, gu.P * (l + 1));
         gemv_decode<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
     }
-    wg_sync();   // the x loads were issued ahead of the second half of the weights
+    wg_sync();
     ln = opaque(lane);
-    if (wave == kCtl) {
-        if (ctl[0]) stage_x_fin<JH>(a, ln, lds);
-    } else {
-        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
-    }
+    if (wave != kCtl) gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
     wg_sync();
     if (!ctl[0]) return false;
     // --------------------------------------------------------- gate/up
@@ -1183,11 +1228,19 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     if constexpr (more) wg_sync();   // the bulk loads below queue behind the arrival
     ln = opaque(lane);
     if (wave == kCtl) {
+        // the next core's inputs are constants of the step: load them before the wait
+        AttnStage as;
+        DnStage ds;
+        if constexpr (NEXT == kATT) attn_stage_load(a, Ln, ln, as);
+        else if constexpr (NEXT == kDN) dn_stage_load(a, Ln, ln, ds);
         const int okw = more ? (int)ctl_wait(a, p0 + 2, ln) : 1;
         if (ln == 0) ctl[0] = okw;
         if (more && okw) {
-            if constexpr (NEXT == kATT) attn_stage(a, Ln, ln, lds);
-            else dn_stage(a, Ln, ln, lds);
+            // x is final now: stage it (and the next norm weight) for the next gate/up
+            stage_x_load<JH>(a, ln, lds);
+            stage_w<JH>(a, Ln.ffn_norm_w, ln, lds);
+            if constexpr (NEXT == kATT) attn_stage_fin(a, Ln, ln, lds, as);
+            else if constexpr (NEXT == kDN) dn_stage_fin(a, Ln, ln, lds, ds);
         }
     } else if constexpr (NEXT == kATT) {
         attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
@@ -1216,7 +1269,13 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     Buf<4 * NKJ> cat;
     // phase 0: core of layer 0 (inputs are ready at launch)
     dn_prefetch(cdn, a, L0, wave, lane);
-    if (wave == kCtl) dn_stage(a, L0, lane, lds);
+    if (wave == kCtl) {
+        DnStage ds;
+        dn_stage_load(a, L0, lane, ds);
+        stage_x_load<JH>(a, lane, lds);
+        stage_w<JH>(a, L0.ffn_norm_w, lane, lds);
+        dn_stage_fin(a, L0, lane, lds, ds);
+    }
     if (tid == 0) {
         ctl[0] = 1;
         ctl[8] = ctl[9] = ctl[10] = 0;   // table-build counters (gate, up, down)
