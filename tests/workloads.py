@@ -266,3 +266,113 @@ def oracle_hybrid_step(orc, m: HybridModel):
         m.x = (m.x + orc.lut6_ffn(n, (L["gate_w"], L["gate_lut"]), (L["up_w"], L["up_lut"]),
                                   (L["down_w"], L["down_lut"]), H, I)).astype(np.float32)
     return outs
+
+
+# ------------------------------------------------ greedy decode of a tiny LM
+TINY_LM = dict(hidden=1024, inter=2048, layers=4, n_heads=8, n_kv_heads=2, head_dim=256, rot_dim=64,
+               theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=16, lin_dim=128, conv_kernel=4,
+               vocab=4096, cap=128)
+
+
+def tiny_lm(seed, dims=TINY_LM, lut_std=0.02):
+    """Seeded random-init Qwen3.5-shaped hybrid LM (layer i is full attention
+    iff (i+1) % 4 == 0) with every projection LUT6-palettised, as the
+    reference's CoreML path stores them (scripts/export_hybrid_chunks.py:42):
+    per layer input/post norms, the first projection (DeltaNet: qkv | z | a | b,
+    attention: q_gate | k | v; models/llm/qwen3_5.cpp:849-910, 944-1002), the
+    DeltaNet conv1d weights, A = exp(A_log) and dt_bias, o_proj and the SwiGLU
+    FFN; an fp32 embedding table, a final norm and a LUT6 LM head."""
+    rng = np.random.default_rng(seed)
+    d = dims
+    H, I, V = d["hidden"], d["inter"], d["vocab"]
+    Hq, Hkv, D = d["n_heads"], d["n_kv_heads"], d["head_dim"]
+    Hk, Hv, dl = d["lin_k_heads"], d["lin_v_heads"], d["lin_dim"]
+    qkv = 2 * Hk * dl + Hv * dl
+
+    def norm_w(n):
+        return (1.0 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+
+    def lut6(out_dim, in_dim):
+        idx = rng.integers(0, 64, (out_dim, in_dim), dtype=np.uint8)
+        lut = f16(lut_std * rng.standard_normal((out_dim // 32, 64)))
+        return pack_lut6(idx), lut
+
+    layers = []
+    for i in range(d["layers"]):
+        L = dict(attn=layer_is_attention(i), in_norm=norm_w(H), post_norm=norm_w(H))
+        if L["attn"]:
+            L["first"] = lut6(Hq * 2 * D + 2 * Hkv * D, H)
+            L["q_norm"], L["k_norm"] = norm_w(D), norm_w(D)
+            L["o"] = lut6(H, Hq * D)
+        else:
+            L["first"] = lut6(qkv + Hv * dl + 2 * Hv, H)
+            L["conv_w"] = (0.5 * rng.standard_normal((qkv, d["conv_kernel"]))).astype(np.float32)
+            L["A"] = np.exp(rng.uniform(0.0, math.log(16.0), Hv)).astype(np.float32)
+            L["dt_bias"] = rng.standard_normal(Hv).astype(np.float32)
+            L["norm_w"] = norm_w(dl)
+            L["o"] = lut6(H, Hv * dl)
+        L["gate"], L["up"], L["down"] = lut6(I, H), lut6(I, H), lut6(H, I)
+        layers.append(L)
+    return dict(dims=d, layers=layers, embed=rng.standard_normal((V, H)).astype(np.float32),
+                final_norm=norm_w(H), lm_head=lut6(V, H))
+
+
+class OracleLM:
+    """Decode loop of the tiny LM on the oracle: Qwen35Model::forward
+    (models/llm/qwen3_5.cpp:1278-1417) -- embedding, per layer RMSNorm, first
+    projection, DeltaNet core (conv1d + SiLU, :867-875, then :879-908) or
+    attention core (:944-1002), o_proj and residual, RMSNorm + SwiGLU FFN and
+    residual; final norm, LM head, and the greedy rule of core/sampling.cpp:47-53
+    (first maximum)."""
+
+    def __init__(self, orc, m):
+        self.orc, self.m = orc, m
+        d = m["dims"]
+        self.st = []
+        for L in m["layers"]:
+            if L["attn"]:
+                shape = (d["cap"], d["n_kv_heads"], d["head_dim"])
+                self.st.append(dict(kc=np.zeros(shape, np.uint16), vc=np.zeros(shape, np.uint16), start=0, len=0))
+            else:
+                qkv = 2 * d["lin_k_heads"] * d["lin_dim"] + d["lin_v_heads"] * d["lin_dim"]
+                self.st.append(dict(conv=np.zeros((qkv, d["conv_kernel"] - 1), np.float32), cpos=0,
+                                    S=np.zeros((d["lin_v_heads"], d["lin_dim"], d["lin_dim"]), np.float32)))
+
+    def step(self, token, pos):
+        orc, m, d = self.orc, self.m, self.m["dims"]
+        H, I = d["hidden"], d["inter"]
+        Hk, Hv, dl = d["lin_k_heads"], d["lin_v_heads"], d["lin_dim"]
+        x = m["embed"][token].copy()
+        for L, s in zip(m["layers"], self.st):
+            xn = orc.rmsnorm(x, L["in_norm"], d["eps"])
+            fw, fl = L["first"]
+            proj = orc.lut6_matvec(fw, fl, xn, fl.shape[0] * 32, H)
+            if L["attn"]:
+                Hq, Hkv, D = d["n_heads"], d["n_kv_heads"], d["head_dim"]
+                qg = proj[:Hq * 2 * D].reshape(Hq, 2 * D)
+                k = proj[Hq * 2 * D:Hq * 2 * D + Hkv * D].reshape(Hkv, D)
+                v = proj[Hq * 2 * D + Hkv * D:].reshape(Hkv, D)
+                pre, s["kc"], s["vc"], s["start"], s["len"] = orc.full_attn_decode(
+                    qg, k, v, s["kc"], s["vc"], L["q_norm"], L["k_norm"], Hq, Hkv, D, d["rot_dim"], pos,
+                    d["theta"], d["eps"], 0, True, s["start"], s["len"], d["cap"])
+            else:
+                qkv = 2 * Hk * dl + Hv * dl
+                co, s["conv"], s["cpos"] = orc.conv1d_update(s["conv"], s["cpos"], proj[:qkv], L["conv_w"],
+                                                            d["conv_kernel"])
+                co = orc.silu(co)
+                q = co[:Hk * dl].reshape(Hk, dl)
+                k = co[Hk * dl:2 * Hk * dl].reshape(Hk, dl)
+                v = co[2 * Hk * dl:].reshape(Hv, dl)
+                z = proj[qkv:qkv + Hv * dl].reshape(Hv, dl)
+                a = proj[qkv + Hv * dl:qkv + Hv * dl + Hv]
+                b = proj[qkv + Hv * dl + Hv:]
+                pre, s["S"] = orc.deltanet_decode(s["S"], q, k, v, a, b, L["A"], L["dt_bias"], 1 | 4, z,
+                                                  L["norm_w"])
+            ow, ol = L["o"]
+            x = x + orc.lut6_matvec(ow, ol, pre.reshape(-1), H, pre.size)
+            xn = orc.rmsnorm(x, L["post_norm"], d["eps"])
+            x = x + orc.lut6_ffn(xn, L["gate"], L["up"], L["down"], H, I)
+        xf = orc.rmsnorm(x, m["final_norm"], d["eps"])
+        lw, ll = m["lm_head"]
+        logits = orc.lut6_matvec(lw, ll, xf, d["vocab"], H)
+        return orc.argmax(logits), logits
