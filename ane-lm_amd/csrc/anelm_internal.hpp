@@ -75,8 +75,8 @@ __device__ __forceinline__ void lds_barrier() {
 // Batched LUT6 GEMM on MFMA (lut6_mfma.hip): column split for in_dim, and the
 // launch for batch <= 32 inputs.
 bool lut6_gemm_geometry(int in_dim, int& np, int& waves);
-int lut6_gemm_launch(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
-                     int in_dim, hipStream_t st);
+int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, const float* x, long ldx, int batch,
+                     int out_dim, int in_dim, int accumulate, hipStream_t st);
 
 // `n` zeroed counters on the current device; nullptr if n exceeds the pool.
 uint32_t* counters(size_t n);

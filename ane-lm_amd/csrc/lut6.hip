@@ -689,23 +689,34 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
     return gemv_dispatch<kStageCopy>(a, 1, st);
 }
 
-// Y[b] = W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs where the
-// column count fits its register-resident window, else one GEMV per input.
+// Y[b] (+)= W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs.  A
+// column count too wide for one register-resident window is cut into equal
+// column slices (a multiple of 256 columns each, 16-byte aligned in the packed
+// rows) accumulated into Y one after the other; shapes that fit neither way
+// take one GEMV per input.
 int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
-                 int in_dim, hipStream_t st) {
-    int np = 0, waves = 0;
+                 int in_dim, int accumulate, hipStream_t st) {
+    int np = 0, waves = 0, nsplit = 1;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    if (aligned && lut6_gemm_geometry(in_dim, np, waves)) {
+    while (nsplit <= 16 && (in_dim % nsplit != 0 || !lut6_gemm_geometry(in_dim / nsplit, np, waves) ||
+                            (nsplit > 1 && (in_dim / nsplit) % 256 != 0)))
+        nsplit++;
+    if (aligned && nsplit <= 16) {
+        const int part = in_dim / nsplit;
+        const long ldw = (long)in_dim * 3 / 4;
         for (int b0 = 0; b0 < batch; b0 += 32) {
             const int nb = batch - b0 < 32 ? batch - b0 : 32;
-            const int rc = lut6_gemm_launch(y + (size_t)b0 * out_dim, w, lut, x + (size_t)b0 * in_dim, nb, out_dim,
-                                            in_dim, st);
-            if (rc) return rc;
+            for (int sp = 0; sp < nsplit; sp++) {
+                const int rc = lut6_gemm_launch(y + (size_t)b0 * out_dim, w + (size_t)sp * part * 3 / 4, ldw, lut,
+                                                x + (size_t)b0 * in_dim + (size_t)sp * part, in_dim, nb, out_dim, part,
+                                                accumulate || sp > 0, st);
+                if (rc) return rc;
+            }
         }
         return ANELM_OK;
     }
     for (int b = 0; b < batch; b++) {
-        const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, 0, st);
+        const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, accumulate, st);
         if (rc) return rc;
     }
     return ANELM_OK;
@@ -797,7 +808,7 @@ int anelm_lut6_ffn(float* x, float* gu_scratch, const float* norm_w, float eps,
 }
 
 int anelm_lut6_gemm(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
-                    int in_dim, void* stream) {
+                    int in_dim, int accumulate, void* stream) {
     ANELM_NONNULL(y);
     ANELM_NONNULL(w);
     ANELM_NONNULL(lut);
@@ -805,7 +816,20 @@ int anelm_lut6_gemm(float* y, const uint8_t* w, const uint16_t* lut, const float
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
     ANELM_REQUIRE(batch > 0, "lut6_gemm: batch %d", batch);
-    return batched_gemv(y, w, lut, x, batch, out_dim, in_dim, as_stream(stream));
+    ANELM_REQUIRE(accumulate == 0 || accumulate == 1, "lut6_gemm: accumulate %d", accumulate);
+    return batched_gemv(y, w, lut, x, batch, out_dim, in_dim, accumulate, as_stream(stream));
+}
+
+int anelm_swiglu(float* h, const float* g, const float* u, int64_t n, void* stream) {
+    ANELM_NONNULL(h);
+    ANELM_NONNULL(g);
+    ANELM_NONNULL(u);
+    ANELM_REQUIRE(n >= 0 && n <= 0x7fffffffLL - 255, "swiglu: n %lld", (long long)n);
+    if (n == 0) return ANELM_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), h, g, u,
+                       (int)n);
+    ANELM_LAUNCHED("swiglu_kernel");
+    return ANELM_OK;
 }
 
 int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
@@ -829,7 +853,7 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     float* logits = reinterpret_cast<float*>(ws);
     float* cv = reinterpret_cast<float*>(ws + logits_bytes);
     int* ci = reinterpret_cast<int*>(ws + logits_bytes + (size_t)batch * n_cand * sizeof(float));
-    rc = batched_gemv(logits, w, lut, x, batch, out_dim, in_dim, st);
+    rc = batched_gemv(logits, w, lut, x, batch, out_dim, in_dim, 0, st);
     if (rc) return rc;
     hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(256), 0, st, logits, out_dim, k,
                        n_chunks, cv, ci);

@@ -42,10 +42,12 @@ __device__ __forceinline__ int red_pos(int e, int l) { return e * kRedRow + (l &
 
 struct GemmArgs {
     float* y;              // [batch][out_dim]
-    const uint8_t* w;      // [out_dim][in_dim * 3 / 4]
+    const uint8_t* w;      // row r at w + r * ldw bytes, in_dim * 3 / 4 bytes used
     const uint16_t* lut;   // [out_dim / 32][64]
-    const float* x;        // [batch][in_dim]
+    const float* x;        // vector b at x + b * ldx, in_dim floats used
     int batch, out_dim, in_dim;
+    long ldw, ldx;         // row strides (bytes of w, floats of x): a column slice of wider matrices
+    int accumulate;        // y += W x instead of y = W x
 };
 
 // Pair-table byte offset of pair p (indices 2p, 2p + 1: the 12-bit field at
@@ -69,8 +71,7 @@ template <int NP>
 __device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w,
                                              int lane) {
     const int m = lane & 31, hh = lane >> 5;
-    const size_t row_bytes = (size_t)a.in_dim * 3 / 4;
-    const u32x4* p = reinterpret_cast<const u32x4*>(a.w + ((size_t)g * 32 + m) * row_bytes +
+    const u32x4* p = reinterpret_cast<const u32x4*>(a.w + ((size_t)g * 32 + m) * (size_t)a.ldw +
                                                     (size_t)w * 96 * NP + hh * 48 * NP);
 #pragma unroll
     for (int i = 0; i < 3 * NP; i++) {
@@ -130,7 +131,7 @@ __device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0,
 // Stores are raw buffer stores over y: an element outside the batch gets an
 // offset past the buffer's end, which the hardware drops, so the store is
 // issued by every thread without a branch.
-template <int NW>
+template <int NW, bool ACC>
 __device__ __forceinline__ void reduce_store(const GemmArgs& a, int g, const char* lds, int tid) {
     constexpr int NT = NW * 64;
     const float* red = reinterpret_cast<const float*>(lds + kRedOff);
@@ -148,12 +149,14 @@ __device__ __forceinline__ void reduce_store(const GemmArgs& a, int g, const cha
         const uint32_t off = (t < 1024 && n < a.batch) ? ((uint32_t)n * (uint32_t)a.out_dim + (uint32_t)g * 32u +
                                                             (uint32_t)m) * 4u
                                                          : bytes;
+        if constexpr (ACC)   // out-of-range offsets read 0 and drop the store
+            s += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, (int)off, 0, 0));
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s), ry, (int)off, 0, 0);
     }
 }
 
 // NP = 2: 64 registers of X per lane; NP = 1: 32.
-template <int NP, int NW>
+template <int NP, int NW, bool ACC>
 __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     constexpr int nt = NW * 64, nw = NW;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
     half8 xb[8 * NP];
     {
         const int n = lane & 31, hh = lane >> 5;
-        const float* xr = a.x + (size_t)n * a.in_dim + (size_t)w * 128 * NP + hh * 64 * NP;
+        const float* xr = a.x + (size_t)n * a.ldx + (size_t)w * 128 * NP + hh * 64 * NP;
 #pragma unroll
         for (int t = 0; t < 8 * NP; t++) {
             half8 v = half8{};
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
         }
         build_table(lds, 1, j + 1, w, nw, lane);      // next group (table 1 is free since the last barrier)
         lds_barrier();                                 // partial tiles and table 1 complete
-        reduce_store<NW>(a, g, lds, tid);
+        reduce_store<NW, ACC>(a, g, lds, tid);
         g += stride;
         if (g >= n_groups) break;
         load_weights<NP>(wa, a, min(g + stride, last), w, lane);
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
         }
         build_table(lds, 0, j + 2, w, nw, lane);
         lds_barrier();
-        reduce_store<NW>(a, g, lds, tid);
+        reduce_store<NW, ACC>(a, g, lds, tid);
         g += stride;
         if (g >= n_groups) break;
         load_weights<NP>(wb, a, min(g + stride, last), w, lane);
@@ -252,8 +255,8 @@ bool lut6_gemm_geometry(int in_dim, int& np, int& waves) {
 
 // Y[b][r] for b < batch (batch <= 32), out_dim % 32 == 0, in_dim accepted by
 // lut6_gemm_geometry.  Shapes are validated by the caller.
-int lut6_gemm_launch(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
-                     int in_dim, hipStream_t st) {
+int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, const float* x, long ldx, int batch,
+                     int out_dim, int in_dim, int accumulate, hipStream_t st) {
     int np = 0, waves = 0;
     if (!lut6_gemm_geometry(in_dim, np, waves) || batch < 1 || batch > 32 || out_dim % 32 ||
         (long long)batch * out_dim * 4 >= (1LL << 31))
@@ -261,26 +264,31 @@ int lut6_gemm_launch(float* y, const uint8_t* w, const uint16_t* lut, const floa
                          in_dim);
     Device* dev = device();
     if (!dev) return ANELM_EHIP;
-    GemmArgs a{y, w, lut, x, batch, out_dim, in_dim};
+    GemmArgs a{y, w, lut, x, batch, out_dim, in_dim, ldw, ldx, accumulate};
     const int n_groups = out_dim / 32;
     const int grid = n_groups < dev->num_cus ? n_groups : dev->num_cus;
     const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float);
     using K = void (*)(GemmArgs);
-    static const K k2[11] = {nullptr, lut6_gemm_kernel<2, 1>, lut6_gemm_kernel<2, 2>, lut6_gemm_kernel<2, 3>,
-                             lut6_gemm_kernel<2, 4>, lut6_gemm_kernel<2, 5>, lut6_gemm_kernel<2, 6>,
-                             lut6_gemm_kernel<2, 7>, lut6_gemm_kernel<2, 8>, lut6_gemm_kernel<2, 9>,
-                             lut6_gemm_kernel<2, 10>};
-    static const K k1[16] = {nullptr, lut6_gemm_kernel<1, 1>, nullptr, lut6_gemm_kernel<1, 3>, nullptr,
-                             lut6_gemm_kernel<1, 5>, nullptr, lut6_gemm_kernel<1, 7>, nullptr,
-                             lut6_gemm_kernel<1, 9>, nullptr, lut6_gemm_kernel<1, 11>, nullptr,
-                             lut6_gemm_kernel<1, 13>, nullptr, lut6_gemm_kernel<1, 15>};
-    const K kp = np == 2 ? k2[waves] : k1[waves];
+#define ANELM_K2(A) {nullptr, lut6_gemm_kernel<2, 1, A>, lut6_gemm_kernel<2, 2, A>, lut6_gemm_kernel<2, 3, A>,     \
+                     lut6_gemm_kernel<2, 4, A>, lut6_gemm_kernel<2, 5, A>, lut6_gemm_kernel<2, 6, A>,              \
+                     lut6_gemm_kernel<2, 7, A>, lut6_gemm_kernel<2, 8, A>, lut6_gemm_kernel<2, 9, A>,              \
+                     lut6_gemm_kernel<2, 10, A>}
+#define ANELM_K1(A) {nullptr, lut6_gemm_kernel<1, 1, A>, nullptr, lut6_gemm_kernel<1, 3, A>, nullptr,              \
+                     lut6_gemm_kernel<1, 5, A>, nullptr, lut6_gemm_kernel<1, 7, A>, nullptr,                         \
+                     lut6_gemm_kernel<1, 9, A>, nullptr, lut6_gemm_kernel<1, 11, A>, nullptr,                        \
+                     lut6_gemm_kernel<1, 13, A>, nullptr, lut6_gemm_kernel<1, 15, A>}
+    static const K k2[2][11] = {ANELM_K2(false), ANELM_K2(true)};
+    static const K k1[2][16] = {ANELM_K1(false), ANELM_K1(true)};
+#undef ANELM_K2
+#undef ANELM_K1
+    const int acc = accumulate ? 1 : 0;
+    const K kp = np == 2 ? k2[acc][waves] : k1[acc][waves];
     if (!kp) return set_error(ANELM_EINVAL, "lut6_gemm: no kernel for %d waves (np %d)", waves, np);
-    static bool attr_set[2][16] = {};
-    if (!attr_set[np - 1][waves]) {
+    static bool attr_set[2][2][16] = {};
+    if (!attr_set[acc][np - 1][waves]) {
         ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kp), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)lds));
-        attr_set[np - 1][waves] = true;
+        attr_set[acc][np - 1][waves] = true;
     }
     hipLaunchKernelGGL(kp, dim3(grid), dim3(waves * 64), lds, st, a);
     ANELM_LAUNCHED("lut6_gemm_kernel");

@@ -228,11 +228,22 @@ def lut6_gate_up(x, norm_w, eps, gate, up, hidden, inter):
     return g, u
 
 
-def lut6_gemm(w, lut, x, out_dim, in_dim, out=None):
-    """y[b] = W x[b] for a batch x [batch][in_dim] (weights dequantised once per 32 inputs)."""
+def lut6_gemm(w, lut, x, out_dim, in_dim, out=None, accumulate=False):
+    """y[b] = W x[b] (or y[b] += W x[b]) for a batch x [batch][in_dim]
+    (weights dequantised once per 32 inputs)."""
     batch = x.shape[0]
-    out = torch.empty(batch, out_dim, device=x.device, dtype=_F32) if out is None else out
-    call("anelm_lut6_gemm", _p(out), _p(w), _p(lut), _p(x), batch, out_dim, in_dim, _s())
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs out")
+        out = torch.empty(batch, out_dim, device=x.device, dtype=_F32)
+    call("anelm_lut6_gemm", _p(out), _p(w), _p(lut), _p(x), batch, out_dim, in_dim, 1 if accumulate else 0, _s())
+    return out
+
+
+def swiglu(g, u, out=None):
+    """silu(g) * u elementwise."""
+    out = torch.empty_like(g) if out is None else out
+    call("anelm_swiglu", _p(out), _p(g), _p(u), g.numel(), _s())
     return out
 
 

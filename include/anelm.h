@@ -219,13 +219,18 @@ int anelm_lut6_swiglu(float* h, const float* x, const float* norm_w, float eps,
                       const uint8_t* up_w, const uint16_t* up_lut,
                       int hidden, int inter, void* stream);
 
-/* Batched LUT6 projection: y[b] = W x[b] for b < batch (x [batch][in_dim],
- * y [batch][out_dim], fp32; x enters the products as fp16, as in
- * anelm_lut6_gemv).  Each weight is dequantised once per 32 inputs.  No
- * reference counterpart as one call: matvec (core/cpu_ops.cpp:77-80) per input
- * on the dequantised weights. */
+/* Batched LUT6 projection: y[b] = W x[b] (accumulate = 0) or y[b] += W x[b]
+ * (accumulate = 1, e.g. the residual add after the FFN down projection) for
+ * b < batch (x [batch][in_dim], y [batch][out_dim], fp32; x enters the
+ * products as fp16, as in anelm_lut6_gemv).  Each weight is dequantised once
+ * per 32 inputs.  No reference counterpart as one call: matvec
+ * (core/cpu_ops.cpp:77-80) per input on the dequantised weights. */
 int anelm_lut6_gemm(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch,
-                    int out_dim, int in_dim, void* stream);
+                    int out_dim, int in_dim, int accumulate, void* stream);
+
+/* h[i] = silu(g[i]) * u[i] for i < n -- the SwiGLU product of the FFN
+ * (models/llm/qwen3_5.cpp:1118-1130) on batched gate / up outputs. */
+int anelm_swiglu(float* h, const float* g, const float* u, int64_t n, void* stream);
 
 /* Top-k of logits = W x for a batch of inputs (in-model top-k LM head,
  * scripts/export_hybrid_chunks.py:409-421).  x [batch][in_dim] fp32;

@@ -52,7 +52,7 @@ def test_ffn_block(anelm, orc, dev, hidden, inter):
 
 @pytest.mark.parametrize("out_dim,in_dim,batch", [(9216, 2560, 32), (2560, 2560, 1), (4096, 1024, 5),
                                                   (512, 1280, 33), (256, 128, 7), (1024, 2048, 64),
-                                                  (96, 2176, 3)])
+                                                  (96, 2176, 3), (2560, 9216, 32), (1024, 3584, 9)])
 def test_gemm_batched(anelm, orc, dev, out_dim, in_dim, batch):
     """Batched projection y[b] = W x[b]: the MFMA path (column windows of 128 or
     256 per wave, tiles of 32 inputs, ragged last tile) and the per-input
@@ -66,6 +66,37 @@ def test_gemm_batched(anelm, orc, dev, out_dim, in_dim, batch):
     # repeated call: same bits (no state carried between launches)
     again = to_host(anelm.ops.lut6_gemm(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim, in_dim))
     assert np.array_equal(got, again)
+
+
+def test_gemm_accumulate_and_batched_ffn(anelm, orc, dev):
+    """y += W x (the residual add), and a batched SwiGLU FFN block built from
+    the batched pieces -- RMSNorm rows, gate / up projections, silu(g) * u, the
+    9216-column down projection accumulated into x -- against the oracle's FFN
+    per input (models/llm/qwen3_5.cpp:1118-1130, 1335-1354)."""
+    H, I, B = 2560, 9216, 32
+    g, u, d = (lut6_matrix(660 + i, *shape) for i, shape in enumerate([(I, H), (I, H), (H, I)]))
+    rng = np.random.default_rng(661)
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    dg, du, dd = ((to_dev(m[0], dev), to_dev(m[1], dev)) for m in (g, u, d))
+    xd = to_dev(x, dev)
+    n = anelm.ops.rmsnorm(xd, to_dev(w, dev), 1e-6)
+    gv = anelm.ops.lut6_gemm(dg[0], dg[1], n, I, H)
+    uv = anelm.ops.lut6_gemm(du[0], du[1], n, I, H)
+    h = anelm.ops.swiglu(gv, uv)
+    anelm.ops.lut6_gemm(dd[0], dd[1], h, H, I, out=xd, accumulate=True)
+    got = to_host(xd)
+    for b in (0, 17, 31):
+        nb = orc.rmsnorm(x[b], w, 1e-6)
+        want = x[b] + orc.lut6_ffn(nb, g[:2], u[:2], d[:2], H, I)
+        assert_close(got[b], want, what=f"batched ffn input {b}")
+    # accumulate on its own: y0 + W x
+    y0 = rng.standard_normal((5, 1024)).astype(np.float32)
+    pk, lut, _ = lut6_matrix(662, 1024, 2560)
+    xs = rng.standard_normal((5, 2560)).astype(np.float32)
+    yd = to_dev(y0, dev)
+    anelm.ops.lut6_gemm(to_dev(pk, dev), to_dev(lut, dev), to_dev(xs, dev), 1024, 2560, out=yd, accumulate=True)
+    assert_close(to_host(yd)[3], y0[3] + orc.lut6_matvec(pk, lut, xs[3], 1024, 2560), what="accumulate")
 
 
 def _check_topk(orc, idx, val, logits, k):
