@@ -48,6 +48,8 @@ struct Device {
     int num_cus = 0;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* ws2 = nullptr;      // second slot: split-K partials of the batched GEMM
+    size_t ws2_bytes = 0;
     uint32_t* counters = nullptr;
     size_t n_counters = 0;
 };
@@ -59,6 +61,8 @@ Device* device();
 // Workspace of at least `bytes` on the current device (grows with a stream
 // sync + free + malloc).  Returns nullptr on failure with the error recorded.
 void* workspace(size_t bytes, hipStream_t stream);
+// Same, from a second per-device buffer (for callees of a workspace user).
+void* workspace2(size_t bytes, hipStream_t stream);
 
 // Workgroup barrier for LDS exchange only: this wave's LDS operations
 // complete, then s_barrier.  __syncthreads() also carries a release fence that
@@ -76,7 +80,8 @@ __device__ __forceinline__ void lds_barrier() {
 // launch for batch <= 32 inputs.
 bool lut6_gemm_geometry(int in_dim, int& np, int& waves);
 int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, const float* x, long ldx, int batch,
-                     int out_dim, int in_dim, int accumulate, hipStream_t st);
+                     int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st);
+int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st);
 
 // `n` zeroed counters on the current device; nullptr if n exceeds the pool.
 uint32_t* counters(size_t n);

@@ -689,34 +689,53 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
     return gemv_dispatch<kStageCopy>(a, 1, st);
 }
 
-// Y[b] (+)= W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs.  A
-// column count too wide for one register-resident window is cut into equal
-// column slices (a multiple of 256 columns each, 16-byte aligned in the packed
-// rows) accumulated into Y one after the other; shapes that fit neither way
-// take one GEMV per input.
+// Y[b] (+)= W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs.  The
+// columns are cut into S equal slices (each a valid register-resident window,
+// a multiple of 256 columns when S > 1): S is the smallest count that fits,
+// raised until the (32-row group, slice) units cover every CU twice, so small
+// projections still fill the chip.  With S > 1 one launch writes the slices'
+// partial products (second workspace) and split_sum adds them (and Y when
+// accumulating) -- a fixed order, so results do not vary between calls.
+// Shapes that fit no slicing take one GEMV per input.
 int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
                  int in_dim, int accumulate, hipStream_t st) {
-    int np = 0, waves = 0, nsplit = 1;
+    int np = 0, waves = 0;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    while (nsplit <= 16 && (in_dim % nsplit != 0 || !lut6_gemm_geometry(in_dim / nsplit, np, waves) ||
-                            (nsplit > 1 && (in_dim / nsplit) % 256 != 0)))
-        nsplit++;
-    if (aligned && nsplit <= 16) {
-        const int part = in_dim / nsplit;
-        const long ldw = (long)in_dim * 3 / 4;
-        for (int b0 = 0; b0 < batch; b0 += 32) {
-            const int nb = batch - b0 < 32 ? batch - b0 : 32;
-            for (int sp = 0; sp < nsplit; sp++) {
-                const int rc = lut6_gemm_launch(y + (size_t)b0 * out_dim, w + (size_t)sp * part * 3 / 4, ldw, lut,
-                                                x + (size_t)b0 * in_dim + (size_t)sp * part, in_dim, nb, out_dim, part,
-                                                accumulate || sp > 0, st);
-                if (rc) return rc;
-            }
+    auto fits = [&](int s) {
+        return in_dim % s == 0 && lut6_gemm_geometry(in_dim / s, np, waves) && (s == 1 || (in_dim / s) % 256 == 0);
+    };
+    int ns = 1;
+    while (ns <= 64 && !fits(ns)) ns++;
+    if (!aligned || ns > 64) {
+        for (int b = 0; b < batch; b++) {
+            const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, accumulate, st);
+            if (rc) return rc;
         }
         return ANELM_OK;
     }
-    for (int b = 0; b < batch; b++) {
-        const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, accumulate, st);
+    Device* dev = device();
+    if (!dev) return ANELM_EHIP;
+    const int n_groups = out_dim / 32;
+    for (int s = ns + 1; n_groups * ns < 2 * dev->num_cus && s <= 64; s++)
+        if (fits(s)) ns = s;
+    if (!fits(ns)) return set_error(ANELM_EINVAL, "lut6_gemm: no column split for in_dim %d", in_dim);
+    const int part = in_dim / ns;
+    const long ldw = (long)in_dim * 3 / 4;
+    for (int b0 = 0; b0 < batch; b0 += 32) {
+        const int nb = batch - b0 < 32 ? batch - b0 : 32;
+        float* yb = y + (size_t)b0 * out_dim;
+        const float* xb = x + (size_t)b0 * in_dim;
+        if (ns == 1) {
+            const int rc = lut6_gemm_launch(yb, w, ldw, lut, xb, in_dim, nb, out_dim, part, accumulate, 1, 0, st);
+            if (rc) return rc;
+            continue;
+        }
+        const long n = (long)nb * out_dim;
+        float* parts = static_cast<float*>(workspace2((size_t)ns * n * sizeof(float), st));
+        if (!parts) return ANELM_ENOMEM;
+        int rc = lut6_gemm_launch(parts, w, ldw, lut, xb, in_dim, nb, out_dim, part, 0, ns, n, st);
+        if (rc) return rc;
+        rc = lut6_split_sum(yb, parts, n, ns, accumulate, st);
         if (rc) return rc;
     }
     return ANELM_OK;

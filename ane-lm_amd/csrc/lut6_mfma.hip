@@ -48,6 +48,7 @@ struct GemmArgs {
     int batch, out_dim, in_dim;
     long ldw, ldx;         // row strides (bytes of w, floats of x): a column slice of wider matrices
     int accumulate;        // y += W x instead of y = W x
+    long sw, sx, sy;       // per column slice blockIdx.y: offsets of w (bytes), x and y (floats)
 };
 
 // Pair-table byte offset of pair p (indices 2p, 2p + 1: the 12-bit field at
@@ -110,14 +111,27 @@ __device__ __forceinline__ void build_table(char* lds, int slot, int j, int w, i
 }
 
 // Stages the LUTs of the workgroup's groups j0 .. j0 + kLutSlots - 1 (group
-// index blockIdx.x + j * gridDim.x, clamped) into LDS.  Called with every
-// wave between two barriers.
-__device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0, int tid, int nt) {
+// index blockIdx.x + j * gridDim.x) that exist into LDS.  Every load is issued
+// before the first LDS store (a fixed count per thread), so the staging costs
+// one round trip.  Called with every wave between two barriers.
+template <int NT>
+__device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0, int tid) {
+    constexpr int K = (kLutSlots * 64 + NT - 1) / NT;
     uint16_t* l = reinterpret_cast<uint16_t*>(lds + kLutOff);
-    const int last = a.out_dim / 32 - 1;
-    for (int e = tid; e < kLutSlots * 64; e += nt) {
-        const int g = min((int)blockIdx.x + (j0 + (e >> 6)) * (int)gridDim.x, last);
-        l[e] = a.lut[(size_t)g * 64 + (e & 63)];
+    const int n_groups = a.out_dim / 32;
+    const int mine = (n_groups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;   // groups of this workgroup
+    const int n_e = min(kLutSlots, mine - j0) * 64;
+    uint16_t v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int e = tid + k * NT;
+        const int g = (int)blockIdx.x + (j0 + (e >> 6)) * (int)gridDim.x;
+        v[k] = a.lut[(size_t)(e < n_e ? g : (int)blockIdx.x) * 64 + (e & 63)];
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int e = tid + k * NT;
+        if (e < n_e) l[e] = v[k];
     }
 }
 
@@ -157,8 +171,13 @@ __device__ __forceinline__ void reduce_store(const GemmArgs& a, int g, const cha
 
 // NP = 2: 64 registers of X per lane; NP = 1: 32.
 template <int NP, int NW, bool ACC>
-__global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
+    // column slice blockIdx.y of a split-K launch (0 otherwise)
+    GemmArgs a = a0;
+    a.w += (size_t)blockIdx.y * a0.sw;
+    a.x += (size_t)blockIdx.y * a0.sx;
+    a.y += (size_t)blockIdx.y * a0.sy;
     constexpr int nt = NW * 64, nw = NW;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = tid >> 6;
@@ -169,18 +188,25 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
     // the wave's X window as MFMA B operands (fp16), zero for vectors >= batch
     half8 xb[8 * NP];
     {
+        // every lane loads (vectors past the batch read vector 0 and are
+        // zeroed afterwards): no branch, so all loads are in flight at once
         const int n = lane & 31, hh = lane >> 5;
-        const float* xr = a.x + (size_t)n * a.ldx + (size_t)w * 128 * NP + hh * 64 * NP;
+        const bool live = n < a.batch;
+        const float* xr = a.x + (size_t)(live ? n : 0) * a.ldx + (size_t)w * 128 * NP + hh * 64 * NP;
+        const float z = live ? 1.0f : 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8 * NP; t++) {
-            half8 v = half8{};
-            if (n < a.batch) {
-                const float4 lo = *reinterpret_cast<const float4*>(xr + 8 * t);
-                const float4 hi = *reinterpret_cast<const float4*>(xr + 8 * t + 4);
-                v = half8{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
-                          (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+        for (int h0 = 0; h0 < 8 * NP; h0 += 4 * NP) {   // two halves bound the registers in flight
+            float4 lo[4 * NP], hi[4 * NP];
+#pragma unroll
+            for (int t = 0; t < 4 * NP; t++) {
+                lo[t] = *reinterpret_cast<const float4*>(xr + 8 * (h0 + t));
+                hi[t] = *reinterpret_cast<const float4*>(xr + 8 * (h0 + t) + 4);
             }
-            xb[t] = v;
+#pragma unroll
+            for (int t = 0; t < 4 * NP; t++)
+                xb[h0 + t] = half8{(_Float16)(lo[t].x * z), (_Float16)(lo[t].y * z), (_Float16)(lo[t].z * z),
+                                   (_Float16)(lo[t].w * z), (_Float16)(hi[t].x * z), (_Float16)(hi[t].y * z),
+                                   (_Float16)(hi[t].z * z), (_Float16)(hi[t].w * z)};
         }
     }
     // Software pipeline, one group ahead: while group g is multiplied from
@@ -192,9 +218,21 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
     const int stride = gridDim.x, last = n_groups - 1;
     uint32_t wa[12 * NP], wb[12 * NP];
     load_weights<NP>(wa, a, g, w, lane);
-    stage_luts(a, lds, 0, tid, nt);
+    stage_luts<nt>(a, lds, 0, tid);
     lds_barrier();
     build_table(lds, 0, 0, w, nw, lane);
+    if (g + stride >= n_groups) {
+        // the only group of this workgroup: no prefetch of a next one
+        float* red = reinterpret_cast<float*>(lds + kRedOff);
+        lds_barrier();
+        float16_t c = float16_t{};
+        group_mfma<NP>(c, wa, xb, lds, 0u);
+#pragma unroll
+        for (int e = 0; e < 16; e++) red[w * 16 * kRedRow + red_pos(e, lane)] = c[e];
+        lds_barrier();
+        reduce_store<NW, ACC>(a, g, lds, tid);
+        return;
+    }
     load_weights<NP>(wb, a, min(g + stride, last), w, lane);
     float* red = reinterpret_cast<float*>(lds + kRedOff);
     // j counts the workgroup's groups; LUTs are restaged every kLutSlots groups
@@ -222,7 +260,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
         if (((j + 2) & (kLutSlots - 1)) == 0) {
             // restage the next kLutSlots LUTs (every 64 groups of this workgroup)
             lds_barrier();
-            stage_luts(a, lds, j + 2, tid, nt);
+            stage_luts<nt>(a, lds, j + 2, tid);
             lds_barrier();
         }
         build_table(lds, 0, j + 2, w, nw, lane);
@@ -234,7 +272,23 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a) {
     }
 }
 
+// y[i] = (y[i] if accumulate) + sum over the column slices of part[s][i].
+__global__ __launch_bounds__(256) void split_sum_kernel(float* y, const float* part, long n, int nsplit, int accumulate) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = accumulate ? y[i] : 0.f;
+    for (int k = 0; k < nsplit; k++) s += part[(long)k * n + i];
+    y[i] = s;
+}
+
 }  // namespace
+
+int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st) {
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, part, n, nsplit,
+                       accumulate);
+    ANELM_LAUNCHED("split_sum_kernel");
+    return ANELM_OK;
+}
 
 // Column split for the GEMM: NP (1 or 2) and the wave count in_dim / (128 NP).
 // NP = 2 (256 columns per wave) up to 10 waves; otherwise NP = 1 (128 columns
@@ -256,7 +310,7 @@ bool lut6_gemm_geometry(int in_dim, int& np, int& waves) {
 // Y[b][r] for b < batch (batch <= 32), out_dim % 32 == 0, in_dim accepted by
 // lut6_gemm_geometry.  Shapes are validated by the caller.
 int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, const float* x, long ldx, int batch,
-                     int out_dim, int in_dim, int accumulate, hipStream_t st) {
+                     int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st) {
     int np = 0, waves = 0;
     if (!lut6_gemm_geometry(in_dim, np, waves) || batch < 1 || batch > 32 || out_dim % 32 ||
         (long long)batch * out_dim * 4 >= (1LL << 31))
@@ -264,9 +318,13 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
                          in_dim);
     Device* dev = device();
     if (!dev) return ANELM_EHIP;
-    GemmArgs a{y, w, lut, x, batch, out_dim, in_dim, ldw, ldx, accumulate};
+    GemmArgs a{y, w, lut, x, batch, out_dim, in_dim, ldw, ldx, accumulate,
+               (long)in_dim * 3 / 4, (long)in_dim, sy};
     const int n_groups = out_dim / 32;
-    const int grid = n_groups < dev->num_cus ? n_groups : dev->num_cus;
+    // one group per workgroup once the split already gives 2 units per CU,
+    // else a grid-stride walk over the groups (prefetching the next one)
+    int grid = n_groups;
+    if (nsplit == 1 && grid > dev->num_cus) grid = dev->num_cus;
     const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float);
     using K = void (*)(GemmArgs);
 #define ANELM_K2(A) {nullptr, lut6_gemm_kernel<2, 1, A>, lut6_gemm_kernel<2, 2, A>, lut6_gemm_kernel<2, 3, A>,     \
@@ -290,7 +348,7 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
                                       (int)lds));
         attr_set[acc][np - 1][waves] = true;
     }
-    hipLaunchKernelGGL(kp, dim3(grid), dim3(waves * 64), lds, st, a);
+    hipLaunchKernelGGL(kp, dim3(grid, nsplit), dim3(waves * 64), lds, st, a);
     ANELM_LAUNCHED("lut6_gemm_kernel");
     return ANELM_OK;
 }

@@ -52,19 +52,17 @@ Device* device() {
     return d;
 }
 
-void* workspace(size_t bytes, hipStream_t stream) {
-    Device* d = device();
-    if (!d) return nullptr;
-    if (bytes <= d->ws_bytes) return d->ws;
+static void* grow(void*& buf, size_t& have, size_t bytes, hipStream_t stream) {
+    if (bytes <= have) return buf;
     size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
     want = (want + 0xffff) & ~size_t(0xffff);
-    if (d->ws) {
+    if (buf) {
         hipError_t e = hipStreamSynchronize(stream);
         if (e != hipSuccess) { hip_fail(e, "hipStreamSynchronize"); return nullptr; }
-        e = hipFree(d->ws);
+        e = hipFree(buf);
         if (e != hipSuccess) { hip_fail(e, "hipFree(workspace)"); return nullptr; }
-        d->ws = nullptr;
-        d->ws_bytes = 0;
+        buf = nullptr;
+        have = 0;
     }
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, want);
@@ -72,9 +70,21 @@ void* workspace(size_t bytes, hipStream_t stream) {
         set_error(ANELM_ENOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
         return nullptr;
     }
-    d->ws = p;
-    d->ws_bytes = want;
+    buf = p;
+    have = want;
     return p;
+}
+
+void* workspace(size_t bytes, hipStream_t stream) {
+    Device* d = device();
+    if (!d) return nullptr;
+    return grow(d->ws, d->ws_bytes, bytes, stream);
+}
+
+void* workspace2(size_t bytes, hipStream_t stream) {
+    Device* d = device();
+    if (!d) return nullptr;
+    return grow(d->ws2, d->ws2_bytes, bytes, stream);
 }
 
 uint32_t* counters(size_t n) {

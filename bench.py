@@ -326,6 +326,102 @@ def measure_cores(anelm, torch, dev, seed=11):
     return res
 
 
+def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
+    """32 concurrent sequences at the 4B shape through one decode step of 32
+    hybrid layers: per full-attention layer the paged attention of every
+    sequence over its own shuffled 16-token pages (ragged lengths U[256, 16384],
+    seeded; q / k already normalised and rotated), per DeltaNet layer one
+    launch over the 32 x 32 value heads (own fp32 state each, gated norm), per
+    layer the batched LUT6 SwiGLU FFN (RMSNorm rows, gate and up projections,
+    silu(g) * u, down projection accumulated into the residual), then the
+    top-32 of the 262144-row LUT6 LM head for the 32 hidden states.  Every
+    layer has its own weights, caches and states (nothing is re-read from a
+    cache by construction)."""
+    import numpy as np
+    c = CFG
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    H, I, D = c["hidden"], c["inter"], c["head_dim"]
+    Hq, Hkv, Hk, Hv, dl = c["n_heads"], c["n_kv_heads"], c["lin_k_heads"], c["lin_v_heads"], c["lin_dim"]
+    B, P, V = 32, 16, 262144
+
+    def randn(*shape, std=1.0, dtype=torch.float32):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(dtype)
+
+    def randbytes(*shape):
+        return torch.randint(0, 256, shape, generator=g, device=dev, dtype=torch.uint8)
+
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, 16385, B).astype(np.int32)
+    npg = (lens + P - 1) // P
+    n_pages = int(npg.sum())
+    layers, kv_bytes, dn_bytes = [], 0, 0
+    for i in range(c["layers"]):
+        L = {"ffn_norm": 1 + randn(H, std=0.02),
+             "gate": (randbytes(I, H * 3 // 4), randn(I // 32, 64, std=0.02, dtype=torch.float16)),
+             "up": (randbytes(I, H * 3 // 4), randn(I // 32, 64, std=0.02, dtype=torch.float16)),
+             "down": (randbytes(H, I * 3 // 4), randn(H // 32, 64, std=0.02, dtype=torch.float16))}
+        if (i + 1) % 4 == 0:
+            perm = rng.permutation(n_pages).astype(np.int32)
+            table = np.zeros((B, int(npg.max())), np.int32)
+            off = 0
+            for s in range(B):
+                table[s, :npg[s]] = perm[off:off + npg[s]]
+                off += npg[s]
+            L["kp"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
+            L["vp"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
+            L["table"] = torch.from_numpy(table).to(dev)
+            L["q"] = randn(B, Hq, D)
+            L["out"] = torch.empty(B, Hq, D, device=dev)
+            kv_bytes += int(lens.sum()) * Hkv * D * 2 * 2
+        else:
+            L["S"] = randn(B * Hv, dl, dl, std=0.1)
+            L["q"] = randn(B * Hk, dl)
+            L["k"] = randn(B * Hk, dl)
+            L["v"] = randn(B * Hv, dl)
+            L["a"], L["b"], L["dt"] = randn(B * Hv), randn(B * Hv), randn(B * Hv)
+            L["A"] = torch.exp(torch.rand(B * Hv, generator=g, device=dev) * math.log(16.0))
+            L["z"] = randn(B * Hv, dl)
+            L["nw"] = 1 + randn(dl, std=0.02)
+            L["y"] = torch.empty(B * Hv, dl, device=dev)
+            dn_bytes += B * Hv * dl * dl * 4 * 2
+        layers.append(L)
+    lm = (randbytes(V, H * 3 // 4), randn(V // 32, 64, std=0.02, dtype=torch.float16))
+    lens_d = torch.from_numpy(lens).to(dev)
+    x = randn(B, H)
+    xn = torch.empty(B, H, device=dev)
+    gv = torch.empty(B, I, device=dev)
+    uv = torch.empty(B, I, device=dev)
+    hv = torch.empty(B, I, device=dev)
+    ops = anelm.ops
+    max_len = int(lens.max())
+
+    def step():
+        for L in layers:
+            if "kp" in L:
+                ops.attn_decode_paged(L["q"], L["kp"], L["vp"], L["table"], lens_d, max_len, Hq, Hkv, D, P,
+                                      out=L["out"])
+            else:
+                ops.deltanet_decode(L["S"], L["q"], L["k"], L["v"], L["a"], L["b"], L["A"], L["dt"], 1 | 4,
+                                    L["z"], L["nw"], out=L["y"])
+            ops.rmsnorm(x, L["ffn_norm"], c["eps"], out=xn)
+            ops.lut6_gemm(L["gate"][0], L["gate"][1], xn, I, H, out=gv)
+            ops.lut6_gemm(L["up"][0], L["up"][1], xn, I, H, out=uv)
+            ops.swiglu(gv, uv, out=hv)
+            ops.lut6_gemm(L["down"][0], L["down"][1], hv, H, I, out=x, accumulate=True)
+        return ops.lut6_topk(lm[0], lm[1], x, V, H, 32)
+
+    us = _gpu_us(torch, step, reps, warm=1)
+    w_bytes = c["layers"] * (3 * H * I * 3 // 4 + (2 * I // 32 + H // 32) * 128)
+    lm_bytes = V * H * 3 // 4 + (V // 32) * 128
+    total = kv_bytes + dn_bytes + w_bytes + lm_bytes
+    r = _hbm(us, total)
+    r.update({"sequences": B, "sum_len": int(lens.sum()), "kv_bytes": kv_bytes, "deltanet_state_bytes": dn_bytes,
+              "lut6_ffn_bytes": w_bytes, "lm_head_bytes": lm_bytes,
+              "note": "q/k of the attention layers enter already normalised and rotated"})
+    return r
+
+
 def cpu_baseline(seconds=12.0):
     """The oracle (a single-threaded C restatement of the reference cpu_ops
     path) on a bounded sample of the same step: one block of four layers
@@ -453,6 +549,9 @@ def main():
         del keep
         torch.cuda.empty_cache()
         cores = None if args.skip_cores else measure_cores(anelm, torch, dev)
+        if cores is not None:
+            torch.cuda.empty_cache()
+            cores["batch32_decode_step"] = measure_batch32_step(anelm, torch, dev)
 
     b = step_bytes()
     gbps = b["total"] / (us_step * 1e-6) / 1e9
