@@ -397,132 +397,173 @@ __global__ __launch_bounds__(kPreNT, 2) void dn_chunk_pre_kernel(float* __restri
 }
 
 // Sequential part: workgroup (slab of 16 state columns, value head) keeps its
-// 128 x 16 slab of S in registers across all chunks; thread (c = tid & 15,
-// rb = tid >> 4) holds rows 8 rb .. 8 rb + 7 of column c.  Per chunk:
-//   U = Ut - Wm S0;  y = Op + Qh S0;  S = gC S0 + Kh^T U
-// with Wm, Qh, Kh staged through LDS (the next one is loaded into registers
-// while the current one is used); the 16 row-block partial sums are first
-// combined within each wave (4 row blocks per wave) and then across the 4
-// waves in LDS.
-constexpr int kSeqNT = 256;
+// The state is carried through the chunks in slabs of 16 columns (8 per head).
 constexpr int kSeqCB = 16;
 constexpr int kSlabs = kDV / kSeqCB;
-__device__ __forceinline__ void dn_seq_fetch(float4 (&r)[8], const float* src, int tid) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) r[k] = reinterpret_cast<const float4*>(src)[tid + kSeqNT * k];
-}
-__device__ __forceinline__ void dn_seq_park(float* dst, const float4 (&r)[8], int tid) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) reinterpret_cast<float4*>(dst)[tid + kSeqNT * k] = r[k];
-}
-// part[t] = sum over this thread's 8 rows of M[t][row] * s[row], summed over
-// the wave's 4 row blocks (lanes sharing lane & 15)
-__device__ __forceinline__ void dn_seq_rowdot(float (&part)[kChunk], const float* M, const float (&s)[8], int rb) {
-#pragma unroll
-    for (int t = 0; t < kChunk; t++) {
-        const float4* mrow = reinterpret_cast<const float4*>(M + t * kDK + 8 * rb);
-        const float4 m0 = mrow[0], m1 = mrow[1];
-        const float a0 = fmaf(m0.y, s[1], m0.x * s[0]);
-        const float a1 = fmaf(m0.w, s[3], m0.z * s[2]);
-        const float a2 = fmaf(m1.y, s[5], m1.x * s[4]);
-        const float a3 = fmaf(m1.w, s[7], m1.z * s[6]);
-        part[t] = (a0 + a1) + (a2 + a3);
-    }
-#pragma unroll
-    for (int t = 0; t < kChunk; t++) {
-        part[t] += __shfl_xor(part[t], 16, 64);
-        part[t] += __shfl_xor(part[t], 32, 64);
-    }
-}
 
-__global__ __launch_bounds__(kSeqNT) void dn_chunk_seq_kernel(float* __restrict__ y, float* __restrict__ state,
-                                                              const float* __restrict__ rec, int S, int Hv,
-                                                              int n_chunks) {
-    __shared__ __attribute__((aligned(16))) float M[2][kCMat];           // 64 KB: current / next matrix
-    __shared__ __attribute__((aligned(16))) float red[4][kChunk][kSeqCB];  // 16 KB: per-wave sums
-    __shared__ __attribute__((aligned(16))) float Ul[kChunk][kSeqCB];      // 4 KB
-    // XCD-aware: workgroups are dealt round-robin over the 8 XCDs (id % 8);
-    // the 8 slabs of a head share its chunk matrices, so they go to one XCD
-    // (one L2) -- with Hv a multiple of 8, heads 4x .. 4x+3 on XCD x
+// ------------------------------------------------ chunk scan on fp32 MFMA
+// The same three products per chunk on v_mfma_f32_16x16x4_f32 (fp32 inputs,
+// fp32 accumulation).  A workgroup (4 waves, one per SIMD) owns a 16-column
+// slab of one head's state, kept in LDS column-major (Sc[c][i]):
+//   wave w: X = Wm S0 and Y = Qh S0 for chunk rows t in [16w, 16w + 16)
+//           (32 MFMAs each over the 128 state rows), U = Ut - X, y = Op + Y;
+//   then    S = gC S0 + Kh^T U for state rows i in [32w, 32w + 32)
+//           (2 tiles x 16 MFMAs over the 64 chunk rows).
+// MFMA operand layouts (16x16x4, one block): A[m][k] in lane m + 16 k,
+// B[k][n] in lane n + 16 k, D[m][n] in lane n + 16 (m / 4), element m % 4.
+// The contraction index is permuted identically in both operands: lane (m, k)
+// of k-step (x, e) takes state row (or chunk row) 16 x + 4 k + e, so an A
+// operand is one 16-byte read per lane and four.
+// The chunk's operands (Wm, Qh, Kh whole; the slab's columns of Ut and Op)
+// stream into LDS with buffer loads (16 bytes per lane, 1 KiB per wave
+// instruction) while the previous chunk is computed; each wave then reads its
+// operands from LDS into registers.  Wm / Qh rows are stored with their
+// 16-byte chunks XOR-swizzled by the row (conflict-free operand reads).
+constexpr int kMsNT = 256;
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kScP = kDK + 4;                      // Sc row pitch (floats)
+constexpr int kOpWm = 0, kOpQh = kCMat, kOpKh = 2 * kCMat;   // operand buffer (floats)
+constexpr int kOpUt = 3 * kCMat, kOpOp = 3 * kCMat + kChunk * 16;
+constexpr int kOpFloats = 3 * kCMat + 2 * kChunk * 16;
+constexpr int kMsLds = (kOpFloats + kSeqCB * kScP + kChunk * (kSeqCB + 1)) * 4;
+
+__global__ __launch_bounds__(kMsNT) __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_chunk_mfma_kernel(
+    float* __restrict__ y, float* __restrict__ state, const float* __restrict__ rec, int S, int Hv, int n_chunks) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* opb = smem;                                     // operand buffer
+    float (*Sc)[kScP] = reinterpret_cast<float (*)[kScP]>(smem + kOpFloats);        // state slab
+    float (*Ul)[kSeqCB + 1] = reinterpret_cast<float (*)[kSeqCB + 1]>(smem + kOpFloats + kSeqCB * kScP);
+    // XCD-aware: the 8 slabs of a head share its chunk matrices, so they go to
+    // one XCD (workgroup id mod 8 selects the XCD; Hv * 8 workgroups)
     const int nwg = gridDim.x, id = blockIdx.x;
-    const int per_xcd = nwg / 8, k = id / 8, xcd = id % 8;
-    const int h = (xcd * per_xcd + k) / kSlabs, slab = (xcd * per_xcd + k) % kSlabs;
-    const int tid = threadIdx.x;
-    const int c = tid & (kSeqCB - 1), rb = tid >> 4, w = tid >> 6;
-    const bool lead = (tid & 63) < kSeqCB;   // one lane per column of each wave
-    const int col = slab * kSeqCB + c;
+    const int per_xcd = nwg / 8, k8 = id / 8, xcd = id % 8;
+    const int h = (xcd * per_xcd + k8) / kSlabs, slab = (xcd * per_xcd + k8) % kSlabs;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lq = lane >> 4;
+    const int c0 = slab * kSeqCB, col = c0 + lr;
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(y, 0, (int)((size_t)S * Hv * kDV * 4), 0x00020000);
+    // per-lane byte offsets of this wave's 26 operand loads within a chunk record
+    // (instruction k of the workgroup covers 1 KiB of the operand buffer)
+    auto issue = [&](int ch) __attribute__((always_inline)) {
+        // one chunk record per resource: offsets stay small for any sequence length
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(rec) + ((size_t)ch * Hv + h) * kCRec, 0, kCRec * 4, 0x00020000);
+        constexpr int base = 0;
+        char* ob = reinterpret_cast<char*>(opb);
+        // Wm, Qh: 32 instructions each (rows 2k, 2k+1); Kh: 32 (straight copy)
+#pragma unroll
+        for (int x = 0; x < 8; x++) {
+            const int k = 8 * w + x, row = 2 * k + (lane >> 5), p = lane & 31, c = p ^ (row & 15);
+            const int go = row * kDK * 4 + c * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpWm * 4 + k * 1024)), 16,
+                                                     base + kCMat * 4 + go, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpQh * 4 + k * 1024)), 16,
+                                                     base + 3 * kCMat * 4 + go, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpKh * 4 + k * 1024)), 16,
+                                                     base + 4 * kCMat * 4 + k * 1024 + lane * 16, 0, 0, 0);
+        }
+        // the slab's 16 columns of Ut and Op: row 16 w + lane / 4, 16-byte chunk lane % 4
+        const int go = (16 * w + (lane >> 2)) * kDK * 4 + c0 * 4 + (lane & 3) * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpUt * 4 + w * 1024)), 16,
+                                                 base + go, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpOp * 4 + w * 1024)), 16,
+                                                 base + 2 * kCMat * 4 + go, 0, 0, 0);
+    };
+
     float* Sp = state + (size_t)h * kDK * kDV;
-    float s[8];
-#pragma unroll
-    for (int r = 0; r < 8; r++) s[r] = Sp[(size_t)(8 * rb + r) * kDV + col];
-    float4 nxt[8];
-    dn_seq_fetch(nxt, rec + (size_t)h * kCRec + kCMat, tid);   // Wm of chunk 0
-    int buf = 0;
-    for (int ch = 0; ch < n_chunks; ch++) {
-        const float* rc = rec + ((size_t)ch * Hv + h) * kCRec;
-        const int t0 = ch * kChunk, L = min(kChunk, S - t0);
-        float part[kChunk];
-        // this thread's 4 rows of Ut and Op (t = 4 rb + k), issued early
-        float ut[4], op[4];
-        const float gC = rc[5 * kCMat];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            ut[k] = rc[(4 * rb + k) * kDK + col];
-            op[k] = rc[2 * kCMat + (4 * rb + k) * kDK + col];
-        }
-        // ---- U = Ut - Wm S0
-        dn_seq_park(M[buf], nxt, tid);
-        lds_barrier();
-        dn_seq_fetch(nxt, rc + 3 * kCMat, tid);                 // Qh
-        dn_seq_rowdot(part, M[buf], s, rb);
-        if (lead) {
-#pragma unroll
-            for (int t = 0; t < kChunk; t++) red[w][t][c] = part[t];
-        }
-        buf ^= 1;
-        dn_seq_park(M[buf], nxt, tid);
-        lds_barrier();
-        dn_seq_fetch(nxt, rc + 4 * kCMat, tid);                 // Kh
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int t = 4 * rb + k;
-            Ul[t][c] = ut[k] - (red[0][t][c] + red[1][t][c] + red[2][t][c] + red[3][t][c]);
-        }
-        // ---- y = Op + Qh S0
-        dn_seq_rowdot(part, M[buf], s, rb);
-        lds_barrier();   // red consumed by the U rows above
-        if (lead) {
-#pragma unroll
-            for (int t = 0; t < kChunk; t++) red[w][t][c] = part[t];
-        }
-        buf ^= 1;
-        dn_seq_park(M[buf], nxt, tid);
-        lds_barrier();
-        if (ch + 1 < n_chunks) dn_seq_fetch(nxt, rc + (size_t)Hv * kCRec + kCMat, tid);   // next Wm
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int t = 4 * rb + k;
-            if (t < L)
-                y[((size_t)(t0 + t) * Hv + h) * kDV + col] =
-                    op[k] + (red[0][t][c] + red[1][t][c] + red[2][t][c] + red[3][t][c]);
-        }
-        // ---- S = gC S0 + Kh^T U
-        const float* Kh = M[buf];
-#pragma unroll
-        for (int r = 0; r < 8; r++) s[r] *= gC;
-#pragma unroll 4
-        for (int t = 0; t < kChunk; t++) {
-            const float uv = Ul[t][c];
-            const float4* krow = reinterpret_cast<const float4*>(Kh + t * kDK + 8 * rb);
-            const float4 k0 = krow[0], k1 = krow[1];
-            s[0] = fmaf(k0.x, uv, s[0]); s[1] = fmaf(k0.y, uv, s[1]); s[2] = fmaf(k0.z, uv, s[2]); s[3] = fmaf(k0.w, uv, s[3]);
-            s[4] = fmaf(k1.x, uv, s[4]); s[5] = fmaf(k1.y, uv, s[5]); s[6] = fmaf(k1.z, uv, s[6]); s[7] = fmaf(k1.w, uv, s[7]);
-        }
-        lds_barrier();   // Ul, red and M[buf] are rewritten in the next chunk
-        buf ^= 1;
+    for (int e = tid; e < kDK * kSeqCB; e += kMsNT) {
+        const int i = e / kSeqCB, c = e % kSeqCB;
+        Sc[c][i] = Sp[(size_t)i * kDV + c0 + c];
     }
+    issue(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's part of chunk 0 landed
+    lds_barrier();
+
+    for (int ch = 0; ch < n_chunks; ch++) {
+        const int t0 = ch * kChunk;
+        // ---- operands of this chunk from LDS
+        float4 wa[8], qa[8], sb[8];
+        {
+            const int row = 16 * w + lr;
 #pragma unroll
-    for (int r = 0; r < 8; r++) Sp[(size_t)(8 * rb + r) * kDV + col] = s[r];
+            for (int x = 0; x < 8; x++) {
+                const int c = (4 * x + lq) ^ (row & 15);
+                wa[x] = *reinterpret_cast<const float4*>(opb + kOpWm + row * kDK + 4 * c);
+                qa[x] = *reinterpret_cast<const float4*>(opb + kOpQh + row * kDK + 4 * c);
+                sb[x] = *reinterpret_cast<const float4*>(&Sc[lr][16 * x + 4 * lq]);
+            }
+        }
+        float kh[2][16];
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+                kh[tb][s] = opb[kOpKh + (16 * (s >> 2) + 4 * lq + (s & 3)) * kDK + 32 * w + 16 * tb + lr];
+        float utv[4], opv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            utv[j] = opb[kOpUt + (16 * w + 4 * lq + j) * 16 + lr];
+            opv[j] = opb[kOpOp + (16 * w + 4 * lq + j) * 16 + lr];
+        }
+        const float gc = rec[((size_t)ch * Hv + h) * kCRec + 5 * kCMat];
+        lds_barrier();   // every wave holds its operands: the buffer takes the next chunk
+        if (ch + 1 < n_chunks) issue(ch + 1);
+        // ---- X = Wm S0, Y = Qh S0 (four independent accumulation chains)
+        v4f X0 = {0.f, 0.f, 0.f, 0.f}, X1 = X0, Y0 = X0, Y1 = X0;
+#pragma unroll
+        for (int x = 0; x < 8; x++) {
+            X0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].x, sb[x].x, X0, 0, 0, 0);
+            Y0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].x, sb[x].x, Y0, 0, 0, 0);
+            X1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].y, sb[x].y, X1, 0, 0, 0);
+            Y1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].y, sb[x].y, Y1, 0, 0, 0);
+            X0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].z, sb[x].z, X0, 0, 0, 0);
+            Y0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].z, sb[x].z, Y0, 0, 0, 0);
+            X1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].w, sb[x].w, X1, 0, 0, 0);
+            Y1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].w, sb[x].w, Y1, 0, 0, 0);
+        }
+        const v4f X = X0 + X1, Y = Y0 + Y1;
+        // ---- U = Ut - X (to LDS), y = Op + Y; element j is chunk row 16w + 4 lq + j
+        // (y rows past S fall out of the buffer range and are dropped)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int t = 16 * w + 4 * lq + j;
+            Ul[t][lr] = utv[j] - X[j];
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, opv[j] + Y[j]), ry,
+                                                  (((t0 + t) * Hv + h) * kDV + col) * 4, 0, 0);
+        }
+        lds_barrier();   // U complete; every wave's reads of S0 are done
+        // ---- S = gC S0 + Kh^T U for state rows 32w + 16 tb + (0..15)
+        float ubv[16];
+#pragma unroll
+        for (int s = 0; s < 16; s++) ubv[s] = Ul[16 * (s >> 2) + 4 * lq + (s & 3)][lr];
+        v4f Sn[2][2];
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                Sn[tb][0][j] = gc * Sc[lr][32 * w + 16 * tb + 4 * lq + j];
+                Sn[tb][1][j] = 0.f;
+            }
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int tb = 0; tb < 2; tb++)
+                Sn[tb][s & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kh[tb][s], ubv[s], Sn[tb][s & 1], 0, 0, 0);
+        // rows written here are read (as C) only by this wave
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++) {
+            const v4f sn = Sn[tb][0] + Sn[tb][1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) Sc[lr][32 * w + 16 * tb + 4 * lq + j] = sn[j];
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's part of the next chunk landed (and its y stores)
+        lds_barrier();   // new state complete, U consumed, next chunk's operands in LDS
+    }
+    for (int e = tid; e < kDK * kSeqCB; e += kMsNT) {
+        const int i = e / kSeqCB, c = e % kSeqCB;
+        Sp[(size_t)i * kDV + c0 + c] = Sc[c][i];
+    }
 }
 
 }  // namespace
@@ -595,6 +636,8 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
     ANELM_REQUIRE(S >= 0, "deltanet_prefill: S %d", S);
     ANELM_REQUIRE(chunk == kChunk || chunk == 1,
                   "deltanet_prefill: chunk %d (64: chunked form; 1: token-by-token scan)", chunk);
+    ANELM_REQUIRE((size_t)(S + kChunk) * Hv * kDV * sizeof(float) < 0x7fffffffu,
+                  "deltanet_prefill: %d tokens x %d heads exceed the 2 GiB output range", S, Hv);
     ANELM_REQUIRE((flags & ~3) == 0, "deltanet_prefill: flags 0x%x (GATED_NORM is decode-only)", flags);
     if (S == 0) return ANELM_OK;
     hipStream_t st = as_stream(stream);
@@ -627,8 +670,14 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
                            v, beta, ldecay, S, Hk, Hv);
     ANELM_LAUNCHED("dn_chunk_pre_kernel");
     // grid = Hv * kSlabs, a multiple of 8 (XCD mapping inside the kernel)
-    hipLaunchKernelGGL(dn_chunk_seq_kernel, dim3(kSlabs * Hv), dim3(kSeqNT), 0, st, y, state, rec, S, Hv,
+    static bool ms_attr = false;
+    if (!ms_attr) {
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&dn_chunk_mfma_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kMsLds));
+        ms_attr = true;
+    }
+    hipLaunchKernelGGL(dn_chunk_mfma_kernel, dim3(kSlabs * Hv), dim3(kMsNT), kMsLds, st, y, state, rec, S, Hv,
                        n_chunks);
-    ANELM_LAUNCHED("dn_chunk_seq_kernel");
+    ANELM_LAUNCHED("dn_chunk_mfma_kernel");
     return ANELM_OK;
 }
