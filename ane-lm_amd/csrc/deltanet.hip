@@ -129,25 +129,36 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
 // Pre-pass: per (token, key head) l2-normalise q and k and scale q
 // (qwen3_5.cpp:879-887); per (token, value head) beta and decay
 // (qwen3_5.cpp:896-898).
-__global__ __launch_bounds__(kDK) void dn_prep_kernel(float* qn, float* kn, float* beta, float* decay,
-                                                      float* ldecay, const float* q, const float* k,
-                                                      const float* a, const float* b, const float* A,
-                                                      const float* dt_bias, int Hk, int Hv, int flags) {
-    __shared__ float red[kDK / 64];
-    const int t = blockIdx.x, kh = blockIdx.y, i = threadIdx.x;
-    const size_t off = ((size_t)t * Hk + kh) * kDK + i;
-    float qv = q[off], kv = k[off];
+// One wave per (token, key head) row, four rows per workgroup; each lane
+// holds two adjacent elements and the norms reduce within the wave.
+constexpr int kPrepRows = 4;
+__global__ __launch_bounds__(64 * kPrepRows) void dn_prep_kernel(float* qn, float* kn, float* beta, float* decay,
+                                                                 float* ldecay, const float* q, const float* k,
+                                                                 const float* a, const float* b, const float* A,
+                                                                 const float* dt_bias, int S, int Hk, int Hv,
+                                                                 int flags) {
+    const int row = blockIdx.x * kPrepRows + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= S * Hk) return;   // (no barrier in this kernel)
+    const int t = row / Hk, kh = row % Hk;
+    const size_t off = (size_t)row * kDK + 2 * lane;
+    float2 qv = *reinterpret_cast<const float2*>(q + off), kv = *reinterpret_cast<const float2*>(k + off);
     if (flags & ANELM_DN_L2NORM) {
-        const float sq = block_sum<kDK>(qv * qv, red);
-        const float sk = block_sum<kDK>(kv * kv, red);
-        qv = qv * (1.0f / sqrtf(sq + 1e-12f));
-        kv = kv * (1.0f / sqrtf(sk + 1e-12f));
+        float sq = qv.x * qv.x + qv.y * qv.y, sk = kv.x * kv.x + kv.y * kv.y;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            sq += __shfl_xor(sq, m, 64);
+            sk += __shfl_xor(sk, m, 64);
+        }
+        const float iq = 1.0f / sqrtf(sq + 1e-12f), ik = 1.0f / sqrtf(sk + 1e-12f);
+        qv = make_float2(qv.x * iq, qv.y * iq);
+        kv = make_float2(kv.x * ik, kv.y * ik);
     }
-    qn[off] = qv * (1.0f / sqrtf((float)kDK));
-    kn[off] = kv;
+    const float qs = 1.0f / sqrtf((float)kDK);
+    *reinterpret_cast<float2*>(qn + off) = make_float2(qv.x * qs, qv.y * qs);
+    *reinterpret_cast<float2*>(kn + off) = kv;
     const int group = Hv / Hk;
-    if (i < group) {
-        const int h = kh * group + i;
+    for (int gi = lane; gi < group; gi += 64) {
+        const int h = kh * group + gi;
         const size_t g = (size_t)t * Hv + h;
         beta[g] = 1.0f / (1.0f + expf(-b[g]));
         const float sp = logf(1.0f + expf(a[g] + dt_bias[h]));
@@ -653,8 +664,8 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
     float* decay = beta + ng;
     float* ldecay = decay + ng;
     float* rec = ws + rec_off;
-    hipLaunchKernelGGL(dn_prep_kernel, dim3(S, Hk), dim3(kDK), 0, st, qn, kn, beta, decay, ldecay, q, k, a,
-                       b, A, dt_bias, Hk, Hv, flags);
+    hipLaunchKernelGGL(dn_prep_kernel, dim3((S * Hk + kPrepRows - 1) / kPrepRows), dim3(64 * kPrepRows), 0, st, qn,
+                       kn, beta, decay, ldecay, q, k, a, b, A, dt_bias, S, Hk, Hv, flags);
     ANELM_LAUNCHED("dn_prep_kernel");
     if (chunk == 1) {
         hipLaunchKernelGGL(dn_scan_kernel, dim3(kDV / kScanCB, Hv), dim3(kScanNT), 0, st, y, state, qn,
