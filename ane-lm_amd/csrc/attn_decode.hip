@@ -342,6 +342,214 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
 }
 
+// Paged decode over many sequences: a workgroup owns kPagedChunks chunks of
+// 256/G keys of one (sequence, kv head) and walks them one after the other
+// (online softmax across chunks: running maximum per head, rescaled sums).
+// The split's page-table entries are read once into LDS.  Fewer, longer
+// splits than the ring path also shrink the partial records 4x.
+constexpr int kPagedChunks = 4;
+
+template <typename KV, int D, int G>
+__global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
+    constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
+    constexpr int KPI = 64 / LPK;     // key rows per wave instruction
+    constexpr int KPB = kNW * KPI;    // key rows per workgroup instruction
+    constexpr int KB = LPK / G;       // instructions per chunk
+    constexpr int CK = KPB * KB;      // keys per chunk (= 256 / G)
+    constexpr int KPS = CK * kPagedChunks;
+    constexpr int REC = D + 2;
+    static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
+
+    __shared__ float sc[G][CK];
+    __shared__ float red_g[kNW][G];
+    __shared__ float red_o[kNW][G][D];
+    __shared__ int pg[KPS + 1];   // page-table entries of the split (any page size)
+
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int Hkv = p.n_kv_heads;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int sub = lane / LPK, dl = lane % LPK;
+    const int len = min(p.seq_lens[seq], p.len);
+    float* out = p.out + (size_t)seq * Hkv * G * D;
+    if (len <= 0) {   // empty sequence: zeros, as cpu_ops.cpp:152-155
+        if (split == 0)
+            for (int e = tid; e < G * D; e += kNT) out[(size_t)kvh * G * D + e] = 0.f;
+        return;
+    }
+    const int n_splits = (len + KPS - 1) / KPS;
+    if (split >= n_splits) return;   // (uniform: before any barrier)
+    const int k0 = split * KPS, nk_all = min(KPS, len - k0);
+    const int nch = (nk_all + CK - 1) / CK;
+    const float* q = p.q + (size_t)seq * Hkv * G * p.q_stride;
+
+    const int ps = p.page_size;
+    const int pfirst = k0 / ps, pcount = (k0 + nk_all - 1) / ps - pfirst + 1;
+    const int32_t* ptab = p.page_table + (size_t)seq * p.max_pages;
+    for (int i = tid; i < pcount; i += kNT) pg[i] = min(max(ptab[pfirst + i], 0), p.n_pages - 1);
+    float qr[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float* src = q + (size_t)(kvh * G + g) * p.q_stride + dl * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) qr[g][i] = src[i];
+    }
+    lds_barrier();
+
+    const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
+    const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
+    // rows past the split's last key load that key again (masked below): the
+    // loads stay unconditional, so the counted waits stay exact
+    auto load_rows = [&](int c, const KV* base, Raw8<KV> (&r)[KB]) __attribute__((always_inline)) {
+        c = min(c, nch - 1);   // (past the last chunk: reload it, unused)
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int lt = min(c * CK + b * KPB + w * KPI + sub, nk_all - 1);   // key index inside the split
+            const int kt = k0 + lt;
+            const int page = pg[kt / ps - pfirst], row = kt % ps;
+            r[b] = load_raw(base + (((size_t)page * Hkv + kvh) * ps + row) * D + dl * 8);
+        }
+    };
+
+    float m[G], lsum[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        lsum[g] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
+    }
+    auto chunk = [&](int c, const Raw8<KV> (&rk)[KB], const Raw8<KV> (&rv)[KB]) __attribute__((always_inline)) {
+        const int nk = min(CK, nk_all - c * CK);
+        // ---- scores: one transpose reduction over the KB rows of each lane
+        {
+            float part[KB * G];
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                float kf[8];
+                to_f32(rk[b], kf);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    float sv = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sv = fmaf(qr[g][i], kf[i], sv);
+                    part[b * G + g] = sv;
+                }
+            }
+            transpose_reduce<LPK, KB * G>(part, dl);
+            const int b = dl / G, g = dl % G;
+            const int t = b * KPB + w * KPI + sub;
+            sc[g][t] = t < nk ? part[0] * p.scale : -INFINITY;
+        }
+        lds_barrier();
+        // ---- running maximum per head (one reduction for all G heads)
+        float mc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float v = -INFINITY;
+            for (int t = tid; t < CK; t += kNT) v = fmaxf(v, sc[g][t]);
+            mc[g] = wave_max(v);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++) red_g[w][g] = mc[g];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float mx = red_g[0][g];
+#pragma unroll
+            for (int ww = 1; ww < kNW; ww++) mx = fmaxf(mx, red_g[ww][g]);
+            const float m_new = fmaxf(m[g], mx);
+            const float alpha = __expf(m[g] - m_new);   // 0 on the first chunk (m = -inf)
+            lsum[g] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[g][i] *= alpha;
+            m[g] = m_new;
+            for (int t = tid; t < CK; t += kNT) {
+                const float e = __expf(sc[g][t] - m_new);   // masked keys: exp(-inf) = 0
+                sc[g][t] = e;
+                lsum[g] += e;
+            }
+        }
+        lds_barrier();
+        // ---- P V
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            const int t = b * KPB + w * KPI + sub;
+            float vf[8];
+            to_f32(rv[b], vf);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float pgv = sc[g][t];
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pgv, vf[i], acc[g][i]);
+            }
+        }
+        lds_barrier();   // sc is rewritten by the next chunk
+    };
+
+    // one chunk's rows in registers at a time (several workgroups per CU hide
+    // each other's load latency)
+    for (int c = 0; c < nch; c++) {
+        Raw8<KV> rk[KB], rv[KB];
+        load_rows(c, kc, rk);
+        load_rows(c, vc, rv);
+        chunk(c, rk, rv);
+    }
+
+    // ---- totals: l over the workgroup, O over the lanes sharing dims and the waves
+    float lt[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) lt[g] = wave_sum(lsum[g]);
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) red_g[w][g] = lt[g];
+    }
+#pragma unroll
+    for (int mm = LPK; mm < 64; mm <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[g][i] += shfl_xor(acc[g][i], mm);
+    if (sub == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) red_o[w][g][dl * 8 + i] = acc[g][i];
+    }
+    lds_barrier();
+    float ltot[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        ltot[g] = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kNW; ww++) ltot[g] += red_g[ww][g];
+    }
+    if (n_splits == 1) {
+        for (int e = tid; e < G * D; e += kNT) {
+            const int g = e / D, d = e % D;
+            float o = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+            const int hq = kvh * G + g;
+            float yv = o / ltot[g];
+            if (p.gate) yv = yv / (1.0f + expf(-q[(size_t)hq * p.q_stride + D + d]));
+            out[(size_t)hq * D + d] = yv;
+        }
+        return;
+    }
+    float* rec = p.part + (((size_t)seq * Hkv + kvh) * p.max_splits + split) * G * REC;
+    for (int e = tid; e < G * D; e += kNT) {
+        const int g = e / D, d = e % D;
+        float o = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+        rec[(size_t)g * REC + 2 + d] = o;
+        if (d == 0) { rec[(size_t)g * REC] = m[g]; rec[(size_t)g * REC + 1] = ltot[g]; }
+    }
+}
+
 // Log-sum-exp merge of the split partials of one (sequence, q head) for 64
 // output dims per workgroup: M = max m_s, L = sum l_s e^(m_s-M),
 // O = sum o_s e^(m_s-M), out = O / L, then the sigmoid gate.  The 256
@@ -402,8 +610,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p)
 
 template <typename KV, int D, int G>
 int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
-    ANELM_LAUNCHED("attn_decode_kernel");
+    if (p.paged) {
+        hipLaunchKernelGGL((attn_paged_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
+        ANELM_LAUNCHED("attn_paged_kernel");
+    } else {
+        hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
+        ANELM_LAUNCHED("attn_decode_kernel");
+    }
     if (p.max_splits > 1) {
         dim3 cgrid(D / 64, grid.y * G, grid.z);
         hipLaunchKernelGGL((attn_combine_kernel<D, G>), cgrid, dim3(256), 0, st, p);
@@ -434,14 +647,14 @@ int launch_kv(DecodeParams& p, int D, int G, dim3 grid, hipStream_t st) {
 }
 
 // Sets the split layout and workspace for one decode call, then launches.
-// A split is 256/G keys: every lane of the workgroup then loads all of its
-// K and V rows at once.  `max_len` bounds every sequence's key count;
+// A split is 256/G keys (ring mode: every lane of the workgroup then loads all
+// of its K and V rows at once) or kPagedChunks such chunks (paged mode).  `max_len` bounds every sequence's key count;
 // `n_seqs` sequences (1 in ring mode).
 int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, int max_len,
                hipStream_t st) {
     const int Hkv = p.n_kv_heads;
     const int G = n_heads / Hkv;
-    const int kps = 256 / G;
+    const int kps = (256 / G) * (p.paged ? kPagedChunks : 1);
     const int max_splits = (max_len + kps - 1) / kps;
     p.kps = kps;
     p.max_splits = max_splits;

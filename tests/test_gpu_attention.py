@@ -120,10 +120,12 @@ def test_full_attn_decode_consecutive_steps_wrap_ring(anelm, orc, dev):
     assert (st, ln) == (3, 32)
 
 
-def test_paged_decode(anelm, orc, dev):
-    """Ragged sequences over shuffled 16-token pages."""
-    rng = np.random.default_rng(307)
-    n_seqs, nh, nkv, D, P = 6, 16, 4, 256, 16
+@pytest.mark.parametrize("nh,nkv,D,P", [(16, 4, 256, 16), (16, 2, 128, 5), (4, 4, 64, 32), (8, 1, 128, 1)])
+def test_paged_decode(anelm, orc, dev, nh, nkv, D, P):
+    """Ragged sequences over shuffled pages (lengths cross the split sizes of
+    every head grouping; page sizes that do and do not divide a split)."""
+    rng = np.random.default_rng(307 + P)
+    n_seqs = 6
     lens = np.array([1, 17, 300, 1024, 2049, 0], np.int32)
     max_len = 2049
     max_pages = (max_len + P - 1) // P
