@@ -62,6 +62,7 @@ SIGNATURES = {
     "anelm_lut6_swiglu": [_P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _P],
     "anelm_lut6_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "anelm_swiglu": [_P, _P, _P, _I64, _P],
+    "anelm_swiglu_rows": [_P, _P, _I, _I, _P],
     "anelm_lut6_topk": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "anelm_hybrid_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P, _I, _P],
     "anelm_hybrid_step_run": [_P, _P],

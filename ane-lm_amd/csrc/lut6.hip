@@ -481,6 +481,17 @@ __global__ void swiglu_kernel(float* h, const float* g, const float* u, int n) {
     }
 }
 
+// h[r][i] = silu(gu[r][i]) * gu[r][n + i]: the gate and up projections of row r
+// computed as one projection with 2n outputs (gate rows first).
+__global__ void swiglu_rows_kernel(float* h, const float* gu, int n, long total) {
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < total) {
+        const long r = e / n, i = e - r * n;
+        const float gv = gu[r * 2 * n + i];
+        h[e] = (gv / (1.0f + expf(-gv))) * gu[r * 2 * n + n + i];
+    }
+}
+
 // ---------------------------------------------------------------- top-k
 // Ordering (value desc, index asc): a precedes b.
 __device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
@@ -848,6 +859,19 @@ int anelm_swiglu(float* h, const float* g, const float* u, int64_t n, void* stre
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), h, g, u,
                        (int)n);
     ANELM_LAUNCHED("swiglu_kernel");
+    return ANELM_OK;
+}
+
+int anelm_swiglu_rows(float* h, const float* gu, int rows, int n, void* stream) {
+    ANELM_NONNULL(h);
+    ANELM_NONNULL(gu);
+    ANELM_REQUIRE(rows >= 0 && n >= 0, "swiglu_rows: rows %d n %d", rows, n);
+    const long total = (long)rows * n;
+    ANELM_REQUIRE(total / 256 < 0x7fffffffL, "swiglu_rows: %ld elements", total);
+    if (total == 0) return ANELM_OK;
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, as_stream(stream), h,
+                       gu, n, total);
+    ANELM_LAUNCHED("swiglu_rows_kernel");
     return ANELM_OK;
 }
 

@@ -247,6 +247,14 @@ def swiglu(g, u, out=None):
     return out
 
 
+def swiglu_rows(gu, n, out=None):
+    """h[r] = silu(gu[r][:n]) * gu[r][n:2n] for the stacked gate / up output gu [rows][2n]."""
+    rows = gu.numel() // (2 * n)
+    out = out if out is not None else torch.empty(rows, n, device=gu.device)
+    call("anelm_swiglu_rows", _p(out), _p(gu), rows, n, _s())
+    return out
+
+
 def lut6_topk(w, lut, x, out_dim, in_dim, k):
     batch = x.shape[0] if x.dim() == 2 else 1
     idx = torch.empty(batch, k, device=x.device, dtype=torch.int32)

@@ -358,8 +358,8 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
     layers, kv_bytes, dn_bytes = [], 0, 0
     for i in range(c["layers"]):
         L = {"ffn_norm": 1 + randn(H, std=0.02),
-             "gate": (randbytes(I, H * 3 // 4), randn(I // 32, 64, std=0.02, dtype=torch.float16)),
-             "up": (randbytes(I, H * 3 // 4), randn(I // 32, 64, std=0.02, dtype=torch.float16)),
+             # gate and up stacked as one projection ([gate; up] rows and LUT groups)
+             "gate_up": (randbytes(2 * I, H * 3 // 4), randn(2 * I // 32, 64, std=0.02, dtype=torch.float16)),
              "down": (randbytes(H, I * 3 // 4), randn(H // 32, 64, std=0.02, dtype=torch.float16))}
         if (i + 1) % 4 == 0:
             perm = rng.permutation(n_pages).astype(np.int32)
@@ -390,8 +390,7 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
     lens_d = torch.from_numpy(lens).to(dev)
     x = randn(B, H)
     xn = torch.empty(B, H, device=dev)
-    gv = torch.empty(B, I, device=dev)
-    uv = torch.empty(B, I, device=dev)
+    guv = torch.empty(B, 2 * I, device=dev)
     hv = torch.empty(B, I, device=dev)
     ops = anelm.ops
     max_len = int(lens.max())
@@ -405,9 +404,8 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
                 ops.deltanet_decode(L["S"], L["q"], L["k"], L["v"], L["a"], L["b"], L["A"], L["dt"], 1 | 4,
                                     L["z"], L["nw"], out=L["y"])
             ops.rmsnorm(x, L["ffn_norm"], c["eps"], out=xn)
-            ops.lut6_gemm(L["gate"][0], L["gate"][1], xn, I, H, out=gv)
-            ops.lut6_gemm(L["up"][0], L["up"][1], xn, I, H, out=uv)
-            ops.swiglu(gv, uv, out=hv)
+            ops.lut6_gemm(L["gate_up"][0], L["gate_up"][1], xn, 2 * I, H, out=guv)
+            ops.swiglu_rows(guv, I, out=hv)
             ops.lut6_gemm(L["down"][0], L["down"][1], hv, H, I, out=x, accumulate=True)
         return ops.lut6_topk(lm[0], lm[1], x, V, H, 32)
 

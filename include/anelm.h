@@ -232,6 +232,12 @@ int anelm_lut6_gemm(float* y, const uint8_t* w, const uint16_t* lut, const float
  * (models/llm/qwen3_5.cpp:1118-1130) on batched gate / up outputs. */
 int anelm_swiglu(float* h, const float* g, const float* u, int64_t n, void* stream);
 
+/* h[r][i] = silu(gu[r][i]) * gu[r][n + i] for r < rows, i < n: SwiGLU over the
+ * output of one projection that holds the gate rows then the up rows (a
+ * batched FFN computes gate and up in one anelm_lut6_gemm over the stacked
+ * [gate; up] weights).  Replaces qwen3_5.cpp:1123-1126 per row. */
+int anelm_swiglu_rows(float* h, const float* gu, int rows, int n, void* stream);
+
 /* Top-k of logits = W x for a batch of inputs (in-model top-k LM head,
  * scripts/export_hybrid_chunks.py:409-421).  x [batch][in_dim] fp32;
  * out_idx / out_val [batch][k], ordered by (value desc, index asc), so

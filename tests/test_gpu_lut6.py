@@ -90,6 +90,19 @@ def test_gemm_accumulate_and_batched_ffn(anelm, orc, dev):
         nb = orc.rmsnorm(x[b], w, 1e-6)
         want = x[b] + orc.lut6_ffn(nb, g[:2], u[:2], d[:2], H, I)
         assert_close(got[b], want, what=f"batched ffn input {b}")
+    # the same block with gate and up stacked into one projection ([gate; up]
+    # rows and LUT groups concatenated), one GEMM, then silu(g) * u per row
+    gu = (np.concatenate([g[0], u[0]]), np.concatenate([g[1], u[1]]))
+    xd2 = to_dev(x, dev)
+    n2 = anelm.ops.rmsnorm(xd2, to_dev(w, dev), 1e-6)
+    guv = anelm.ops.lut6_gemm(to_dev(gu[0], dev), to_dev(gu[1], dev), n2, 2 * I, H)
+    h2 = anelm.ops.swiglu_rows(guv, I)
+    assert_close(to_host(h2), to_host(h), what="stacked gate/up vs separate projections")
+    anelm.ops.lut6_gemm(dd[0], dd[1], h2, H, I, out=xd2, accumulate=True)
+    got2 = to_host(xd2)
+    for b in (0, 17, 31):
+        nb = orc.rmsnorm(x[b], w, 1e-6)
+        assert_close(got2[b], x[b] + orc.lut6_ffn(nb, g[:2], u[:2], d[:2], H, I), what=f"stacked ffn input {b}")
     # accumulate on its own: y0 + W x
     y0 = rng.standard_normal((5, 1024)).astype(np.float32)
     pk, lut, _ = lut6_matrix(662, 1024, 2560)
