@@ -17,6 +17,29 @@ __global__ __launch_bounds__(kNT) void rmsnorm_kernel(float* out, const float* x
     __shared__ float red[kNT / 64];
     const float* xr = x + (size_t)blockIdx.x * xs;
     float* orow = out + (size_t)blockIdx.x * os;
+    constexpr int kReg = 16;   // rows up to 16 * kNT elements stay in registers
+    if (dim <= kReg * kNT) {
+        // every load of the row issued at once (one memory round trip), then
+        // the sum and the scaled row from registers
+        float v[kReg], wv[kReg];
+#pragma unroll
+        for (int k = 0; k < kReg; k++) {
+            const int i = threadIdx.x + kNT * k;
+            v[k] = i < dim ? xr[i] : 0.f;
+            wv[k] = i < dim ? w[i] : 0.f;
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < kReg; k++) ss += v[k] * v[k];
+        ss = block_sum<kNT>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+        for (int k = 0; k < kReg; k++) {
+            const int i = threadIdx.x + kNT * k;
+            if (i < dim) orow[i] = (v[k] * inv) * wv[k];
+        }
+        return;
+    }
     float ss = 0.f;
     for (int i = threadIdx.x; i < dim; i += kNT) ss += xr[i] * xr[i];
     ss = block_sum<kNT>(ss, red);
