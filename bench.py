@@ -502,7 +502,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark measures one GPU; the decode step does not "
-                                   "shard across GPUs in this build (run with --gpus 1)"}))
+                                   "shard across GPUs here (run with --gpus 1)"}))
         sys.exit(2)
 
     import torch

@@ -1,7 +1,7 @@
 /*
  * anelm_oracle.c -- CPU restatement of ANE-LM's core/cpu_ops hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker).  Loaded by tests/, smoke() and the
+ * TEST INFRASTRUCTURE ONLY (the oracle).  Loaded by tests/, smoke() and the
  * cpu_baseline leg of bench.py; never by the product library.
  *
  * Accelerate calls in the reference are restated from their documented

@@ -1,7 +1,8 @@
 /*
  * anelm_oracle.h -- CPU restatement of ANE-LM's core/cpu_ops hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP kernels:
+ * TEST INFRASTRUCTURE ONLY.  This library is the reference the HIP kernels are
+ * tested against:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it.  The product path (ane-lm_amd/libanelm.so) never links or calls it.
  *

@@ -1,7 +1,7 @@
 """numpy binding of liboracle.so, the CPU restatement of ANE-LM's cpu_ops path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py as the checker.  The product library never uses
+cpu_baseline leg of bench.py, as the oracle.  The product library never uses
 it.  Every wrapper names the C function (and through it the reference
 file:line) it calls.
 """

@@ -33,7 +33,7 @@ def load_package():
 
 
 def load_oracle():
-    """Imports oracle/oracle.py as module `anelm_oracle` (the checker)."""
+    """Imports oracle/oracle.py as module `anelm_oracle` (the oracle)."""
     if "anelm_oracle" in sys.modules:
         return sys.modules["anelm_oracle"]
     path = os.path.join(ROOT, "oracle", "oracle.py")
