@@ -135,6 +135,48 @@ __device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p,
     __syncthreads();
 }
 
+// The same for the G rows rows[0..G) at once: one reduction round for all
+// the rows' sums of squares (partial sums in the same order as block_sum, so
+// every row is normalised bit-identically to norm_rope_row).
+template <int D, int G>
+__device__ void norm_rope_rows(float (*rows)[D], const float* w, const DecodeParams& p, float (*red_g)[G]) {
+    if (w != nullptr) {
+        float ss[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float v = 0.f;
+            for (int d = threadIdx.x; d < D; d += kNT) v += rows[g][d] * rows[g][d];
+            ss[g] = wave_sum(v);
+        }
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++) red_g[threadIdx.x >> 6][g] = ss[g];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < kNW; i++) t += red_g[i][g];
+            const float inv = 1.0f / sqrtf(t / (float)D + p.eps);
+            for (int d = threadIdx.x; d < D; d += kNT) rows[g][d] = (rows[g][d] * inv) * w[d];
+        }
+    }
+    __syncthreads();
+    const float* cs = p.cs;
+    const float* sn = p.sn;
+    for (int e = threadIdx.x; e < G * p.rot_pairs; e += kNT) {
+        const int g = e / p.rot_pairs, j = e - g * p.rot_pairs;
+        const int i0 = p.rope_mode == 0 ? 2 * j : j;
+        const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
+        const float c = cs[j], sv = sn[j];
+        const float v0 = rows[g][i0], v1 = rows[g][i1];
+        rotate_pair(rows[g][i0], rows[g][i1], v0, v1, c, sv);
+    }
+    __syncthreads();
+}
+
 template <typename KV, int D, int G>
 __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) {
     constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
@@ -149,6 +191,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     __shared__ float sc[G][256 / G];
     __shared__ float red_o[kNW][G][D];
     __shared__ float red[kNW];
+    __shared__ float red_g[kNW][G];
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -211,7 +254,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
     __syncthreads();
     if (p.fused) {
-        for (int g = 0; g < G; g++) norm_rope_row<D>(q_s[g], p.q_norm_w, p, red);
+        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g);
         if (owner) {
             for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
             __syncthreads();
@@ -264,24 +307,56 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     __syncthreads();
 
     // ---- softmax statistics per head over this split
+    // (one reduction round for all G heads each: the same per-wave partials
+    // and the same order over the waves as block_max / block_sum)
     float mloc[G], lloc[G];
+    {
+        float mw[G];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        float m = -INFINITY;
-        for (int t = tid; t < nk; t += kNT) m = fmaxf(m, sc[g][t]);
-        mloc[g] = block_max<kNT>(m, red);
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float l = 0.f;
-        for (int t = tid; t < nk; t += kNT) {
-            const float e = __expf(sc[g][t] - mloc[g]);
-            sc[g][t] = e;
-            l += e;
+        for (int g = 0; g < G; g++) {
+            float m = -INFINITY;
+            for (int t = tid; t < nk; t += kNT) m = fmaxf(m, sc[g][t]);
+            mw[g] = wave_max(m);
         }
-        lloc[g] = block_sum<kNT>(l, red);
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++) red_g[w][g] = mw[g];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float t = red_g[0][g];
+#pragma unroll
+            for (int i = 1; i < kNW; i++) t = fmaxf(t, red_g[i][g]);
+            mloc[g] = t;
+        }
+        __syncthreads();   // red_g is rewritten below
     }
-    __syncthreads();
+    {
+        float lw[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float l = 0.f;
+            for (int t = tid; t < nk; t += kNT) {
+                const float e = __expf(sc[g][t] - mloc[g]);
+                sc[g][t] = e;
+                l += e;
+            }
+            lw[g] = wave_sum(l);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++) red_g[w][g] = lw[g];
+        }
+        __syncthreads();   // (also publishes the probabilities in sc)
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < kNW; i++) t += red_g[i][g];
+            lloc[g] = t;
+        }
+    }
 
     // ---- P V
     float acc[G][8];
