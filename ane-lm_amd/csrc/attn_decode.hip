@@ -223,8 +223,13 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
     const bool owner = p.fused && split == sv.n_splits - 1;   // holds the newest key
 
-    // ---- every K and V row of this lane is requested first, so the HBM
-    // latency overlaps the q prologue below
+    // ---- the q rows are requested first (registers; D <= kNT), then every K
+    // and V row of this lane, so the q prologue below waits for q only (memory
+    // loads retire in issue order) and the K / V latency overlaps it
+    float qv[G];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        qv[g] = tid < D ? sv.q[(size_t)(kvh * G + g) * p.q_stride + tid] : 0.f;
     const int32_t* ptab = p.paged ? p.page_table + (size_t)seq * p.max_pages : nullptr;
     auto row_ptr = [&](const KV* base, int t) -> const KV* {
         const int lt = t0 + t;
@@ -248,9 +253,9 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
 
     // ---- q rows (and, for the split holding the newest key, the append)
-    for (int g = 0; g < G; g++) {
-        const float* src = sv.q + (size_t)(kvh * G + g) * p.q_stride;
-        for (int d = tid; d < D; d += kNT) q_s[g][d] = src[d];
+    if (tid < D) {
+#pragma unroll
+        for (int g = 0; g < G; g++) q_s[g][tid] = qv[g];
     }
     __syncthreads();
     if (p.fused) {
