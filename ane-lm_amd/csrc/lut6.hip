@@ -482,13 +482,28 @@ __global__ void swiglu_kernel(float* h, const float* g, const float* u, int n) {
 }
 
 // h[r][i] = silu(gu[r][i]) * gu[r][n + i]: the gate and up projections of row r
-// computed as one projection with 2n outputs (gate rows first).
-__global__ void swiglu_rows_kernel(float* h, const float* gu, int n, long total) {
-    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < total) {
-        const long r = e / n, i = e - r * n;
-        const float gv = gu[r * 2 * n + i];
-        h[e] = (gv / (1.0f + expf(-gv))) * gu[r * 2 * n + n + i];
+// computed as one projection with 2n outputs (gate rows first).  Row r is
+// blockIdx.y; each thread takes 4 consecutive elements (float4 when n % 4 == 0).
+__global__ void swiglu_rows_kernel(float* h, const float* gu, int n) {
+    const int r = blockIdx.y, i0 = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    const float* g = gu + (size_t)r * 2 * n;
+    float* hr = h + (size_t)r * n;
+    if ((n & 3) == 0) {
+        if (i0 < n) {
+            const float4 gv = *reinterpret_cast<const float4*>(g + i0);
+            const float4 uv = *reinterpret_cast<const float4*>(g + n + i0);
+            float4 o;
+            o.x = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
+            o.y = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
+            o.z = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
+            o.w = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+            *reinterpret_cast<float4*>(hr + i0) = o;
+        }
+        return;
+    }
+    for (int i = i0; i < min(i0 + 4, n); i++) {
+        const float gv = g[i];
+        hr[i] = (gv / (1.0f + expf(-gv))) * g[n + i];
     }
 }
 
@@ -866,11 +881,13 @@ int anelm_swiglu_rows(float* h, const float* gu, int rows, int n, void* stream) 
     ANELM_NONNULL(h);
     ANELM_NONNULL(gu);
     ANELM_REQUIRE(rows >= 0 && n >= 0, "swiglu_rows: rows %d n %d", rows, n);
-    const long total = (long)rows * n;
-    ANELM_REQUIRE(total / 256 < 0x7fffffffL, "swiglu_rows: %ld elements", total);
-    if (total == 0) return ANELM_OK;
-    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, as_stream(stream), h,
-                       gu, n, total);
+    ANELM_REQUIRE(rows <= 65535, "swiglu_rows: rows %d (at most 65535)", rows);
+    if (rows == 0 || n == 0) return ANELM_OK;
+    // 16-byte rows need 16-byte aligned buffers for the float4 path
+    ANELM_REQUIRE((n & 3) != 0 || ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(gu)) & 15) == 0,
+                  "swiglu_rows: buffers must be 16-byte aligned");
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((n + 1023) / 1024), (unsigned)rows), dim3(256), 0,
+                       as_stream(stream), h, gu, n);
     ANELM_LAUNCHED("swiglu_rows_kernel");
     return ANELM_OK;
 }
