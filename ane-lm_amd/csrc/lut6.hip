@@ -561,21 +561,69 @@ __device__ __forceinline__ Cand wave_offer(Cand L, Cand c, int lane, int k) {
 }
 
 // Stage 1: each workgroup selects the best k of one chunk of one batch row's
-// logits -- every wave keeps a running list over its quarter, then wave 0
-// merges the four lists -- into candidates [batch][n_chunks][k].
+// logits -- every wave selects over its quarter, then wave 0 merges the four
+// lists -- into candidates [batch][n_chunks][k].
+//
+// A wave first loads its 2048 logits (32 per lane) and sorts the 64 lane
+// maxima once; the k-th best lane maximum T is a threshold: the k lanes whose
+// maxima are not after T supply k elements that precede every element after
+// T, so the best k lie among the elements not after T.  Only those are queued
+// (64 LDS slots per wave, compacted by ballot prefix) and offered to the
+// running list when the queue fills and at the end; on random logits that is
+// one or two sort-and-merge passes per wave instead of 32.  The result is the
+// same (value desc, index asc) list as offering every element.
+constexpr int kTopkPerLane = kTopkChunk / 4 / 64;
 __global__ __launch_bounds__(256) void topk_stage1(const float* logits, int n, int k, int n_chunks,
                                                    float* cv, int* ci) {
     __shared__ Cand lists[4][64];
+    __shared__ Cand queue[4][64];
     const int chunk = blockIdx.x, b = blockIdx.y;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const float* row = logits + (size_t)b * n;
-    Cand L{-INFINITY, 0x7fffffff};
     const int base = chunk * kTopkChunk + w * (kTopkChunk / 4);
-    for (int j = 0; j < kTopkChunk / 4; j += 64) {
-        const int r = base + j + lane;
-        const Cand c = r < n ? Cand{row[r], r} : Cand{-INFINITY, 0x7fffffff};
-        L = wave_offer(L, c, lane, k);
+    float v[kTopkPerLane];
+#pragma unroll
+    for (int t = 0; t < kTopkPerLane; t++) v[t] = row[min(base + t * 64 + lane, n - 1)];
+    auto idx_of = [&](int t) { return base + t * 64 + lane < n ? base + t * 64 + lane : 0x7fffffff; };
+    Cand m{-INFINITY, 0x7fffffff};
+#pragma unroll
+    for (int t = 0; t < kTopkPerLane; t++) {
+        const int it = idx_of(t);
+        const float vt = it != 0x7fffffff ? v[t] : -INFINITY;
+        v[t] = vt;
+        if (before(vt, it, m.v, m.i)) m = Cand{vt, it};
     }
+    const Cand sm = wave_sort(m, lane);
+    const float tv = __shfl(sm.v, k - 1, 64);
+    const int ti = __shfl(sm.i, k - 1, 64);
+
+    Cand L{-INFINITY, 0x7fffffff};
+    int filled = 0;   // queue entries in use (wave-uniform)
+#pragma unroll
+    for (int t = 0; t < kTopkPerLane; t++) {
+        const int it = idx_of(t);
+        const bool pass = !before(tv, ti, v[t], it);
+        const uint64_t bits = __ballot(pass);
+        const int cnt = __popcll(bits);
+        if (cnt == 0) continue;
+        if (filled + cnt > 64) {
+            __builtin_amdgcn_wave_barrier();
+            const Cand q = lane < filled ? queue[w][lane] : Cand{-INFINITY, 0x7fffffff};
+            __builtin_amdgcn_wave_barrier();
+            L = wave_offer(L, q, lane, k);
+            filled = 0;
+        }
+        if (pass) {
+            const int pos = filled + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+            queue[w][pos] = Cand{v[t], it};
+        }
+        filled += cnt;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const Cand q = lane < filled ? queue[w][lane] : Cand{-INFINITY, 0x7fffffff};
+    L = wave_offer(L, q, lane, k);
+
     lists[w][lane] = L;
     __syncthreads();
     if (w != 0) return;
@@ -587,15 +635,35 @@ __global__ __launch_bounds__(256) void topk_stage1(const float* logits, int n, i
     }
 }
 
-// Stage 2: one wave per batch row merges the rows' chunk candidates.
+// Stage 2: one wave per batch row merges the rows' chunk candidates; the
+// lists are loaded eight at a time, the next eight while the current merge.
+constexpr int kTopkGroup = 8;
 __global__ __launch_bounds__(64) void topk_stage2(const float* cv, const int* ci, int n_chunks, int k,
                                                   int32_t* out_idx, float* out_val) {
     const int b = blockIdx.x, lane = threadIdx.x;
+    const int le = min(lane, k - 1);
+    Cand nx[kTopkGroup];
+    auto load_group = [&](int c0) {
+#pragma unroll
+        for (int g = 0; g < kTopkGroup; g++) {
+            const size_t o = ((size_t)b * n_chunks + min(c0 + g, n_chunks - 1)) * k + le;
+            nx[g] = Cand{cv[o], ci[o]};
+        }
+    };
+    load_group(0);
     Cand L{-INFINITY, 0x7fffffff};
-    for (int c = 0; c < n_chunks; c++) {
-        const size_t o = ((size_t)b * n_chunks + c) * k;
-        const Cand n = lane < k ? Cand{cv[o + lane], ci[o + lane]} : Cand{-INFINITY, 0x7fffffff};
-        L = wave_merge(L, n, lane);   // chunk lists arrive sorted
+    for (int c0 = 0; c0 < n_chunks; c0 += kTopkGroup) {
+        Cand cur[kTopkGroup];
+#pragma unroll
+        for (int g = 0; g < kTopkGroup; g++) cur[g] = nx[g];
+        load_group(c0 + kTopkGroup);
+#pragma unroll
+        for (int g = 0; g < kTopkGroup; g++) {
+            // lists past n_chunks and lanes past k are empty entries; the lists
+            // arrive sorted
+            const bool ok = c0 + g < n_chunks && lane < k;
+            L = wave_merge(L, ok ? cur[g] : Cand{-INFINITY, 0x7fffffff}, lane);
+        }
     }
     if (lane < k) {
         out_idx[(size_t)b * k + lane] = L.i;

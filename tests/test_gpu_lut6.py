@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from gpu_util import assert_close, rel_l2, to_dev, to_host
-from workloads import lut6_matrix, widen
+from workloads import lut6_matrix, pack_lut6, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -143,6 +143,52 @@ def test_topk(anelm, orc, dev, out_dim, in_dim, batch, k):
         _check_topk(orc, idx[b], val[b], logits, k)
         if k == 1:
             assert idx[b, 0] == orc.argmax(logits)
+
+
+def _topk_of_exact_logits(anelm, dev, target, in_dim, k):
+    """Runs lut6_topk on a matrix whose logits are exactly `target` (fp16
+    bit patterns): row r of LUT group g picks entry r % 32, which holds
+    target[r], for input 0; x = e_0, so every other term is an exact zero."""
+    out_dim = target.size
+    idx = np.zeros((out_dim, in_dim), dtype=np.uint8)
+    idx[:, 0] = np.arange(out_dim) % 32
+    lut = np.zeros((out_dim // 32, 64), dtype=np.uint16)
+    lut[:, :32] = target.reshape(-1, 32)
+    x = np.zeros(in_dim, dtype=np.float32)
+    x[0] = 1.0
+    i, v = anelm.ops.lut6_topk(to_dev(pack_lut6(idx), dev), to_dev(lut, dev), to_dev(x, dev), out_dim,
+                               in_dim, k)
+    return to_host(i)[0], to_host(v)[0]
+
+
+@pytest.mark.parametrize("layout", ["equal", "ascending", "descending", "one_lane", "three_levels"])
+@pytest.mark.parametrize("out_dim", [24576, 20000])
+def test_topk_selection_layouts(anelm, orc, dev, layout, out_dim):
+    """Selection on exact logits laid out against the per-lane thresholding of
+    the chunk pass: all ties, monotone runs (the best values in one wave or
+    spread over every lane), the best values in one lane of every wave, and
+    three tie levels.  20000 rows leave the last chunk partly empty.  Indices
+    and values must equal the oracle's (value desc, index asc) order."""
+    rng = np.random.default_rng(700)
+    r = np.arange(out_dim)
+    if layout == "equal":
+        t = np.full(out_dim, 0x3C00, dtype=np.uint16)                       # 1.0
+    elif layout == "ascending":
+        t = (0x1000 + r).astype(np.uint16)                                  # increasing positive fp16
+    elif layout == "descending":
+        t = (0x1000 + out_dim - 1 - r).astype(np.uint16)
+    elif layout == "one_lane":
+        t = rng.integers(0x1000, 0x2000, out_dim).astype(np.uint16)
+        hot = r % 64 == 5
+        t[hot] = rng.integers(0x4000, 0x4010, int(hot.sum())).astype(np.uint16)   # with ties
+    else:
+        t = np.array([0x3C00, 0x4000, 0x4200], dtype=np.uint16)[rng.integers(0, 3, out_dim)]
+    logits = widen(t)
+    for k in (1, 32, 64):
+        idx, val = _topk_of_exact_logits(anelm, dev, t, 64, k)
+        oi, ov = orc.topk(logits, k)
+        assert np.array_equal(idx, oi), (layout, k)
+        assert np.array_equal(val, ov), (layout, k)
 
 
 def test_topk_ties_prefer_lower_index(anelm, orc, dev):
