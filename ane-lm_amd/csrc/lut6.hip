@@ -635,28 +635,24 @@ __global__ __launch_bounds__(256) void topk_stage1(const float* logits, int n, i
     }
 }
 
-// Stage 2: one wave per batch row merges the rows' chunk candidates; the
-// lists are loaded eight at a time, the next eight while the current merge.
+// Stage 2: one workgroup per batch row merges the row's chunk candidates:
+// wave w takes lists w*8 .. w*8+7, then w+32 .., loading eight at once, and
+// wave 0 merges the four lists.  Entries are distinct under (value desc,
+// index asc), so the merge order does not change the result.
 constexpr int kTopkGroup = 8;
-__global__ __launch_bounds__(64) void topk_stage2(const float* cv, const int* ci, int n_chunks, int k,
-                                                  int32_t* out_idx, float* out_val) {
-    const int b = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void topk_stage2(const float* cv, const int* ci, int n_chunks, int k,
+                                                   int32_t* out_idx, float* out_val) {
+    __shared__ Cand lists[4][64];
+    const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int le = min(lane, k - 1);
-    Cand nx[kTopkGroup];
-    auto load_group = [&](int c0) {
+    Cand L{-INFINITY, 0x7fffffff};
+    for (int c0 = w * kTopkGroup; c0 < n_chunks; c0 += 4 * kTopkGroup) {
+        Cand cur[kTopkGroup];
 #pragma unroll
         for (int g = 0; g < kTopkGroup; g++) {
             const size_t o = ((size_t)b * n_chunks + min(c0 + g, n_chunks - 1)) * k + le;
-            nx[g] = Cand{cv[o], ci[o]};
+            cur[g] = Cand{cv[o], ci[o]};
         }
-    };
-    load_group(0);
-    Cand L{-INFINITY, 0x7fffffff};
-    for (int c0 = 0; c0 < n_chunks; c0 += kTopkGroup) {
-        Cand cur[kTopkGroup];
-#pragma unroll
-        for (int g = 0; g < kTopkGroup; g++) cur[g] = nx[g];
-        load_group(c0 + kTopkGroup);
 #pragma unroll
         for (int g = 0; g < kTopkGroup; g++) {
             // lists past n_chunks and lanes past k are empty entries; the lists
@@ -665,6 +661,11 @@ __global__ __launch_bounds__(64) void topk_stage2(const float* cv, const int* ci
             L = wave_merge(L, ok ? cur[g] : Cand{-INFINITY, 0x7fffffff}, lane);
         }
     }
+    lists[w][lane] = L;
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int o = 1; o < 4; o++) L = wave_merge(L, lists[o][lane], lane);
     if (lane < k) {
         out_idx[(size_t)b * k + lane] = L.i;
         out_val[(size_t)b * k + lane] = L.v;
@@ -986,7 +987,7 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     hipLaunchKernelGGL(topk_stage1, dim3(n_chunks, batch), dim3(256), 0, st, logits, out_dim, k,
                        n_chunks, cv, ci);
     ANELM_LAUNCHED("topk_stage1");
-    hipLaunchKernelGGL(topk_stage2, dim3(batch), dim3(64), 0, st, cv, ci, n_chunks, k, out_idx, out_val);
+    hipLaunchKernelGGL(topk_stage2, dim3(batch), dim3(256), 0, st, cv, ci, n_chunks, k, out_idx, out_val);
     ANELM_LAUNCHED("topk_stage2");
     return ANELM_OK;
 }
