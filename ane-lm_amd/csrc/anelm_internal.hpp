@@ -83,6 +83,16 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
                      int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st);
 int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st);
 
+// anelm_full_attn_decode with the split partials in `part` (part_cap bytes)
+// instead of the library workspace when part != nullptr; and the partials
+// size a call over max_len keys needs (0 for one split).
+int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const float* v, uint16_t* k_cache,
+                          uint16_t* v_cache, const float* q_norm_w, const float* k_norm_w, int n_heads,
+                          int n_kv_heads, int head_dim, int rot_dim, int pos, float theta, float eps,
+                          int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                          int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
+size_t full_attn_part_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
+
 // `n` zeroed counters on the current device; nullptr if n exceeds the pool.
 uint32_t* counters(size_t n);
 

@@ -726,12 +726,23 @@ int launch_kv(DecodeParams& p, int D, int G, dim3 grid, hipStream_t st) {
     }
 }
 
-// Sets the split layout and workspace for one decode call, then launches.
-// A split is 256/G keys (ring mode: every lane of the workgroup then loads all
-// of its K and V rows at once) or kPagedChunks such chunks (paged mode).  `max_len` bounds every sequence's key count;
-// `n_seqs` sequences (1 in ring mode).
+// Bytes of split partials one decode call needs (0 when one split suffices).
+size_t part_bytes(int n_heads, int n_kv_heads, int D, int n_seqs, int max_len, bool paged) {
+    const int G = n_heads / n_kv_heads;
+    const int kps = (256 / G) * (paged ? kPagedChunks : 1);
+    const int max_splits = (max_len + kps - 1) / kps;
+    if (max_splits <= 1) return 0;
+    return (size_t)n_seqs * n_kv_heads * max_splits * G * (D + 2) * sizeof(float);
+}
+
+// Sets the split layout and partials buffer for one decode call, then
+// launches.  A split is 256/G keys (ring mode: every lane of the workgroup
+// then loads all of its K and V rows at once) or kPagedChunks such chunks
+// (paged mode).  `max_len` bounds every sequence's key count; `n_seqs`
+// sequences (1 in ring mode).  The partials go to `part` (part_cap bytes)
+// when it is given, else to the library workspace.
 int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, int max_len,
-               hipStream_t st) {
+               hipStream_t st, float* part = nullptr, size_t part_cap = 0) {
     const int Hkv = p.n_kv_heads;
     const int G = n_heads / Hkv;
     const int kps = (256 / G) * (p.paged ? kPagedChunks : 1);
@@ -739,9 +750,13 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
     p.kps = kps;
     p.max_splits = max_splits;
     p.n_seqs = n_seqs;
-    const size_t rec = (size_t)G * (D + 2);
-    if (max_splits > 1) {
-        const size_t need = (size_t)n_seqs * Hkv * max_splits * rec * sizeof(float);
+    const size_t need = part_bytes(n_heads, Hkv, D, n_seqs, max_len, p.paged != 0);
+    if (need > 0 && part != nullptr) {
+        if (need > part_cap)
+            return set_error(ANELM_ERANGE, "decode attention: %zu bytes of split partials, buffer holds %zu",
+                             need, part_cap);
+        p.part = part;
+    } else if (need > 0) {
         float* ws = static_cast<float*>(workspace(need, st));
         if (!ws) return ANELM_ENOMEM;
         p.part = ws;
@@ -751,6 +766,11 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
     dim3 grid(max_splits, Hkv, n_seqs);
     return kv_dtype == ANELM_F16 ? launch_kv<uint16_t>(p, D, G, grid, st)
                                  : launch_kv<float>(p, D, G, grid, st);
+}
+
+__global__ void zero_kernel(float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = 0.f;
 }
 
 int check_heads(int n_heads, int n_kv_heads, int head_dim) {
@@ -780,7 +800,11 @@ extern "C" int anelm_gqa_attention(float* out, const float* q, const void* k_cac
     ANELM_REQUIRE(kv_dtype == ANELM_F16 || kv_dtype == ANELM_F32, "kv_dtype %d unknown", kv_dtype);
     hipStream_t st = as_stream(stream);
     if (cache_len <= 0) {
-        ANELM_HIP(hipMemsetAsync(out, 0, (size_t)n_heads * head_dim * sizeof(float), st));
+        // zeros (cpu_ops.cpp:152-155) from a fill kernel: the call stays
+        // capturable into a HIP graph without a memset node
+        const int n = n_heads * head_dim;
+        hipLaunchKernelGGL(zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, out, n);
+        ANELM_LAUNCHED("zero_kernel");
         return ANELM_OK;
     }
     ANELM_NONNULL(q);
@@ -807,14 +831,14 @@ extern "C" int anelm_gqa_attention(float* out, const float* q, const void* k_cac
     return run_decode(p, kv_dtype, n_heads, head_dim, 1, cache_len, st);
 }
 
-extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const float* k,
-                                      const float* v, uint16_t* k_cache, uint16_t* v_cache,
-                                      const float* q_norm_w, const float* k_norm_w, int n_heads,
-                                      int n_kv_heads, int head_dim, int rot_dim, int pos,
-                                      float theta, float eps, int rope_mode, int gate,
-                                      const float* cos_row, const float* sin_row,
-                                      int* cache_start, int* cache_len, int cache_capacity,
-                                      void* stream) {
+namespace anelm {
+
+int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const float* v, uint16_t* k_cache,
+                          uint16_t* v_cache, const float* q_norm_w, const float* k_norm_w, int n_heads,
+                          int n_kv_heads, int head_dim, int rot_dim, int pos, float theta, float eps,
+                          int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                          int* cache_len, int cache_capacity, hipStream_t stream, float* part,
+                          size_t part_cap) {
     ANELM_NONNULL(out);
     ANELM_NONNULL(q_gate);
     ANELM_NONNULL(k);
@@ -875,12 +899,31 @@ extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const flo
     } else {
         rope_row(p.cs, p.sn, rot_dim, pos, theta);
     }
-    rc = run_decode(p, ANELM_F16, n_heads, head_dim, 1, len, as_stream(stream));
+    rc = run_decode(p, ANELM_F16, n_heads, head_dim, 1, len, stream, part, part_cap);
     if (rc == ANELM_OK) {
         *cache_start = start;
         *cache_len = len;
     }
     return rc;
+}
+
+size_t full_attn_part_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len) {
+    return part_bytes(n_heads, n_kv_heads, head_dim, 1, max_len, false);
+}
+
+}  // namespace anelm
+
+extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const float* k,
+                                      const float* v, uint16_t* k_cache, uint16_t* v_cache,
+                                      const float* q_norm_w, const float* k_norm_w, int n_heads,
+                                      int n_kv_heads, int head_dim, int rot_dim, int pos,
+                                      float theta, float eps, int rope_mode, int gate,
+                                      const float* cos_row, const float* sin_row,
+                                      int* cache_start, int* cache_len, int cache_capacity,
+                                      void* stream) {
+    return full_attn_decode_impl(out, q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, n_heads, n_kv_heads,
+                                 head_dim, rot_dim, pos, theta, eps, rope_mode, gate, cos_row, sin_row,
+                                 cache_start, cache_len, cache_capacity, as_stream(stream), nullptr, 0);
 }
 
 extern "C" int anelm_attn_decode_paged(float* out, const float* q, int q_head_stride,

@@ -589,7 +589,9 @@ __global__ __launch_bounds__(256) void topk_stage1(const float* logits, int n, i
 #pragma unroll
     for (int t = 0; t < kTopkPerLane; t++) {
         const int it = idx_of(t);
-        const float vt = it != 0x7fffffff ? v[t] : -INFINITY;
+        // a NaN logit ranks as -inf (keeping its index for ties), so the
+        // ordering stays total and NaN never wins the greedy pick
+        const float vt = (it != 0x7fffffff && !__builtin_isnan(v[t])) ? v[t] : -INFINITY;
         v[t] = vt;
         if (before(vt, it, m.v, m.i)) m = Cand{vt, it};
     }
@@ -970,7 +972,7 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
     ANELM_NONNULL(x);
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
-    ANELM_REQUIRE(batch > 0, "lut6_topk: batch %d", batch);
+    ANELM_REQUIRE(batch > 0 && batch <= 65535, "lut6_topk: batch %d (1..65535)", batch);
     ANELM_REQUIRE(k > 0 && k <= 64 && k <= out_dim, "lut6_topk: k %d must be in [1, min(64, out_dim)]", k);
     hipStream_t st = as_stream(stream);
     const int n_chunks = (out_dim + kTopkChunk - 1) / kTopkChunk;

@@ -16,6 +16,11 @@ struct anelm_hybrid_step {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     anelm::PersistentStep* ps = nullptr;
+    // split partials of the attention layers (graph mode): owned by the step,
+    // so the captured launches never point into the shared workspace, which a
+    // later call may free when it grows
+    float* part = nullptr;
+    size_t part_bytes = 0;
 };
 
 namespace anelm {
@@ -29,10 +34,10 @@ int launch_all(anelm_hybrid_step* s, hipStream_t st, bool advance) {
         int rc;
         if (L.kind == ANELM_LAYER_ATTENTION) {
             int start = L.cache_start, len = L.cache_len;
-            rc = anelm_full_attn_decode(L.core_out, L.q_gate, L.k, L.v, L.k_cache, L.v_cache,
-                                        L.q_norm_w, L.k_norm_w, d.n_heads, d.n_kv_heads,
-                                        d.head_dim, d.rot_dim, L.pos, d.theta, d.eps, d.rope_mode,
-                                        1, nullptr, nullptr, &start, &len, L.cache_capacity, st);
+            rc = full_attn_decode_impl(L.core_out, L.q_gate, L.k, L.v, L.k_cache, L.v_cache, L.q_norm_w,
+                                       L.k_norm_w, d.n_heads, d.n_kv_heads, d.head_dim, d.rot_dim, L.pos,
+                                       d.theta, d.eps, d.rope_mode, 1, nullptr, nullptr, &start, &len,
+                                       L.cache_capacity, st, s->part, s->part_bytes);
             if (rc) return rc;
             if (advance) {
                 L.cache_start = start;
@@ -92,11 +97,19 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
         return ANELM_OK;
     }
     if (s->use_graph) {
-        // Warm-up: grows the workspace outside the capture.
-        int rc = launch_all(s, st, false);
-        if (rc == ANELM_OK) {
-            hipError_t e = hipStreamSynchronize(st);
-            if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+        // The captured launches allocate nothing: the attention layers' split
+        // partials go to a buffer of the step, sized for full rings; the FFN
+        // blocks use h_scratch.  No step runs before the capture.
+        int rc = device() ? ANELM_OK : ANELM_EHIP;
+        for (int i = 0; i < n_layers && rc == ANELM_OK; i++)
+            if (layers[i].kind == ANELM_LAYER_ATTENTION) {
+                const size_t need = full_attn_part_bytes(dims->n_heads, dims->n_kv_heads, dims->head_dim,
+                                                         layers[i].cache_capacity);
+                if (need > s->part_bytes) s->part_bytes = need;
+            }
+        if (rc == ANELM_OK && s->part_bytes > 0) {
+            hipError_t e = hipMalloc(&s->part, s->part_bytes);
+            if (e != hipSuccess) rc = hip_fail(e, "hipMalloc(step partials)");
         }
         if (rc == ANELM_OK) {
             hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
@@ -145,6 +158,7 @@ extern "C" int anelm_hybrid_step_destroy(anelm_hybrid_step* step) {
     if (step->ps) persistent_destroy(step->ps);
     if (step->exec) (void)hipGraphExecDestroy(step->exec);
     if (step->graph) (void)hipGraphDestroy(step->graph);
+    if (step->part) (void)hipFree(step->part);
     delete step;
     return ANELM_OK;
 }

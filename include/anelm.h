@@ -304,8 +304,11 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          attention ring and position by one token, as the
  *                          model's decode loop does;
  *   ANELM_STEP_GRAPH       the eager launches captured once into a HIP graph on
- *                          `stream` (not the null stream) after one warm-up
- *                          run; each run replays the same work (rings do not
+ *                          `stream` (not the null stream) at create (no step
+ *                          runs then; the step owns the attention layers'
+ *                          split-partial buffers, so later calls that grow the
+ *                          library workspace cannot invalidate the graph);
+ *                          each run replays the same work (rings do not
  *                          advance);
  *   ANELM_STEP_PERSISTENT  the whole step as ONE kernel launch (one workgroup
  *                          per compute unit, grid barriers between the

@@ -497,11 +497,14 @@ void orc_lut6_ffn(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
 
 /* torch.topk over logits (scripts/export_hybrid_chunks.py:409-421) with the
  * order (value descending, index ascending); ties therefore keep the first
- * maximal index first, as the greedy rule at core/sampling.cpp:47-53 does. */
+ * maximal index first, as the greedy rule at core/sampling.cpp:47-53 does.
+ * A NaN logit ranks as -inf (the strict > of sampling.cpp:49-51 never picks a
+ * NaN past index 0). */
 void orc_topk(int32_t* idx, float* val, const float* logits, long n, int k) {
     int cnt = 0;
     for (long i = 0; i < n; i++) {
         float v = logits[i];
+        if (v != v) v = -INFINITY;
         if (cnt == k && !(v > val[k - 1])) continue;
         int p = (cnt < k) ? cnt : k - 1;
         if (cnt < k) cnt++;

@@ -109,6 +109,29 @@ def test_deltanet_prefill_chunked_matches_scan_4096(anelm, dev, flags):
     assert_close(to_host(d["state"]), to_host(d2["state"]), rel=1e-4, max_abs=1e-3, what="state")
 
 
+@pytest.mark.parametrize("flags", [1, 3])
+def test_deltanet_prefill_4096_matches_oracle_on_head_subsets(anelm, orc, dev, flags):
+    """The prefill workload at full size (4096 tokens, 16 key / 32 value
+    heads, chunked form) against the oracle's sequential recurrence on
+    subsets of heads: value heads are independent given their key head
+    (qwen3_5.cpp:890 maps value head h to key head h / 2 here), so the oracle
+    runs value heads (2kh, 2kh + 1) with key head kh alone -- the same
+    per-head arithmetic as the full run -- for kh = 0, 7 and 15, in both
+    orders (cpu_ops and decay-first)."""
+    c = deltanet_case(590 + flags, Hk=16, Hv=32, S=4096)
+    d = _dev_case(c, dev)
+    print(f"deltanet prefill 4096 x 16k/32v flags {flags}", flush=True)
+    y = to_host(anelm.ops.deltanet_prefill(d["state"], d["q"], d["k"], d["v"], d["a"], d["b"], d["A"],
+                                           d["dt_bias"], flags))
+    st = to_host(d["state"])
+    for kh in (0, 7, 15):
+        vs = [2 * kh, 2 * kh + 1]
+        yw, Sw = orc.deltanet_prefill(c.state[vs], c.q[:, kh:kh + 1], c.k[:, kh:kh + 1], c.v[:, vs],
+                                      c.a[:, vs], c.b[:, vs], c.A[vs], c.dt_bias[vs], flags)
+        assert_close(y[:, vs], yw, what=f"y of value heads {vs}")
+        assert_close(st[vs], Sw, what=f"state of value heads {vs}")
+
+
 def test_deltanet_prefill_rejects_other_chunks(anelm, dev):
     c = deltanet_case(580, Hk=2, Hv=4, S=8)
     d = _dev_case(c, dev)

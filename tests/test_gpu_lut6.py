@@ -133,16 +133,48 @@ def _check_topk(orc, idx, val, logits, k):
 @pytest.mark.parametrize("out_dim,in_dim,batch,k", [(262144, 2560, 2, 32), (4096, 1024, 3, 64),
                                                     (8192, 2560, 1, 1), (262144, 2560, 32, 32)])
 def test_topk(anelm, orc, dev, out_dim, in_dim, batch, k):
+    """Two checks per row.  Selection, bit-exact: the returned (index, value)
+    list equals the oracle's (value desc, index asc) top-k of the very logits
+    the kernel ranked -- lut6_topk computes them with the same batched GEMM
+    launch that anelm_lut6_gemm makes, which is deterministic, so the GEMM's
+    output is that logit vector bit for bit.  Projection: those logits match
+    the oracle's within the fp32 summation-order bar."""
     packed, lut, _ = lut6_matrix(620 + k, out_dim, in_dim)
     x = np.random.default_rng(621).standard_normal((batch, in_dim)).astype(np.float32)
-    idx, val = anelm.ops.lut6_topk(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim,
-                                   in_dim, k)
+    dp, dl, dx = to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev)
+    idx, val = anelm.ops.lut6_topk(dp, dl, dx, out_dim, in_dim, k)
     idx, val = to_host(idx), to_host(val)
-    for b in (range(batch) if batch <= 3 else (0, batch // 2, batch - 1)):
+    gpu_logits = to_host(anelm.ops.lut6_gemm(dp, dl, dx, out_dim, in_dim))
+    rows = range(batch) if batch <= 3 else (0, 1, batch // 2, batch - 2, batch - 1)
+    for b in rows:
+        oi, ov = orc.topk(gpu_logits[b], k)
+        assert np.array_equal(idx[b], oi), f"row {b}: selection differs from the oracle's on the same logits"
+        assert np.array_equal(val[b], ov), f"row {b}: selected values differ"
         logits = orc.lut6_matvec(packed, lut, x[b], out_dim, in_dim)
+        assert_close(gpu_logits[b], logits, rel=1e-5, max_abs=1e-4, what=f"row {b} logits")
         _check_topk(orc, idx[b], val[b], logits, k)
         if k == 1:
-            assert idx[b, 0] == orc.argmax(logits)
+            assert idx[b, 0] == orc.argmax(gpu_logits[b])
+
+
+def test_topk_nan_logits_rank_last(anelm, orc, dev):
+    """NaN logits rank as -inf (index order among them): planted NaNs never
+    enter the top-k ahead of a finite logit, and the list equals the oracle's
+    on the same exact logits.  Rows r % 32 == 0 stay finite (their LUT entry
+    also weighs the zero inputs, where a NaN would spread to the group)."""
+    rng = np.random.default_rng(704)
+    out_dim = 20000
+    t = rng.integers(0x1000, 0x4000, out_dim).astype(np.uint16)
+    nan_rows = rng.choice(np.nonzero(np.arange(out_dim) % 32 != 0)[0], 300, replace=False)
+    t[nan_rows] = 0x7E00                                     # fp16 quiet NaN
+    t[nan_rows[:5]] = 0xFE00                                 # negative-sign NaN
+    logits = widen(t)
+    for k in (1, 32, 64):
+        idx, val = _topk_of_exact_logits(anelm, dev, t, 64, k)
+        oi, ov = orc.topk(logits, k)
+        assert np.array_equal(idx, oi), k
+        assert np.array_equal(val, ov), k
+        assert not np.isin(idx, nan_rows).any()
 
 
 def _topk_of_exact_logits(anelm, dev, target, in_dim, k):

@@ -451,3 +451,26 @@ def test_topk_and_argmax(orc):
     assert list(idx[:5]) == [17, 4000, 9999, 3, 5]
     assert orc.argmax(logits) == 17
     assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
+
+
+def test_topk_nan_ranks_as_minus_inf(orc):
+    """NaN logits rank as -inf with the index tie rule, so they never precede
+    a finite logit; the greedy pick then equals the reference's strict-> scan
+    (core/sampling.cpp:47-53), which never moves to a NaN past index 0."""
+    rng = np.random.default_rng(26)
+    logits = rng.standard_normal(5000).astype(np.float32)
+    nan_at = rng.choice(np.arange(1, 5000), 400, replace=False)
+    logits[nan_at] = np.nan
+    logits[nan_at[0]] = 50.0       # a finite maximum among the NaNs
+    as_inf = np.where(np.isnan(logits), -np.inf, logits)
+    for k in (1, 7, 64):
+        idx, val = orc.topk(logits, k)
+        order = np.lexsort((np.arange(logits.size), -as_inf.astype(np.float64)))[:k]
+        assert np.array_equal(idx, order)
+        assert np.array_equal(val, as_inf[order])
+        assert not np.isin(idx, nan_at[1:]).any()
+    assert orc.topk(logits, 1)[0][0] == orc.argmax(logits) == nan_at[0]
+    # few finite values: the NaNs fill the tail as -inf, lowest index first
+    small = np.array([np.nan, 2.0, np.nan, 1.0, np.nan], np.float32)
+    idx, val = orc.topk(small, 5)
+    assert list(idx) == [1, 3, 0, 2, 4] and np.all(np.isneginf(val[2:]))

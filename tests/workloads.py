@@ -196,9 +196,10 @@ class HybridModel:
     x: np.ndarray         # [hidden] fp32
 
 
-def hybrid_model(seed, n_layers, dims=QWEN35_4B, rings=None, cap=8192, lut_std=0.02):
+def hybrid_model(seed, n_layers, dims=QWEN35_4B, rings=None, cap=8192, lut_std=0.02, dn_flags=1 | 4):
     """rings: per attention layer (start, len); default (0, 700).  Cached keys
-    and values are fp16 ~ N(0,1); weights as the benchmark describes."""
+    and values are fp16 ~ N(0,1); weights as the benchmark describes;
+    dn_flags for every DeltaNet layer (ANELM_DN_* bits)."""
     rng = np.random.default_rng(seed)
     d = dims
     H, I, D = d["hidden"], d["inter"], d["head_dim"]
@@ -231,7 +232,7 @@ def hybrid_model(seed, n_layers, dims=QWEN35_4B, rings=None, cap=8192, lut_std=0
             L["kind"] = 0
             L.update(state=dn.state, dn_q=dn.q, dn_k=dn.k, dn_v=dn.v, dn_a=dn.a, dn_b=dn.b,
                      dn_A=dn.A, dn_dt_bias=dn.dt_bias, dn_z=dn.z, dn_norm_w=dn.norm_w)
-            L["dn_flags"] = 1 | 4
+            L["dn_flags"] = dn_flags
         L["ffn_norm_w"] = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
         L["gate_w"], L["gate_lut"] = lw(I, H), lut(I)
         L["up_w"], L["up_lut"] = lw(I, H), lut(I)
