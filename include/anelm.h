@@ -124,6 +124,25 @@ int anelm_full_attn_decode(float* out, const float* q_gate, const float* k, cons
                            const float* cos_row, const float* sin_row,
                            int* cache_start, int* cache_len, int cache_capacity, void* stream);
 
+/* anelm_full_attn_decode without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments and results as anelm_full_attn_decode; the split partials live in
+ * a static per-device array of 8 MiB (held by every device the library runs
+ * on until the process ends), which bounds n_kv_heads * ceil(len / (256 / G))
+ * * G * (head_dim + 2) * 4 bytes (len = keys attended after the append,
+ * G = n_heads / n_kv_heads): 16 q / 4 kv heads at head_dim 256 attend up to
+ * 32512 keys.  Larger calls return ANELM_ERANGE.  Calls that overlap on one
+ * device share that array and race; the library's first call on a device
+ * that allocates (e.g. anelm_device_cus) is not needed before this one. */
+int anelm_full_attn_decode_noalloc(float* out, const float* q_gate, const float* k, const float* v,
+                                   uint16_t* k_cache, uint16_t* v_cache,
+                                   const float* q_norm_w, const float* k_norm_w,
+                                   int n_heads, int n_kv_heads, int head_dim, int rot_dim,
+                                   int pos, float theta, float eps, int rope_mode, int gate,
+                                   const float* cos_row, const float* sin_row,
+                                   int* cache_start, int* cache_len, int cache_capacity, void* stream);
+
 /* Batched decode over paged fp16 caches (no reference kernel: per sequence it
  * is gqa_attention, cpu_ops.cpp:148-204, over that sequence's keys).
  * n_pages pages hold page_size tokens each as [page][n_kv_heads][page_size][head_dim].
