@@ -53,6 +53,9 @@ SIGNATURES = {
     "anelm_full_attn_decode_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F,
                                        _I, _I, _FP, _FP, _IP, _IP, _I, _P],
     "anelm_attn_decode_paged": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
+    "anelm_attn_decode_paged_step": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                     _I, _I, _I, _I, _I, _F, _F, _I, _I, _P],
+    "anelm_rope_table": [_P, _I, _I, _F],
     "anelm_attn_prefill": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P],
     "anelm_ssm_step": [_P, _P, _P, _P, _P, _F, _F, _I, _I, _I, _P],
     "anelm_deltanet_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],

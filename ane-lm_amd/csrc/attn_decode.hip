@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <math.h>
+#include <vector>
 
 namespace anelm {
 
@@ -51,6 +52,14 @@ struct DecodeParams {
     int rot_pairs, rope_mode, gate;
     float cs[kMaxRotPairs];
     float sn[kMaxRotPairs];
+    // fused paged step: the new token of sequence s is key seq_lens[s] at
+    // position positions[s] (NULL: seq_lens[s]); RoPE rows from rope_tab
+    // [rope_rows][2 * rot_pairs] (cos then sin) or, past the table, from the
+    // same formula evaluated on the device
+    const int32_t* positions;
+    const float* rope_tab;
+    int rope_rows;
+    float theta;
 };
 
 // Per-workgroup view of its sequence.
@@ -112,7 +121,8 @@ __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
 // in shared memory, in place.  All threads participate.
 // A NULL weight skips the norm (callers whose q/k arrive normalised).
 template <int D>
-__device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p, float* red) {
+__device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p, float* red, const float* cs,
+                              const float* sn) {
     if (w != nullptr) {
         float ss = 0.f;
         for (int d = threadIdx.x; d < D; d += kNT) ss += row[d] * row[d];
@@ -124,10 +134,6 @@ __device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p,
     for (int j = threadIdx.x; j < p.rot_pairs; j += kNT) {
         const int i0 = p.rope_mode == 0 ? 2 * j : j;
         const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
-        // read through a pointer into the argument segment: indexing the
-        // by-value array directly expands into a select over every entry
-        const float* cs = p.cs;
-        const float* sn = p.sn;
         const float c = cs[j], s = sn[j];
         const float v0 = row[i0], v1 = row[i1];
         rotate_pair(row[i0], row[i1], v0, v1, c, s);
@@ -139,7 +145,8 @@ __device__ void norm_rope_row(float* row, const float* w, const DecodeParams& p,
 // the rows' sums of squares (partial sums in the same order as block_sum, so
 // every row is normalised bit-identically to norm_rope_row).
 template <int D, int G>
-__device__ void norm_rope_rows(float (*rows)[D], const float* w, const DecodeParams& p, float (*red_g)[G]) {
+__device__ void norm_rope_rows(float (*rows)[D], const float* w, const DecodeParams& p, float (*red_g)[G],
+                               const float* cs, const float* sn) {
     if (w != nullptr) {
         float ss[G];
 #pragma unroll
@@ -164,8 +171,6 @@ __device__ void norm_rope_rows(float (*rows)[D], const float* w, const DecodePar
         }
     }
     __syncthreads();
-    const float* cs = p.cs;
-    const float* sn = p.sn;
     for (int e = threadIdx.x; e < G * p.rot_pairs; e += kNT) {
         const int g = e / p.rot_pairs, j = e - g * p.rot_pairs;
         const int i0 = p.rope_mode == 0 ? 2 * j : j;
@@ -259,11 +264,13 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
     __syncthreads();
     if (p.fused) {
-        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g);
+        // cos / sin read through pointers into the argument segment: indexing
+        // the by-value arrays directly expands into a select over every entry
+        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, p.cs, p.sn);
         if (owner) {
             for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
             __syncthreads();
-            norm_rope_row<D>(kn_s, p.k_norm_w, p, red);
+            norm_rope_row<D>(kn_s, p.k_norm_w, p, red, p.cs, p.sn);
             KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
             KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
             for (int d = tid; d < D; d += kNT) {
@@ -444,13 +451,20 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
     __shared__ float red_g[kNW][G];
     __shared__ float red_o[kNW][G][D];
     __shared__ int pg[KPS + 1];   // page-table entries of the split (any page size)
+    // fused step only: q rows and the new key after norm + RoPE, RoPE row
+    __shared__ float q_s[G][D];
+    __shared__ float kn_s[D];
+    __shared__ float red[kNW];
+    __shared__ float rope_s[2][kMaxRotPairs];
 
     const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const int Hkv = p.n_kv_heads;
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int sub = lane / LPK, dl = lane % LPK;
-    const int len = min(p.seq_lens[seq], p.len);
+    // fused: the sequence's new token is key `cached` and is attended too
+    const int cached = p.seq_lens[seq];
+    const int len = p.fused ? min(cached + 1, p.len) : min(cached, p.len);
     float* out = p.out + (size_t)seq * Hkv * G * D;
     if (len <= 0) {   // empty sequence: zeros, as cpu_ops.cpp:152-155
         if (split == 0)
@@ -468,11 +482,52 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
     const int32_t* ptab = p.page_table + (size_t)seq * p.max_pages;
     for (int i = tid; i < pcount; i += kNT) pg[i] = min(max(ptab[pfirst + i], 0), p.n_pages - 1);
     float qr[G][8];
+    // fused: local index of the new key in this split (-1: another split's)
+    const int t_new = p.fused && cached >= k0 && cached < k0 + nk_all ? cached - k0 : -1;
+    if (p.fused) {
+        // models/llm/qwen3_5.cpp:952-986 for this sequence: q/k RMSNorm, RoPE
+        // at the token's position (the table row, or the same formula as
+        // cpu_ops.cpp:51-55 past the table), fp16 append into the page
+        const int pos = p.positions ? p.positions[seq] : cached;
+        for (int j = tid; j < p.rot_pairs; j += kNT) {
+            if (p.rope_tab != nullptr && pos >= 0 && pos < p.rope_rows) {
+                rope_s[0][j] = p.rope_tab[(size_t)pos * 2 * p.rot_pairs + j];
+                rope_s[1][j] = p.rope_tab[(size_t)pos * 2 * p.rot_pairs + p.rot_pairs + j];
+            } else {
+                const float freq = 1.0f / powf(p.theta, (float)(2 * j) / (float)(2 * p.rot_pairs));
+                const float angle = (float)pos * freq;
+                rope_s[0][j] = cosf(angle);
+                rope_s[1][j] = sinf(angle);
+            }
+        }
+        for (int e = tid; e < G * D; e += kNT) q_s[e / D][e % D] = q[(size_t)(kvh * G + e / D) * p.q_stride + e % D];
+        __syncthreads();
+        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, rope_s[0], rope_s[1]);
+        if (t_new >= 0) {
+            const size_t nrow = ((size_t)seq * Hkv + kvh) * D;
+            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[nrow + d];
+            __syncthreads();
+            norm_rope_row<D>(kn_s, p.k_norm_w, p, red, rope_s[0], rope_s[1]);
+            const int page = pg[cached / ps - pfirst], row = cached % ps;
+            const size_t off = (((size_t)page * Hkv + kvh) * ps + row) * D;
+            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + off;
+            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + off;
+            for (int d = tid; d < D; d += kNT) {
+                store_kv(kw + d, kn_s[d]);
+                store_kv(vw + d, p.v_new[nrow + d]);
+            }
+        }
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float* src = q + (size_t)(kvh * G + g) * p.q_stride + dl * 8;
+        for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) qr[g][i] = src[i];
+            for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float* src = q + (size_t)(kvh * G + g) * p.q_stride + dl * 8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) qr[g][i] = src[i];
+        }
     }
     lds_barrier();
 
@@ -575,6 +630,17 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
         Raw8<KV> rk[KB], rv[KB];
         load_rows(c, kc, rk);
         load_rows(c, vc, rv);
+        if (t_new >= 0 && c == t_new / CK) {
+            // the new key's row was loaded before (or while) it was stored:
+            // take it from the prologue, rounded as stored
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                if (c * CK + b * KPB + w * KPI + sub == t_new) {
+                    rk[b] = make_raw<KV>(kn_s + dl * 8);
+                    rv[b] = make_raw<KV>(p.v_new + ((size_t)seq * Hkv + kvh) * D + dl * 8);
+                }
+            }
+        }
         chunk(c, rk, rv);
     }
 
@@ -648,7 +714,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p)
     const int h = blockIdx.y, seq = blockIdx.z;
     const int Hkv = p.n_kv_heads;
     const int kvh = h / G, g = h % G;
-    const int len = p.paged ? min(p.seq_lens[seq], p.len) : p.len;
+    const int len = p.paged ? min(p.seq_lens[seq] + (p.fused ? 1 : 0), p.len) : p.len;
     const int n = (len + p.kps - 1) / p.kps;
     if (n <= 1) return;   // written directly by the split kernel (or zeros)
     const size_t rs = (size_t)G * REC;   // record stride between splits
@@ -962,4 +1028,78 @@ extern "C" int anelm_attn_decode_paged(float* out, const float* q, int q_head_st
     p.n_pages = n_pages;
     p.len = max_seq_len;
     return run_decode(p, ANELM_F16, n_heads, head_dim, n_seqs, max_seq_len, as_stream(stream));
+}
+
+extern "C" int anelm_attn_decode_paged_step(float* out, const float* q_gate, const float* k, const float* v,
+                                            uint16_t* k_pages, uint16_t* v_pages, const int32_t* page_table,
+                                            const int32_t* seq_lens, const int32_t* positions,
+                                            const float* q_norm_w, const float* k_norm_w,
+                                            const float* rope_table, int rope_rows, int n_seqs, int max_pages,
+                                            int page_size, int n_pages, int max_seq_len, int n_heads,
+                                            int n_kv_heads, int head_dim, int rot_dim, float theta, float eps,
+                                            int rope_mode, int gate, void* stream) {
+    ANELM_NONNULL(out);
+    ANELM_NONNULL(q_gate);
+    ANELM_NONNULL(k);
+    ANELM_NONNULL(v);
+    ANELM_NONNULL(k_pages);
+    ANELM_NONNULL(v_pages);
+    ANELM_NONNULL(page_table);
+    ANELM_NONNULL(seq_lens);
+    ANELM_REQUIRE((q_norm_w == nullptr) == (k_norm_w == nullptr),
+                  "q_norm_w and k_norm_w must both be given or both be NULL");
+    int rc = check_heads(n_heads, n_kv_heads, head_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(n_seqs > 0 && n_seqs <= 65535, "paged step: n_seqs %d", n_seqs);
+    ANELM_REQUIRE(page_size > 0 && max_pages > 0 && n_pages > 0,
+                  "paged step: page_size %d max_pages %d n_pages %d", page_size, max_pages, n_pages);
+    ANELM_REQUIRE(max_seq_len > 0 && max_seq_len <= max_pages * page_size,
+                  "paged step: max_seq_len %d beyond max_pages*page_size", max_seq_len);
+    ANELM_REQUIRE(rot_dim >= 0 && rot_dim % 2 == 0 && rot_dim <= head_dim && rot_dim / 2 <= kMaxRotPairs,
+                  "paged step: rot_dim %d must be even and <= head_dim", rot_dim);
+    ANELM_REQUIRE(rope_mode == ANELM_ROPE_INTERLEAVED || rope_mode == ANELM_ROPE_HALF_SPLIT,
+                  "paged step: rope_mode %d unknown", rope_mode);
+    ANELM_REQUIRE(rope_table == nullptr || rope_rows > 0, "paged step: rope_rows %d", rope_rows);
+    DecodeParams p{};
+    p.out = out;
+    p.q = q_gate;
+    p.q_stride = 2 * head_dim;
+    p.k_cache = k_pages;
+    p.v_cache = v_pages;
+    p.n_kv_heads = n_kv_heads;
+    p.scale = 1.0f / sqrtf((float)head_dim);
+    p.paged = 1;
+    p.page_table = page_table;
+    p.seq_lens = seq_lens;
+    p.max_pages = max_pages;
+    p.page_size = page_size;
+    p.n_pages = n_pages;
+    p.len = max_seq_len;
+    p.fused = 1;
+    p.q_norm_w = q_norm_w;
+    p.k_norm_w = k_norm_w;
+    p.k_new = k;
+    p.v_new = v;
+    p.k_cache_w = k_pages;
+    p.v_cache_w = v_pages;
+    p.eps = eps;
+    p.rot_pairs = rot_dim / 2;
+    p.rope_mode = rope_mode;
+    p.gate = gate ? 1 : 0;
+    p.positions = positions;
+    p.rope_tab = rope_table;
+    p.rope_rows = rope_table ? rope_rows : 0;
+    p.theta = theta;
+    return run_decode(p, ANELM_F16, n_heads, head_dim, n_seqs, max_seq_len, as_stream(stream));
+}
+
+extern "C" int anelm_rope_table(float* table, int rot_dim, int n_pos, float theta) {
+    ANELM_NONNULL(table);
+    ANELM_REQUIRE(rot_dim > 0 && rot_dim % 2 == 0 && rot_dim / 2 <= kMaxRotPairs, "rope_table: rot_dim %d", rot_dim);
+    ANELM_REQUIRE(n_pos > 0, "rope_table: n_pos %d", n_pos);
+    std::vector<float> host((size_t)n_pos * rot_dim);
+    for (int pos = 0; pos < n_pos; pos++)
+        rope_row(&host[(size_t)pos * rot_dim], &host[(size_t)pos * rot_dim + rot_dim / 2], rot_dim, pos, theta);
+    ANELM_HIP(hipMemcpy(table, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
+    return ANELM_OK;
 }

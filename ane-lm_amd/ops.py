@@ -157,6 +157,31 @@ def attn_decode_paged(q, k_pages, v_pages, page_table, seq_lens, max_seq_len, n_
     return out
 
 
+def rope_table(rot_dim, n_pos, theta, device):
+    """RoPE rows 0..n_pos-1 on the device: [n_pos][rot_dim] = cos pairs, sin pairs."""
+    t = torch.empty(n_pos, rot_dim, device=device, dtype=_F32)
+    call("anelm_rope_table", _p(t), rot_dim, n_pos, theta)
+    return t
+
+
+def attn_decode_paged_step(q_gate, k, v, k_pages, v_pages, page_table, seq_lens, q_norm_w, k_norm_w,
+                           max_seq_len, n_heads, n_kv_heads, head_dim, page_size, rot_dim, theta=1e7,
+                           eps=1e-6, rope_mode=ROPE_INTERLEAVED, gate=True, positions=None, rope_tab=None,
+                           out=None):
+    """qwen3_5.cpp:944-1002 per sequence over paged fp16 caches: norms, RoPE,
+    page append of the new key (key seq_lens[s]), attention over
+    seq_lens[s] + 1 keys, gate.  seq_lens is not advanced."""
+    n_seqs = seq_lens.numel()
+    out = (torch.empty(n_seqs, n_heads, head_dim, device=q_gate.device, dtype=_F32)
+           if out is None else out)
+    call("anelm_attn_decode_paged_step", _p(out), _p(q_gate), _p(k), _p(v), _p(k_pages), _p(v_pages),
+         _p(page_table), _p(seq_lens), _p(positions), _p(q_norm_w), _p(k_norm_w), _p(rope_tab),
+         0 if rope_tab is None else rope_tab.shape[0], n_seqs, page_table.shape[-1], page_size,
+         k_pages.shape[0], max_seq_len, n_heads, n_kv_heads, head_dim, rot_dim, theta, eps, rope_mode,
+         1 if gate else 0, _s())
+    return out
+
+
 def attn_prefill(q, k, v, out_dtype=_F32):
     """Causal GQA prefill; q [S][Hq][D], k/v [S][Hkv][D] fp16."""
     S, Hq, D = q.shape

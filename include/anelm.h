@@ -157,6 +157,41 @@ int anelm_attn_decode_paged(float* out, const float* q, int q_head_stride,
                             int n_seqs, int max_pages, int page_size, int n_pages, int max_seq_len,
                             int n_heads, int n_kv_heads, int head_dim, void* stream);
 
+/* One full-attention decode step for a batch of sequences over paged fp16
+ * caches (no reference kernel as one call): per sequence s the composition
+ * of anelm_full_attn_decode, models/llm/qwen3_5.cpp:944-1002 --
+ *   RMSNorm of its q rows (q_gate [n_seqs][n_heads][2*head_dim]) and k
+ *   (k, v [n_seqs][n_kv_heads][head_dim]) with q_norm_w / k_norm_w (both
+ *   NULL: no norm); RoPE at position positions[s] (device int32; NULL:
+ *   seq_lens[s]); fp16 append of k, v as key seq_lens[s] (page
+ *   page_table[s*max_pages + seq_lens[s]/page_size], row
+ *   seq_lens[s] % page_size); gqa_attention (cpu_ops.cpp:148-204) over keys
+ *   0..seq_lens[s]; the sigmoid output gate when `gate`.
+ * seq_lens (device int32) counts each sequence's cached keys before the
+ * step and is not advanced here; sequences with seq_lens[s] + 1 >
+ * max_seq_len attend their first max_seq_len keys and append nothing.
+ * RoPE cos/sin come from rope_table [rope_rows][rot_dim] (device; row pos =
+ * cos of the rot_dim/2 pairs, then sin -- see anelm_rope_table) for
+ * positions below rope_rows, else from the same formula evaluated on the
+ * device (rope_table may be NULL), as qwen3_5.cpp:961-971 switches from its
+ * table to cpu_ops.cpp:51-55 past 4096.  Pages as for anelm_attn_decode_paged;
+ * out [n_seqs][n_heads][head_dim]. */
+int anelm_attn_decode_paged_step(float* out, const float* q_gate, const float* k, const float* v,
+                                 uint16_t* k_pages, uint16_t* v_pages, const int32_t* page_table,
+                                 const int32_t* seq_lens, const int32_t* positions,
+                                 const float* q_norm_w, const float* k_norm_w,
+                                 const float* rope_table, int rope_rows,
+                                 int n_seqs, int max_pages, int page_size, int n_pages, int max_seq_len,
+                                 int n_heads, int n_kv_heads, int head_dim, int rot_dim, float theta,
+                                 float eps, int rope_mode, int gate, void* stream);
+
+/* RoPE table rows 0..n_pos-1 (models/llm/qwen3_5.cpp:308-324): row pos holds
+ * cosf(pos * f_j) for the rot_dim/2 pairs j, then sinf(pos * f_j), with
+ * f_j = 1 / powf(theta, 2j / rot_dim), evaluated on the host exactly as
+ * cpu_ops.cpp:51-55 and copied to the device array `table`
+ * [n_pos][rot_dim].  Synchronous. */
+int anelm_rope_table(float* table, int rot_dim, int n_pos, float theta);
+
 /* Causal GQA prefill (no reference kernel: generate.cpp:76-84 runs the
  * decode core per token, so row t attends keys 0..t).  q [S][Hq][D],
  * k/v [S][Hkv][D] fp16; out [S][Hq][D] fp32 (out_dtype ANELM_F32) or fp16.

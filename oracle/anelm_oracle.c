@@ -314,11 +314,16 @@ void orc_full_attn_decode(float* out, float* q_gate, float* k, const float* v,
                           int pos, float theta, float eps, int rope_mode, int gate,
                           int* cache_start, int* cache_len, int cache_capacity) {
     int D = head_dim;
-    for (int h = 0; h < n_heads; h++) {
-        float* qh = q_gate + (long)h * 2 * D;
-        orc_rmsnorm(qh, qh, q_norm_w, D, eps);
+    /* NULL norm weights: q and k arrive normalised (scripts/serve_hybrid.py:89-107
+     * applies RoPE only) */
+    if (q_norm_w) {
+        for (int h = 0; h < n_heads; h++) {
+            float* qh = q_gate + (long)h * 2 * D;
+            orc_rmsnorm(qh, qh, q_norm_w, D, eps);
+        }
     }
-    for (int h = 0; h < n_kv_heads; h++) orc_rmsnorm(k + (long)h * D, k + (long)h * D, k_norm_w, D, eps);
+    if (k_norm_w)
+        for (int h = 0; h < n_kv_heads; h++) orc_rmsnorm(k + (long)h * D, k + (long)h * D, k_norm_w, D, eps);
     orc_apply_rope(q_gate, k, n_heads, n_kv_heads, D, 2 * D, D, rot_dim, pos, theta, 0, 0, rope_mode);
 
     int slot;

@@ -216,8 +216,11 @@ def full_attn_decode(q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, n_heads
     st = ctypes.c_int(cache_start)
     ln = ctypes.c_int(cache_len)
     out = np.empty((n_heads, head_dim), np.float32)
+    qn = None if q_norm_w is None else _f32(q_norm_w)
+    kn = None if k_norm_w is None else _f32(k_norm_w)
     lib().orc_full_attn_decode(_p(out), _p(qg), _p(kk), _p(_f32(v)), _p(kc), _p(vc),
-                               _p(_f32(q_norm_w)), _p(_f32(k_norm_w)), n_heads, n_kv_heads,
+                               None if qn is None else _p(qn), None if kn is None else _p(kn),
+                               n_heads, n_kv_heads,
                                head_dim, rot_dim, pos, theta, eps, rope_mode, 1 if gate else 0,
                                ctypes.byref(st), ctypes.byref(ln), cache_capacity)
     return out, kc, vc, st.value, ln.value

@@ -278,6 +278,28 @@ def test_full_attn_decode_composition(orc):
     assert (st2, ln2) == (6, 48) and np.array_equal(kc2[5], f16(kn))
 
 
+def test_full_attn_decode_without_norms(orc):
+    """NULL norm weights: RoPE, append, attention and gate of the raw q / k
+    (a plausible slip -- norming anyway, or skipping RoPE with the norm --
+    breaks the float64 composition)."""
+    c = attn_decode_case(13, n_heads=4, n_kv_heads=2, head_dim=64, cached=30, capacity=40, start=5)
+    out, kc, _, st, ln = orc.full_attn_decode(
+        c.q_gate, c.k, c.v, c.k_cache, c.v_cache, None, None, 4, 2, 64, c.rot_dim, c.pos, c.theta, c.eps, 1,
+        False, c.start, c.length, c.capacity)
+    assert (st, ln) == (5, 31)
+    qr = _rope_ref(c.q_gate[:, :64].astype(np.float64), c.rot_dim, c.pos, c.theta, 1)
+    kr = _rope_ref(c.k.astype(np.float64), c.rot_dim, c.pos, c.theta, 1)
+    assert np.array_equal(kc[35], f16(kr))
+    ref = _attn_ref(qr, widen(kc), widen(_vc_after(c)), 4, 2, 64, 64, 5, 31, 40)
+    assert rel_l2(out, ref) < 1e-5
+
+
+def _vc_after(c):
+    vc = c.v_cache.copy()
+    vc[(c.start + c.length) % c.capacity] = f16(c.v)
+    return vc
+
+
 def _rms64(x, w, eps=1e-6):
     x = x.astype(np.float64)
     return x / np.sqrt((x ** 2).mean() + eps) * w

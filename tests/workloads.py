@@ -377,3 +377,41 @@ class OracleLM:
         lw, ll = m["lm_head"]
         logits = orc.lut6_matvec(lw, ll, xf, d["vocab"], H)
         return orc.argmax(logits), logits
+
+
+# ------------------------------------------- batched decode over paged KV
+@dataclass
+class PagedCase:
+    """Sequences over shuffled fp16 pages [page][Hkv][P][D]: sequence s holds
+    lens[s] cached keys (key t in page table[s][t // P], row t % P) and one
+    page slot for its next key."""
+    lens: np.ndarray      # [n_seqs] int32, cached keys before the step
+    table: np.ndarray     # [n_seqs][max_pages] int32
+    k_pages: np.ndarray   # uint16 fp16 bits
+    v_pages: np.ndarray
+    page_size: int
+
+    def gather(self, s, pages, n):
+        """First n keys of sequence s from `pages` as a contiguous fp32 [n][Hkv][D] cache."""
+        P = self.page_size
+        pg = self.table[s, :(n + P - 1) // P]
+        Hkv, D = pages.shape[1], pages.shape[3]
+        return widen(pages[pg]).transpose(0, 2, 1, 3).reshape(-1, Hkv, D)[:n]
+
+
+def paged_case(seed, n_seqs=32, lo=256, hi=16384, Hkv=4, D=256, P=16, lens=None):
+    """Ragged lengths U[lo, hi] (seeded), a page for every key including the
+    next one, pages shuffled over the pool, fp16 K / V ~ N(0,1)."""
+    rng = np.random.default_rng(seed)
+    lens = (rng.integers(lo, hi + 1, n_seqs) if lens is None else np.asarray(lens)).astype(np.int32)
+    npg = (lens + 1 + P - 1) // P
+    n_pages = int(npg.sum())
+    perm = rng.permutation(n_pages).astype(np.int32)
+    table = np.zeros((len(lens), int(npg.max())), np.int32)
+    off = 0
+    for s in range(len(lens)):
+        table[s, :npg[s]] = perm[off:off + npg[s]]
+        off += npg[s]
+    kp = f16(rng.standard_normal((n_pages, Hkv, P, D), dtype=np.float32))
+    vp = f16(rng.standard_normal((n_pages, Hkv, P, D), dtype=np.float32))
+    return PagedCase(lens, table, kp, vp, P)
