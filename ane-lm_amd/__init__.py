@@ -59,6 +59,7 @@ SIGNATURES = {
     "anelm_attn_prefill": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P],
     "anelm_ssm_step": [_P, _P, _P, _P, _P, _F, _F, _I, _I, _I, _P],
     "anelm_deltanet_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "anelm_deltanet_decode_batched": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "anelm_deltanet_prefill": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "anelm_lut6_unpack": [_P, _P, _I64, _P],
     "anelm_lut6_gemv": [_P, _P, _P, _P, _I, _I, _P],
@@ -73,6 +74,9 @@ SIGNATURES = {
     "anelm_hybrid_step_run": [_P, _P],
     "anelm_hybrid_step_status": [_P, _IP],
     "anelm_hybrid_step_destroy": [_P],
+    "anelm_batch_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P],
+    "anelm_batch_step_run": [_P, _I, _P],
+    "anelm_batch_step_destroy": [_P],
     # compat tier (host pointers, synchronous)
     "anelm_cpu_silu_vec_inplace": [_P, _I, _P],
     "anelm_cpu_mul_sigmoid_inplace": [_P, _P, _I, _P],
@@ -154,6 +158,26 @@ class HybridDims(ctypes.Structure):
     _fields_ = [("hidden", _I), ("inter", _I), ("n_heads", _I), ("n_kv_heads", _I),
                 ("head_dim", _I), ("rot_dim", _I), ("rope_mode", _I), ("theta", _F), ("eps", _F),
                 ("lin_k_heads", _I), ("lin_v_heads", _I), ("lin_dim", _I)]
+
+
+class BatchLayer(ctypes.Structure):
+    """anelm_batch_layer (include/anelm.h)."""
+    _fields_ = [("kind", _I),
+                ("q_gate", _P), ("k", _P), ("v", _P), ("k_pages", _P), ("v_pages", _P), ("page_table", _P),
+                ("q_norm_w", _P), ("k_norm_w", _P),
+                ("state", _P), ("dn_q", _P), ("dn_k", _P), ("dn_v", _P), ("dn_a", _P), ("dn_b", _P),
+                ("dn_A", _P), ("dn_dt_bias", _P), ("dn_z", _P), ("dn_norm_w", _P), ("dn_flags", _I),
+                ("core_out", _P),
+                ("ffn_norm_w", _P), ("gate_up_w", _P), ("gate_up_lut", _P), ("down_w", _P), ("down_lut", _P)]
+
+
+class BatchSeqs(ctypes.Structure):
+    """anelm_batch_seqs (include/anelm.h)."""
+    _fields_ = [("n_seqs", _I), ("seq_lens", _P), ("positions", _P),
+                ("page_size", _I), ("n_pages", _I), ("max_pages", _I), ("max_seq_len", _I),
+                ("rope_table", _P), ("rope_rows", _I),
+                ("final_norm_w", _P), ("lm_w", _P), ("lm_lut", _P), ("vocab", _I), ("top_k", _I),
+                ("top_idx", _P), ("top_val", _P)]
 
 
 LAYER_DELTANET = 0

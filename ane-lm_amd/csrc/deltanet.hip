@@ -33,6 +33,7 @@ struct DnParams {
     const float* z;
     const float* norm_w;
     int Hk, Hv, flags;
+    int w_heads;   // A / dt_bias hold w_heads entries: head h uses entry h % w_heads
 };
 
 // CB state columns per workgroup of NT threads: thread t owns column
@@ -76,8 +77,9 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
 
     // Gates (qwen3_5.cpp:896-898; cpu_ops.h:13-14).
     const float beta = 1.0f / (1.0f + expf(-p.b[h]));
-    const float sp = logf(1.0f + expf(p.a[h] + p.dt_bias[h]));
-    const float decay = expf(-p.A[h] * sp);
+    const int hw = h % p.w_heads;
+    const float sp = logf(1.0f + expf(p.a[h] + p.dt_bias[hw]));
+    const float decay = expf(-p.A[hw] * sp);
     const bool tf = (p.flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
     const float vj = p.v[(size_t)h * kDV + j];
     __syncthreads();
@@ -582,11 +584,41 @@ __global__ __launch_bounds__(kMsNT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 
 using namespace anelm;
 
+namespace anelm {
+namespace {
+int deltanet_decode_impl(float* y, float* state, const float* q, const float* k, const float* v, const float* a,
+                         const float* b, const float* A, const float* dt_bias, const float* z, const float* norm_w,
+                         int n_seqs, int Hk, int Hv, int dk, int dv, int flags, hipStream_t st);
+}  // namespace
+}  // namespace anelm
+
 extern "C" int anelm_deltanet_decode(float* y, float* state, const float* q, const float* k,
                                      const float* v, const float* a, const float* b,
                                      const float* A, const float* dt_bias, const float* z,
                                      const float* norm_w, int Hk, int Hv, int dk, int dv,
                                      int flags, void* stream) {
+    return deltanet_decode_impl(y, state, q, k, v, a, b, A, dt_bias, z, norm_w, 1, Hk, Hv, dk, dv, flags,
+                                as_stream(stream));
+}
+
+extern "C" int anelm_deltanet_decode_batched(float* y, float* state, const float* q, const float* k,
+                                             const float* v, const float* a, const float* b,
+                                             const float* A, const float* dt_bias, const float* z,
+                                             const float* norm_w, int n_seqs, int Hk, int Hv, int dk,
+                                             int dv, int flags, void* stream) {
+    return deltanet_decode_impl(y, state, q, k, v, a, b, A, dt_bias, z, norm_w, n_seqs, Hk, Hv, dk, dv, flags,
+                                as_stream(stream));
+}
+
+namespace anelm {
+namespace {
+// n_seqs sequences of Hk key / Hv value heads as one launch over n_seqs * Hv
+// heads: sequence s's value head j is head s*Hv + j, its key head
+// s*Hk + j/(Hv/Hk) -- the same h / (Hv/Hk) mapping over the stacked heads --
+// and A / dt_bias (layer weights) are shared by the sequences.
+int deltanet_decode_impl(float* y, float* state, const float* q, const float* k, const float* v, const float* a,
+                         const float* b, const float* A, const float* dt_bias, const float* z, const float* norm_w,
+                         int n_seqs, int Hk, int Hv, int dk, int dv, int flags, hipStream_t st) {
     ANELM_NONNULL(y);
     ANELM_NONNULL(state);
     ANELM_NONNULL(q);
@@ -600,7 +632,8 @@ extern "C" int anelm_deltanet_decode(float* y, float* state, const float* q, con
     ANELM_REQUIRE(Hk > 0 && Hv > 0 && Hv % Hk == 0, "deltanet_decode: Hv %d not a multiple of Hk %d",
                   Hv, Hk);
     ANELM_REQUIRE((flags & ~7) == 0, "deltanet_decode: unknown flags 0x%x", flags);
-    hipStream_t st = as_stream(stream);
+    ANELM_REQUIRE(n_seqs > 0 && (long)n_seqs * Hv <= 65535, "deltanet_decode: %d sequences x %d value heads "
+                  "(at most 65535 heads per launch)", n_seqs, Hv);
     DnParams p{};
     p.y = y;
     p.state = state;
@@ -611,22 +644,25 @@ extern "C" int anelm_deltanet_decode(float* y, float* state, const float* q, con
     p.b = b;
     p.A = A;
     p.dt_bias = dt_bias;
-    p.Hk = Hk;
-    p.Hv = Hv;
+    p.Hk = Hk * n_seqs;
+    p.Hv = Hv * n_seqs;
+    p.w_heads = Hv;
     p.flags = flags;
     if (flags & ANELM_DN_GATED_NORM) {
         ANELM_NONNULL(z);
         ANELM_NONNULL(norm_w);
         p.z = z;
         p.norm_w = norm_w;
-        hipLaunchKernelGGL((deltanet_decode_kernel<128, 512, true>), dim3(1, Hv), dim3(512), 0, st, p);
+        hipLaunchKernelGGL((deltanet_decode_kernel<128, 512, true>), dim3(1, p.Hv), dim3(512), 0, st, p);
     } else {
-        hipLaunchKernelGGL((deltanet_decode_kernel<32, 256, false>), dim3(kDV / 32, Hv), dim3(256), 0,
+        hipLaunchKernelGGL((deltanet_decode_kernel<32, 256, false>), dim3(kDV / 32, p.Hv), dim3(256), 0,
                            st, p);
     }
     ANELM_LAUNCHED("deltanet_decode_kernel");
     return ANELM_OK;
 }
+}  // namespace
+}  // namespace anelm
 
 extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, const float* k,
                                       const float* v, const float* a, const float* b,

@@ -211,6 +211,18 @@ def deltanet_decode(state, q, k, v, a, b, A, dt_bias, flags, z=None, norm_w=None
     return out
 
 
+def deltanet_decode_batched(state, q, k, v, a, b, A, dt_bias, flags, z, norm_w, n_seqs, out=None):
+    """n_seqs sequences' DeltaNet steps in one launch; state [n_seqs*Hv][dk][dv],
+    q,k [n_seqs*Hk][dk], v,z [n_seqs*Hv][dv], a,b [n_seqs*Hv]; A, dt_bias [Hv]
+    and norm_w [dv] are the layer's, shared by the sequences."""
+    Hv = A.numel()
+    Hk = q.numel() // (n_seqs * q.shape[-1])
+    out = torch.empty(n_seqs * Hv, v.shape[-1], device=v.device, dtype=_F32) if out is None else out
+    call("anelm_deltanet_decode_batched", _p(out), _p(state), _p(q), _p(k), _p(v), _p(a), _p(b), _p(A),
+         _p(dt_bias), _p(z), _p(norm_w), n_seqs, Hk, Hv, q.shape[-1], v.shape[-1], flags, _s())
+    return out
+
+
 def deltanet_prefill(state, q, k, v, a, b, A, dt_bias, flags, chunk=64):
     """Chunked prefill; q,k [S][Hk][dk], v [S][Hv][dv], a,b [S][Hv]."""
     S, Hk, dk = q.shape

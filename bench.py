@@ -295,26 +295,33 @@ def measure_cores(anelm, torch, dev, seed=11):
         off += npg[s]
     kp = randn(n_pages, 4, P, 256, dtype=torch.float16)
     vp = randn(n_pages, 4, P, 256, dtype=torch.float16)
-    qb = randn(n_seq, 16, 256)
+    qg = randn(n_seq, 16, 512)
+    kb, vb = randn(n_seq, 4, 256), randn(n_seq, 4, 256)
+    qnw, knw = 1 + randn(256, std=0.02), 1 + randn(256, std=0.02)
     tb = torch.from_numpy(table).to(dev)
-    lb = torch.from_numpy(lens).to(dev)
+    lb = torch.from_numpy(lens - 1).to(dev)          # cached keys; the step appends the last one
     ob = torch.empty(n_seq, 16, 256, device=dev)
-    us = _gpu_us(torch, lambda: anelm.ops.attn_decode_paged(qb, kp, vp, tb, lb, int(lens.max()), 16, 4, 256, P,
-                                                            out=ob), 10)
+    rope = anelm.ops.rope_table(64, 16385, 1e7, dev)
+    us = _gpu_us(torch, lambda: anelm.ops.attn_decode_paged_step(
+        qg, kb, vb, kp, vp, tb, lb, qnw, knw, int(lens.max()), 16, 4, 256, P, 64, rope_tab=rope, out=ob), 10)
     r = _hbm(us, int(lens.sum()) * 4 * 256 * 2 * 2)
     r["sum_len"] = int(lens.sum())
+    r["composition"] = "q/k RMSNorm, RoPE, fp16 page append, attention, gate per sequence"
     res["batch32_paged_attention_layer"] = r
     del kp, vp
-    # ... DeltaNet decode of all 32 sequences in one launch (1024 value heads) ...
+    # ... DeltaNet decode of all 32 sequences in one launch (1024 value heads,
+    # the layer's A / dt_bias / norm weight shared, gated norm) ...
     Hk, Hv = 16 * n_seq, 32 * n_seq
     st = randn(Hv, 128, 128, std=0.1)
     bq, bk = l2n(randn(Hk, 128)), l2n(randn(Hk, 128))
-    bv = randn(Hv, 128)
-    ba, bb, bdt = randn(Hv), randn(Hv), randn(Hv)
-    bA = torch.exp(torch.rand(Hv, generator=g, device=dev) * math.log(16.0))
+    bv, bz = randn(Hv, 128), randn(Hv, 128)
+    ba, bb, bdt = randn(Hv), randn(Hv), randn(32)
+    bA = torch.exp(torch.rand(32, generator=g, device=dev) * math.log(16.0))
+    bnw = 1 + randn(128, std=0.02)
     by = torch.empty(Hv, 128, device=dev)
-    us = _gpu_us(torch, lambda: anelm.ops.deltanet_decode(st, bq, bk, bv, ba, bb, bA, bdt, 1, out=by), 20)
-    res["batch32_deltanet_layer"] = _hbm(us, Hv * 128 * 128 * 4 * 2 + (2 * Hk + 2 * Hv) * 128 * 4)
+    us = _gpu_us(torch, lambda: anelm.ops.deltanet_decode_batched(st, bq, bk, bv, ba, bb, bA, bdt, 1 | 4, bz, bnw,
+                                                                  n_seq, out=by), 20)
+    res["batch32_deltanet_layer"] = _hbm(us, Hv * 128 * 128 * 4 * 2 + (2 * Hk + 3 * Hv) * 128 * 4)
     del st
     # ... and the LM head: top-32 of a [262144][2560] LUT6 matrix for 32 fp16-valued inputs
     V, D = 262144, 2560
@@ -328,15 +335,17 @@ def measure_cores(anelm, torch, dev, seed=11):
 
 def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
     """32 concurrent sequences at the 4B shape through one decode step of 32
-    hybrid layers: per full-attention layer the paged attention of every
-    sequence over its own shuffled 16-token pages (ragged lengths U[256, 16384],
-    seeded; q / k already normalised and rotated), per DeltaNet layer one
-    launch over the 32 x 32 value heads (own fp32 state each, gated norm), per
-    layer the batched LUT6 SwiGLU FFN (RMSNorm rows, gate and up projections,
-    silu(g) * u, down projection accumulated into the residual), then the
-    top-32 of the 262144-row LUT6 LM head for the 32 hidden states.  Every
-    layer has its own weights, caches and states (nothing is re-read from a
-    cache by construction)."""
+    hybrid layers with the batched-step executor (anelm_batch_step): per
+    full-attention layer the fused step of every sequence over its own
+    shuffled 16-token pages (q/k RMSNorm, RoPE at the sequence's position,
+    fp16 page append, attention over its ragged U[256, 16384] keys, gate);
+    per DeltaNet layer one launch over the 32 x 32 value heads (own fp32
+    state each, gated norm); per layer the batched LUT6 SwiGLU FFN (RMSNorm
+    rows, stacked gate/up projection, silu(g) * u, down projection into the
+    residual); then the top-32 of the 262144-row LUT6 LM head for the 32
+    hidden states.  Every layer has its own weights, caches and states
+    (nothing is re-read from a cache by construction).  The step is timed
+    without advancing the lengths, so every repetition does the same work."""
     import numpy as np
     c = CFG
     g = torch.Generator(device=dev)
@@ -353,70 +362,84 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
 
     rng = np.random.default_rng(seed)
     lens = rng.integers(256, 16385, B).astype(np.int32)
-    npg = (lens + P - 1) // P
+    npg = (lens + 1 + P - 1) // P          # pages for the cached keys and the new one
     n_pages = int(npg.sum())
-    layers, kv_bytes, dn_bytes = [], 0, 0
+    max_pages = int(npg.max())
+    layers = (anelm.BatchLayer * c["layers"])()
+    keep, kv_bytes, dn_bytes = [], 0, 0
     for i in range(c["layers"]):
-        L = {"ffn_norm": 1 + randn(H, std=0.02),
-             # gate and up stacked as one projection ([gate; up] rows and LUT groups)
-             "gate_up": (randbytes(2 * I, H * 3 // 4), randn(2 * I // 32, 64, std=0.02, dtype=torch.float16)),
-             "down": (randbytes(H, I * 3 // 4), randn(H // 32, 64, std=0.02, dtype=torch.float16))}
+        L = layers[i]
+        t = {"ffn_norm_w": 1 + randn(H, std=0.02),
+             "gate_up_w": randbytes(2 * I, H * 3 // 4),
+             "gate_up_lut": randn(2 * I // 32, 64, std=0.02, dtype=torch.float16),
+             "down_w": randbytes(H, I * 3 // 4),
+             "down_lut": randn(H // 32, 64, std=0.02, dtype=torch.float16)}
         if (i + 1) % 4 == 0:
+            L.kind = anelm.LAYER_ATTENTION
             perm = rng.permutation(n_pages).astype(np.int32)
-            table = np.zeros((B, int(npg.max())), np.int32)
+            table = np.zeros((B, max_pages), np.int32)
             off = 0
-            for s in range(B):
-                table[s, :npg[s]] = perm[off:off + npg[s]]
-                off += npg[s]
-            L["kp"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
-            L["vp"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
-            L["table"] = torch.from_numpy(table).to(dev)
-            L["q"] = randn(B, Hq, D)
-            L["out"] = torch.empty(B, Hq, D, device=dev)
-            kv_bytes += int(lens.sum()) * Hkv * D * 2 * 2
+            for sq in range(B):
+                table[sq, :npg[sq]] = perm[off:off + npg[sq]]
+                off += npg[sq]
+            t["k_pages"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
+            t["v_pages"] = randn(n_pages, Hkv, P, D, dtype=torch.float16)
+            t["page_table"] = torch.from_numpy(table).to(dev)
+            t["q_gate"] = randn(B, Hq, 2 * D)
+            t["k"] = randn(B, Hkv, D)
+            t["v"] = randn(B, Hkv, D)
+            t["q_norm_w"] = 1 + randn(D, std=0.02)
+            t["k_norm_w"] = 1 + randn(D, std=0.02)
+            t["core_out"] = torch.empty(B, Hq * D, device=dev)
+            kv_bytes += int(lens.sum() + B) * Hkv * D * 2 * 2
         else:
-            L["S"] = randn(B * Hv, dl, dl, std=0.1)
-            L["q"] = randn(B * Hk, dl)
-            L["k"] = randn(B * Hk, dl)
-            L["v"] = randn(B * Hv, dl)
-            L["a"], L["b"], L["dt"] = randn(B * Hv), randn(B * Hv), randn(B * Hv)
-            L["A"] = torch.exp(torch.rand(B * Hv, generator=g, device=dev) * math.log(16.0))
-            L["z"] = randn(B * Hv, dl)
-            L["nw"] = 1 + randn(dl, std=0.02)
-            L["y"] = torch.empty(B * Hv, dl, device=dev)
+            L.kind = anelm.LAYER_DELTANET
+            L.dn_flags = 1 | 4
+            t["state"] = randn(B, Hv, dl, dl, std=0.1)
+            t["dn_q"] = randn(B, Hk, dl)
+            t["dn_k"] = randn(B, Hk, dl)
+            t["dn_v"] = randn(B, Hv, dl)
+            t["dn_a"], t["dn_b"] = randn(B, Hv), randn(B, Hv)
+            t["dn_A"] = torch.exp(torch.rand(Hv, generator=g, device=dev) * math.log(16.0))
+            t["dn_dt_bias"] = randn(Hv)
+            t["dn_z"] = randn(B, Hv, dl)
+            t["dn_norm_w"] = 1 + randn(dl, std=0.02)
+            t["core_out"] = torch.empty(B, Hv * dl, device=dev)
             dn_bytes += B * Hv * dl * dl * 4 * 2
-        layers.append(L)
+        for name, ten in t.items():
+            setattr(L, name, ten.data_ptr())
+        keep.append(t)
     lm = (randbytes(V, H * 3 // 4), randn(V // 32, 64, std=0.02, dtype=torch.float16))
+    fnorm = 1 + randn(H, std=0.02)
     lens_d = torch.from_numpy(lens).to(dev)
+    rope = anelm.ops.rope_table(c["rot_dim"], 16385, c["theta"], dev)
     x = randn(B, H)
-    xn = torch.empty(B, H, device=dev)
-    guv = torch.empty(B, 2 * I, device=dev)
-    hv = torch.empty(B, I, device=dev)
-    ops = anelm.ops
-    max_len = int(lens.max())
-
-    def step():
-        for L in layers:
-            if "kp" in L:
-                ops.attn_decode_paged(L["q"], L["kp"], L["vp"], L["table"], lens_d, max_len, Hq, Hkv, D, P,
-                                      out=L["out"])
-            else:
-                ops.deltanet_decode(L["S"], L["q"], L["k"], L["v"], L["a"], L["b"], L["A"], L["dt"], 1 | 4,
-                                    L["z"], L["nw"], out=L["y"])
-            ops.rmsnorm(x, L["ffn_norm"], c["eps"], out=xn)
-            ops.lut6_gemm(L["gate_up"][0], L["gate_up"][1], xn, 2 * I, H, out=guv)
-            ops.swiglu_rows(guv, I, out=hv)
-            ops.lut6_gemm(L["down"][0], L["down"][1], hv, H, I, out=x, accumulate=True)
-        return ops.lut6_topk(lm[0], lm[1], x, V, H, 32)
-
-    us = _gpu_us(torch, step, reps, warm=1)
+    top_idx = torch.empty(B, 32, dtype=torch.int32, device=dev)
+    top_val = torch.empty(B, 32, device=dev)
+    seqs = anelm.BatchSeqs()
+    seqs.n_seqs, seqs.seq_lens, seqs.positions = B, lens_d.data_ptr(), None
+    seqs.page_size, seqs.n_pages, seqs.max_pages, seqs.max_seq_len = P, n_pages, max_pages, max_pages * P
+    seqs.rope_table, seqs.rope_rows = rope.data_ptr(), 16385
+    seqs.final_norm_w, seqs.lm_w, seqs.lm_lut = fnorm.data_ptr(), lm[0].data_ptr(), lm[1].data_ptr()
+    seqs.vocab, seqs.top_k, seqs.top_idx, seqs.top_val = V, 32, top_idx.data_ptr(), top_val.data_ptr()
+    dims = anelm.HybridDims(H, I, Hq, Hkv, D, c["rot_dim"], 0, c["theta"], c["eps"], Hk, Hv, dl)
+    handle = ctypes.c_void_p()
+    anelm.call("anelm_batch_step_create", ctypes.byref(handle), ctypes.byref(dims), layers, c["layers"],
+               ctypes.byref(seqs), ctypes.c_void_p(x.data_ptr()))
+    try:
+        us = _gpu_us(torch, lambda: anelm.call("anelm_batch_step_run", handle, 0,
+                                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                     reps, warm=1)
+    finally:
+        anelm.call("anelm_batch_step_destroy", handle)
     w_bytes = c["layers"] * (3 * H * I * 3 // 4 + (2 * I // 32 + H // 32) * 128)
     lm_bytes = V * H * 3 // 4 + (V // 32) * 128
     total = kv_bytes + dn_bytes + w_bytes + lm_bytes
     r = _hbm(us, total)
     r.update({"sequences": B, "sum_len": int(lens.sum()), "kv_bytes": kv_bytes, "deltanet_state_bytes": dn_bytes,
               "lut6_ffn_bytes": w_bytes, "lm_head_bytes": lm_bytes,
-              "note": "q/k of the attention layers enter already normalised and rotated"})
+              "composition": "fused paged attention step (norms, RoPE, page append, attention, gate), "
+                             "batched DeltaNet, batched LUT6 FFN, final norm + LM-head top-32"})
     return r
 
 

@@ -222,6 +222,17 @@ int anelm_deltanet_decode(float* y, float* state, const float* q, const float* k
                           const float* z, const float* norm_w,
                           int Hk, int Hv, int dk, int dv, int flags, void* stream);
 
+/* anelm_deltanet_decode for n_seqs sequences in one launch: each sequence
+ * has its own inputs and state -- q,k [n_seqs][Hk][dk], v, z, y
+ * [n_seqs][Hv][dv], a,b [n_seqs][Hv], state [n_seqs][Hv][dk][dv] -- and
+ * shares the layer weights A, dt_bias [Hv] and norm_w [dv].  Per sequence
+ * the same composition as anelm_deltanet_decode (qwen3_5.cpp:879-908);
+ * n_seqs * Hv <= 65535. */
+int anelm_deltanet_decode_batched(float* y, float* state, const float* q, const float* k, const float* v,
+                                  const float* a, const float* b, const float* A, const float* dt_bias,
+                                  const float* z, const float* norm_w,
+                                  int n_seqs, int Hk, int Hv, int dk, int dv, int flags, void* stream);
+
 /* Chunked DeltaNet prefill over S tokens (no reference kernel: the reference
  * runs ssm_step per token, qwen3_5.cpp:1204-1217).  q,k [S][Hk][dk],
  * v [S][Hv][dv], a,b [S][Hv]; y [S][Hv][dv]; state [Hv][dk][dv] updated to the
@@ -388,6 +399,76 @@ int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream);
  * clears the flag.  Always 0 for the eager and graph modes. */
 int anelm_hybrid_step_status(anelm_hybrid_step* step, int* status);
 int anelm_hybrid_step_destroy(anelm_hybrid_step* step);
+
+/* ------------------------------------------------ batched decode step */
+/* The layer loop of Qwen35Model::forward (models/llm/qwen3_5.cpp:1278-1356)
+ * over the compute cores for n_seqs concurrent sequences (the JSON-lines
+ * serve loop, main.cpp:241-377, serves them one at a time): per layer the
+ * full-attention core over every sequence's paged cache
+ * (anelm_attn_decode_paged_step) or the DeltaNet core over every
+ * sequence's state (anelm_deltanet_decode_batched), then the SwiGLU FFN
+ * block with residual on x [n_seqs][hidden] through the batched LUT6
+ * projection (each weight dequantised once per 32 sequences); optionally
+ * the final norm and the top-k of the LUT6 LM head.  Per-sequence inputs
+ * carry a leading [n_seqs] dimension. */
+typedef struct {
+    int kind;                     /* ANELM_LAYER_* */
+    /* full attention */
+    const float* q_gate;          /* [B][Hq][2D] */
+    const float* k;               /* [B][Hkv][D] */
+    const float* v;
+    uint16_t* k_pages;            /* [n_pages][Hkv][page_size][D] fp16, this layer's pool */
+    uint16_t* v_pages;
+    const int32_t* page_table;    /* [B][max_pages] */
+    const float* q_norm_w;        /* [D] (both NULL: no q/k norm) */
+    const float* k_norm_w;
+    /* DeltaNet */
+    float* state;                 /* [B][Hv][dk][dv] */
+    const float* dn_q;            /* [B][Hk][dk] */
+    const float* dn_k;
+    const float* dn_v;            /* [B][Hv][dv] */
+    const float* dn_a;            /* [B][Hv] */
+    const float* dn_b;
+    const float* dn_A;            /* [Hv], exp(A_log) */
+    const float* dn_dt_bias;      /* [Hv] */
+    const float* dn_z;            /* [B][Hv][dv] (gated norm) */
+    const float* dn_norm_w;       /* [dv] */
+    int dn_flags;
+    float* core_out;              /* [B][Hq*D] or [B][Hv*dv] */
+    /* FFN */
+    const float* ffn_norm_w;      /* [hidden] */
+    const uint8_t* gate_up_w;     /* LUT6 [2*inter][hidden]: the gate rows, then the up rows */
+    const uint16_t* gate_up_lut;  /* [2*inter/32][64] */
+    const uint8_t* down_w;        /* LUT6 [hidden][inter] */
+    const uint16_t* down_lut;
+} anelm_batch_layer;
+
+typedef struct {
+    int n_seqs;
+    int32_t* seq_lens;            /* device [B]: cached keys per sequence */
+    int32_t* positions;           /* device [B]: position of each new token, or NULL (= seq_lens) */
+    int page_size, n_pages, max_pages, max_seq_len;
+    const float* rope_table;      /* anelm_rope_table rows, or NULL */
+    int rope_rows;
+    /* optional LM head: top_k of lm_w rmsnorm(x[b], final_norm_w) */
+    const float* final_norm_w;    /* NULL: x as is */
+    const uint8_t* lm_w;          /* NULL: no LM head */
+    const uint16_t* lm_lut;
+    int vocab, top_k;
+    int32_t* top_idx;             /* [B][top_k] */
+    float* top_val;
+} anelm_batch_seqs;
+
+typedef struct anelm_batch_step anelm_batch_step;
+
+/* Copies the descriptors; allocates the step's activation scratch. */
+int anelm_batch_step_create(anelm_batch_step** out, const anelm_hybrid_dims* dims,
+                            const anelm_batch_layer* layers, int n_layers,
+                            const anelm_batch_seqs* seqs, float* x);
+/* One step for every sequence; with `advance`, seq_lens (and positions) are
+ * incremented on the device afterwards, as the KV caches grew by one key. */
+int anelm_batch_step_run(anelm_batch_step* step, int advance, void* stream);
+int anelm_batch_step_destroy(anelm_batch_step* step);
 
 #ifdef __cplusplus
 }

@@ -483,6 +483,34 @@ void orc_lut6_matvec(float* y, const uint8_t* packed, const uint16_t* lut, const
     free(w);
 }
 
+/* orc_lut6_matvec for `batch` inputs x [batch][in_dim] -> y [batch][out_dim]:
+ * each row is dequantised once and every input's sum runs over the columns
+ * in the same order as orc_lut6_matvec (the loop over the inputs is the
+ * inner one), so y[b] equals orc_lut6_matvec of x[b] bit for bit. */
+void orc_lut6_matvec_batch(float* y, const uint8_t* packed, const uint16_t* lut, const float* x,
+                           int batch, int out_dim, int in_dim) {
+    float* w = (float*)malloc(sizeof(float) * (size_t)in_dim);
+    float* xt = (float*)malloc(sizeof(float) * (size_t)in_dim * batch);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)batch);
+    for (int b = 0; b < batch; b++)
+        for (int c = 0; c < in_dim; c++)
+            xt[(size_t)c * batch + b] = orc_f16_to_f32(orc_f32_to_f16(x[(size_t)b * in_dim + c]));
+    long row_bytes = (long)in_dim * 3 / 4;
+    for (int r = 0; r < out_dim; r++) {
+        orc_lut6_dequant_row(w, packed + (long)r * row_bytes, lut + (long)(r / 32) * 64, in_dim);
+        for (int b = 0; b < batch; b++) acc[b] = 0.0f;
+        for (int c = 0; c < in_dim; c++) {
+            const float wc = w[c];
+            const float* xc = xt + (size_t)c * batch;
+            for (int b = 0; b < batch; b++) acc[b] += wc * xc[b];
+        }
+        for (int b = 0; b < batch; b++) y[(size_t)b * out_dim + r] = acc[b];
+    }
+    free(acc);
+    free(xt);
+    free(w);
+}
+
 /* SwiGLU FFN (models/llm/qwen3_5.cpp:1118-1130): down(silu(gate x) * (up x)).
  * scratch holds 2*inter floats. */
 void orc_lut6_ffn(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
@@ -498,6 +526,23 @@ void orc_lut6_ffn(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
         g[i] = (gv / (1.0f + expf(-gv))) * u[i];
     }
     orc_lut6_matvec(y, down_w, down_lut, g, hidden, inter, 0, hidden);
+}
+
+/* orc_lut6_ffn for `batch` inputs x [batch][hidden] -> y [batch][hidden],
+ * bit-identical per input; scratch holds 3 * batch * inter floats. */
+void orc_lut6_ffn_batch(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
+                        const uint8_t* up_w, const uint16_t* up_lut,
+                        const uint8_t* down_w, const uint16_t* down_lut,
+                        const float* x, int batch, int hidden, int inter, float* scratch) {
+    float* g = scratch;
+    float* u = scratch + (size_t)batch * inter;
+    orc_lut6_matvec_batch(g, gate_w, gate_lut, x, batch, inter, hidden);
+    orc_lut6_matvec_batch(u, up_w, up_lut, x, batch, inter, hidden);
+    for (size_t i = 0; i < (size_t)batch * inter; i++) {
+        float gv = g[i];
+        g[i] = (gv / (1.0f + expf(-gv))) * u[i];
+    }
+    orc_lut6_matvec_batch(y, down_w, down_lut, g, batch, hidden, inter);
 }
 
 /* torch.topk over logits (scripts/export_hybrid_chunks.py:409-421) with the

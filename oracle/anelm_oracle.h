@@ -92,6 +92,12 @@ void orc_lut6_unpack(uint8_t* idx, const uint8_t* packed, long n);
 void orc_lut6_dequant_row(float* w, const uint8_t* packed_row, const uint16_t* lut64, int in_dim);
 void orc_lut6_matvec(float* y, const uint8_t* packed, const uint16_t* lut, const float* x,
                      int out_dim, int in_dim, int row_begin, int row_end);
+void orc_lut6_matvec_batch(float* y, const uint8_t* packed, const uint16_t* lut, const float* x,
+                           int batch, int out_dim, int in_dim);
+void orc_lut6_ffn_batch(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
+                        const uint8_t* up_w, const uint16_t* up_lut,
+                        const uint8_t* down_w, const uint16_t* down_lut,
+                        const float* x, int batch, int hidden, int inter, float* scratch);
 void orc_lut6_ffn(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
                   const uint8_t* up_w, const uint16_t* up_lut,
                   const uint8_t* down_w, const uint16_t* down_lut,

@@ -46,6 +46,8 @@ _SIGS = {
     "orc_lut6_unpack": (None, [_P, _P, _L]),
     "orc_lut6_dequant_row": (None, [_P, _P, _P, _I]),
     "orc_lut6_matvec": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "orc_lut6_matvec_batch": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "orc_lut6_ffn_batch": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "orc_lut6_ffn": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "orc_topk": (None, [_P, _P, _P, _L, _I]),
     "orc_argmax": (_I, [_P, _I]),
@@ -290,6 +292,28 @@ def lut6_matvec(w, lut, x, out_dim, in_dim, row_begin=0, row_end=None):
     lib().orc_lut6_matvec(_p(y), _p(np.ascontiguousarray(w, np.uint8)),
                           _p(np.ascontiguousarray(lut, np.uint16)), _p(_f32(x)), out_dim, in_dim,
                           row_begin, row_end)
+    return y
+
+
+def lut6_matvec_batch(w, lut, x, out_dim, in_dim):
+    """y[b] = lut6_matvec(x[b]) for x [batch][in_dim], bit-identical per input."""
+    x = _f32(x).reshape(-1, in_dim)
+    y = np.empty((x.shape[0], out_dim), np.float32)
+    lib().orc_lut6_matvec_batch(_p(y), _p(np.ascontiguousarray(w, np.uint8)),
+                                _p(np.ascontiguousarray(lut, np.uint16)), _p(x), x.shape[0], out_dim, in_dim)
+    return y
+
+
+def lut6_ffn_batch(x, gate, up, down, hidden, inter):
+    """lut6_ffn per row of x [batch][hidden], bit-identical per row."""
+    x = _f32(x).reshape(-1, hidden)
+    y = np.empty_like(x)
+    scratch = np.empty(3 * x.shape[0] * inter, np.float32)
+    c = np.ascontiguousarray
+    lib().orc_lut6_ffn_batch(_p(y), _p(c(gate[0], np.uint8)), _p(c(gate[1], np.uint16)),
+                             _p(c(up[0], np.uint8)), _p(c(up[1], np.uint16)),
+                             _p(c(down[0], np.uint8)), _p(c(down[1], np.uint16)), _p(x), x.shape[0],
+                             hidden, inter, _p(scratch))
     return y
 
 

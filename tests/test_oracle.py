@@ -496,3 +496,18 @@ def test_topk_nan_ranks_as_minus_inf(orc):
     small = np.array([np.nan, 2.0, np.nan, 1.0, np.nan], np.float32)
     idx, val = orc.topk(small, 5)
     assert list(idx) == [1, 3, 0, 2, 4] and np.all(np.isneginf(val[2:]))
+
+
+def test_lut6_batch_forms_equal_per_input(orc):
+    """The batched matvec / FFN restate the per-input ones exactly: every
+    input's sum runs over the columns in the same order, so each row of the
+    batch result equals the per-input result bit for bit."""
+    rng = np.random.default_rng(27)
+    H, I, B = 256, 512, 5
+    g, u, d = lut6_matrix(28, I, H), lut6_matrix(29, I, H), lut6_matrix(30, H, I)
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    yb = orc.lut6_matvec_batch(g[0], g[1], x, I, H)
+    fb = orc.lut6_ffn_batch(x, g[:2], u[:2], d[:2], H, I)
+    for b in range(B):
+        assert np.array_equal(yb[b], orc.lut6_matvec(g[0], g[1], x[b], I, H))
+        assert np.array_equal(fb[b], orc.lut6_ffn(x[b], g[:2], u[:2], d[:2], H, I))

@@ -399,12 +399,13 @@ class PagedCase:
         return widen(pages[pg]).transpose(0, 2, 1, 3).reshape(-1, Hkv, D)[:n]
 
 
-def paged_case(seed, n_seqs=32, lo=256, hi=16384, Hkv=4, D=256, P=16, lens=None):
-    """Ragged lengths U[lo, hi] (seeded), a page for every key including the
-    next one, pages shuffled over the pool, fp16 K / V ~ N(0,1)."""
+def paged_case(seed, n_seqs=32, lo=256, hi=16384, Hkv=4, D=256, P=16, lens=None, spare=1):
+    """Ragged lengths U[lo, hi] (seeded), a page for every key including
+    `spare` more (the next steps' keys), pages shuffled over the pool, fp16
+    K / V ~ N(0,1)."""
     rng = np.random.default_rng(seed)
     lens = (rng.integers(lo, hi + 1, n_seqs) if lens is None else np.asarray(lens)).astype(np.int32)
-    npg = (lens + 1 + P - 1) // P
+    npg = (lens + spare + P - 1) // P
     n_pages = int(npg.sum())
     perm = rng.permutation(n_pages).astype(np.int32)
     table = np.zeros((len(lens), int(npg.max())), np.int32)
@@ -415,3 +416,114 @@ def paged_case(seed, n_seqs=32, lo=256, hi=16384, Hkv=4, D=256, P=16, lens=None)
     kp = f16(rng.standard_normal((n_pages, Hkv, P, D), dtype=np.float32))
     vp = f16(rng.standard_normal((n_pages, Hkv, P, D), dtype=np.float32))
     return PagedCase(lens, table, kp, vp, P)
+
+
+@dataclass
+class BatchModel:
+    """Seeded random-init hybrid stack for a batch of sequences (layer i is
+    full attention iff (i+1) % 4 == 0): per attention layer its own page
+    pool (PagedCase, shared lengths) and per-sequence q_gate / k / v; per
+    DeltaNet layer per-sequence states and inputs with the layer's A,
+    dt_bias and norm weights; per layer the FFN with gate and up stacked as
+    one [2*inter][hidden] LUT6 projection; x [B][hidden]."""
+    dims: dict
+    lens: np.ndarray
+    layers: list
+    x: np.ndarray
+
+
+def batch_model(seed, n_layers, n_seqs, lo=256, hi=2048, dims=QWEN35_4B, lut_std=0.02, P=16, spare=2):
+    rng = np.random.default_rng(seed)
+    d = dims
+    H, I, D = d["hidden"], d["inter"], d["head_dim"]
+    Hq, Hkv, Hk, Hv, dl = d["n_heads"], d["n_kv_heads"], d["lin_k_heads"], d["lin_v_heads"], d["lin_dim"]
+    lens = rng.integers(lo, hi + 1, n_seqs).astype(np.int32)
+    layers = []
+
+    def l2n(x):
+        return (x / np.sqrt((x.astype(np.float64) ** 2).sum(-1, keepdims=True))).astype(np.float32)
+
+    def normal(*shape, std=1.0):
+        return (std * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+
+    for i in range(n_layers):
+        L = {}
+        if layer_is_attention(i):
+            L["kind"] = 1
+            L["pages"] = paged_case(int(rng.integers(1 << 30)), lens=lens, Hkv=Hkv, D=D, P=P, spare=spare)
+            L["q_gate"] = normal(n_seqs, Hq, 2 * D)
+            L["k"] = normal(n_seqs, Hkv, D)
+            L["v"] = normal(n_seqs, Hkv, D)
+            L["q_norm_w"] = 1 + normal(D, std=0.02)
+            L["k_norm_w"] = 1 + normal(D, std=0.02)
+        else:
+            L["kind"] = 0
+            L["state"] = normal(n_seqs, Hv, dl, dl, std=0.1)
+            L["dn_q"] = l2n(normal(n_seqs, Hk, dl))
+            L["dn_k"] = l2n(normal(n_seqs, Hk, dl))
+            L["dn_v"] = normal(n_seqs, Hv, dl)
+            L["dn_a"] = normal(n_seqs, Hv)
+            L["dn_b"] = normal(n_seqs, Hv)
+            L["dn_A"] = np.exp(rng.uniform(0.0, math.log(16.0), Hv)).astype(np.float32)
+            L["dn_dt_bias"] = normal(Hv)
+            L["dn_z"] = normal(n_seqs, Hv, dl)
+            L["dn_norm_w"] = 1 + normal(dl, std=0.02)
+            L["dn_flags"] = 1 | 4
+        L["ffn_norm_w"] = 1 + normal(H, std=0.02)
+        L["gate_up_w"] = rng.integers(0, 256, (2 * I, H * 3 // 4), dtype=np.uint8)
+        L["gate_up_lut"] = f16(lut_std * rng.standard_normal((2 * I // 32, 64)))
+        L["down_w"] = rng.integers(0, 256, (H, I * 3 // 4), dtype=np.uint8)
+        L["down_lut"] = f16(lut_std * rng.standard_normal((H // 32, 64)))
+        layers.append(L)
+    return BatchModel(dict(d), lens, layers, normal(n_seqs, H))
+
+
+class OracleBatch:
+    """The oracle's decode step for every sequence of a BatchModel: per
+    sequence its attention ring (the gathered pages, capacity for `steps`
+    more keys) or DeltaNet state, then the FFN on all rows."""
+
+    def __init__(self, orc, m: BatchModel, steps):
+        self.orc, self.m = orc, m
+        self.rings = {}
+        for i, L in enumerate(m.layers):
+            if L["kind"] == 1:
+                c = L["pages"]
+                rows = []
+                for s, n in enumerate(m.lens):
+                    cap = int(n) + steps
+                    kc = np.zeros((cap,) + c.k_pages.shape[1:2] + c.k_pages.shape[3:], np.uint16)
+                    vc = np.zeros_like(kc)
+                    kc[:n], vc[:n] = f16(c.gather(s, c.k_pages, int(n))), f16(c.gather(s, c.v_pages, int(n)))
+                    rows.append([kc, vc, 0, int(n), cap])
+                self.rings[i] = rows
+        self.state = {i: L["state"].copy() for i, L in enumerate(m.layers) if L["kind"] == 0}
+        self.x = m.x.copy()
+
+    def step(self):
+        orc, m, d = self.orc, self.m, self.m.dims
+        H, I, D = d["hidden"], d["inter"], d["head_dim"]
+        outs = []
+        for i, L in enumerate(m.layers):
+            if L["kind"] == 1:
+                o = []
+                for s, r in enumerate(self.rings[i]):
+                    kc, vc, st, ln, cap = r
+                    y, r[0], r[1], r[2], r[3] = orc.full_attn_decode(
+                        L["q_gate"][s], L["k"][s], L["v"][s], kc, vc, L["q_norm_w"], L["k_norm_w"], d["n_heads"],
+                        d["n_kv_heads"], D, d["rot_dim"], ln, d["theta"], d["eps"], 0, True, st, ln, cap)
+                    o.append(y.reshape(-1))
+                outs.append(np.stack(o))
+            else:
+                o = []
+                for s in range(len(m.lens)):
+                    y, self.state[i][s] = orc.deltanet_decode(
+                        self.state[i][s], L["dn_q"][s], L["dn_k"][s], L["dn_v"][s], L["dn_a"][s], L["dn_b"][s],
+                        L["dn_A"], L["dn_dt_bias"], L["dn_flags"], L["dn_z"][s], L["dn_norm_w"])
+                    o.append(y.reshape(-1))
+                outs.append(np.stack(o))
+            n = np.stack([orc.rmsnorm(xr, L["ffn_norm_w"], d["eps"]) for xr in self.x])
+            gu, gl = L["gate_up_w"], L["gate_up_lut"]
+            self.x = (self.x + orc.lut6_ffn_batch(n, (gu[:I], gl[:I // 32]), (gu[I:], gl[I // 32:]),
+                                                  (L["down_w"], L["down_lut"]), H, I)).astype(np.float32)
+        return outs
