@@ -60,9 +60,11 @@ SIGNATURES = {
     "anelm_ssm_step": [_P, _P, _P, _P, _P, _F, _F, _I, _I, _I, _P],
     "anelm_deltanet_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "anelm_deltanet_decode_batched": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "anelm_deltanet_decode_from_proj": [_P, _P, _P, _IP, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "anelm_deltanet_prefill": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "anelm_lut6_unpack": [_P, _P, _I64, _P],
     "anelm_lut6_gemv": [_P, _P, _P, _P, _I, _I, _P],
+    "anelm_lut6_proj": [_P, _P, _P, _P, _P, _F, _I, _I, _I, _P],
     "anelm_lut6_ffn": [_P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _I, _P],
     "anelm_lut6_gate_up": [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _P],
     "anelm_lut6_swiglu": [_P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _P],
@@ -70,6 +72,7 @@ SIGNATURES = {
     "anelm_swiglu": [_P, _P, _P, _I64, _P],
     "anelm_swiglu_rows": [_P, _P, _I, _I, _P],
     "anelm_lut6_topk": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "anelm_sample_token": [_P, _P, _I, _P, _I, _F, _F, _I, _F, _F, _P],
     "anelm_hybrid_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P, _I, _P],
     "anelm_hybrid_step_run": [_P, _P],
     "anelm_hybrid_step_status": [_P, _IP],
@@ -150,14 +153,16 @@ class HybridLayer(ctypes.Structure):
                 ("dn_b", _P), ("dn_A", _P), ("dn_dt_bias", _P), ("dn_z", _P), ("dn_norm_w", _P),
                 ("dn_flags", _I), ("core_out", _P),
                 ("ffn_norm_w", _P), ("gate_w", _P), ("gate_lut", _P), ("up_w", _P),
-                ("up_lut", _P), ("down_w", _P), ("down_lut", _P)]
+                ("up_lut", _P), ("down_w", _P), ("down_lut", _P),
+                ("in_norm_w", _P), ("first_w", _P), ("first_lut", _P), ("o_w", _P), ("o_lut", _P),
+                ("proj", _P), ("conv_state", _P), ("conv_w", _P), ("conv_pos", _I)]
 
 
 class HybridDims(ctypes.Structure):
     """anelm_hybrid_dims (include/anelm.h)."""
     _fields_ = [("hidden", _I), ("inter", _I), ("n_heads", _I), ("n_kv_heads", _I),
                 ("head_dim", _I), ("rot_dim", _I), ("rope_mode", _I), ("theta", _F), ("eps", _F),
-                ("lin_k_heads", _I), ("lin_v_heads", _I), ("lin_dim", _I)]
+                ("lin_k_heads", _I), ("lin_v_heads", _I), ("lin_dim", _I), ("conv_kernel", _I)]
 
 
 class BatchLayer(ctypes.Structure):

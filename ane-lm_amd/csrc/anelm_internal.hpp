@@ -83,6 +83,10 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
                      int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st);
 int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st);
 
+// y (+)= W x over a LUT6 matrix, x optionally RMS-normalised first (norm_w).
+int lut6_gemv_impl(float* y, const uint8_t* w, const uint16_t* lut, const float* x, const float* norm_w,
+                   float eps, int out_dim, int in_dim, int residual, hipStream_t st);
+
 // anelm_full_attn_decode with the split partials in `part` (part_cap bytes)
 // instead of the library workspace when part != nullptr; and the partials
 // size a call over max_len keys needs (0 for one split).

@@ -34,11 +34,41 @@ struct DnParams {
     const float* norm_w;
     int Hk, Hv, flags;
     int w_heads;   // A / dt_bias hold w_heads entries: head h uses entry h % w_heads
+    // conv prologue (qwen3_5.cpp:867-874): q, k, v are channels of the raw
+    // mixed projection `mix`, passed through the conv ring and SiLU here
+    const float* mix;       // [2*Hk*dk + Hv*dv]
+    float* conv_state;      // [2*Hk*dk + Hv*dv][conv_k - 1]
+    const float* conv_w;    // [2*Hk*dk + Hv*dv][conv_k]
+    int conv_pos, conv_k;
+    uint32_t* readers_done; // [Hk] zeroed counters: workgroups done reading a key head's ring
+    int readers;            // workgroups that read one key head's q/k channels
 };
+
+// conv1d_update for one channel (core/cpu_ops.cpp:89-129): the K-1 ring
+// entries oldest first from `pos`, then the new input; followed by SiLU
+// (silu_vec_inplace, cpu_ops.cpp:6-13: x / (1 + exp(-x))).  The ring write
+// of the new input is left to the caller (it may be shared by workgroups).
+__device__ __forceinline__ float conv_silu(const DnParams& p, int c, float xc) {
+    const int sl = p.conv_k - 1;
+    const float* st = p.conv_state + (size_t)c * sl;
+    const float* w = p.conv_w + (size_t)c * p.conv_k;
+    float sum = 0.f;
+    int idx = p.conv_pos;
+    for (int j = 0; j < sl; j++) {
+        sum += st[idx] * w[j];
+        idx = idx + 1 == sl ? 0 : idx + 1;
+    }
+    const float y = sum + xc * w[sl];
+    return y / (expf(-y) + 1.0f);
+}
 
 // CB state columns per workgroup of NT threads: thread t owns column
 // t % CB for rows [(t / CB) * RPT, +RPT).
-template <int CB, int NT, bool GATED>
+// CONV: the inputs come from the raw projection through conv_silu; each
+// value channel is read by exactly one workgroup, which also writes its ring
+// slot; a key head's q/k channels are read by `readers` workgroups, and the
+// last of them to finish reading (counter) writes their ring slots.
+template <int CB, int NT, bool GATED, bool CONV = false>
 __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
     constexpr int RC = NT / CB;       // row chunks
     constexpr int RPT = kDK / RC;     // rows per thread
@@ -46,6 +76,8 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
     __shared__ float qs[kDK], ks[kDK];
     __shared__ float red_a[RC][CB];
     __shared__ float red[NT / 64];
+    __shared__ float vs[CB];
+    __shared__ int last_reader;
 
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
@@ -61,8 +93,39 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
 
     // q, k of the key head: optional l2 normalisation (cpu_ops.cpp:82-87) and
     // the 1/sqrt(dk) query scale (qwen3_5.cpp:879-887).
-    float qv = 0.f, kv = 0.f;
-    if (tid < kDK) {
+    float qv = 0.f, kv = 0.f, qx = 0.f, kx = 0.f;
+    if constexpr (CONV) {
+        // channels: Q [Hk][dk] | K [Hk][dk] | V [Hv][dv] (qwen3_5.cpp:872-874)
+        const int cq = kh * kDK + tid, ck = p.Hk * kDK + kh * kDK + tid;
+        if (tid < kDK) {
+            qx = p.mix[cq];
+            kx = p.mix[ck];
+            qv = conv_silu(p, cq, qx);
+            kv = conv_silu(p, ck, kx);
+        }
+        if (tid < CB) {
+            const int cv = 2 * p.Hk * kDK + h * kDV + j;
+            const float vx = p.mix[cv];
+            vs[tid] = conv_silu(p, cv, vx);
+            p.conv_state[(size_t)cv * (p.conv_k - 1) + p.conv_pos] = vx;   // this workgroup is its only reader
+        }
+        // every ring read of this workgroup has returned (its values are in
+        // registers): count this workgroup as done with the key head; the last
+        // one stores the new q/k inputs into the ring
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t n = __hip_atomic_fetch_add(p.readers_done + kh, 1u, __ATOMIC_ACQ_REL,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+            last_reader = n == (uint32_t)p.readers - 1u;
+            if (last_reader) __hip_atomic_store(p.readers_done + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last_reader && tid < kDK) {
+            const int sl = p.conv_k - 1;
+            p.conv_state[(size_t)(kh * kDK + tid) * sl + p.conv_pos] = qx;
+            p.conv_state[(size_t)(p.Hk * kDK + kh * kDK + tid) * sl + p.conv_pos] = kx;
+        }
+    } else if (tid < kDK) {
         qv = p.q[(size_t)kh * kDK + tid];
         kv = p.k[(size_t)kh * kDK + tid];
     }
@@ -81,8 +144,10 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
     const float sp = logf(1.0f + expf(p.a[h] + p.dt_bias[hw]));
     const float decay = expf(-p.A[hw] * sp);
     const bool tf = (p.flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
-    const float vj = p.v[(size_t)h * kDV + j];
+    float vj = 0.f;
+    if constexpr (!CONV) vj = p.v[(size_t)h * kDV + j];
     __syncthreads();
+    if constexpr (CONV) vj = vs[c];
 
     float part = 0.f;
 #pragma unroll
@@ -663,6 +728,66 @@ int deltanet_decode_impl(float* y, float* state, const float* q, const float* k,
 }
 }  // namespace
 }  // namespace anelm
+
+extern "C" int anelm_deltanet_decode_from_proj(float* y, float* state, float* conv_state, int* conv_pos,
+                                               const float* proj, const float* conv_w, const float* A,
+                                               const float* dt_bias, const float* norm_w, int Hk, int Hv,
+                                               int dk, int dv, int conv_kernel, int flags, void* stream) {
+    ANELM_NONNULL(y);
+    ANELM_NONNULL(state);
+    ANELM_NONNULL(conv_state);
+    ANELM_NONNULL(conv_pos);
+    ANELM_NONNULL(proj);
+    ANELM_NONNULL(conv_w);
+    ANELM_NONNULL(A);
+    ANELM_NONNULL(dt_bias);
+    ANELM_REQUIRE(dk == kDK && dv == kDV, "deltanet_decode_from_proj: dk=%d dv=%d (only 128x128)", dk, dv);
+    ANELM_REQUIRE(Hk > 0 && Hv > 0 && Hv % Hk == 0 && Hv <= 65535,
+                  "deltanet_decode_from_proj: Hv %d not a multiple of Hk %d", Hv, Hk);
+    ANELM_REQUIRE(conv_kernel >= 2 && conv_kernel <= 16, "deltanet_decode_from_proj: conv kernel %d",
+                  conv_kernel);
+    ANELM_REQUIRE(*conv_pos >= 0 && *conv_pos < conv_kernel - 1, "deltanet_decode_from_proj: conv_pos %d",
+                  *conv_pos);
+    ANELM_REQUIRE((flags & ~7) == 0, "deltanet_decode_from_proj: unknown flags 0x%x", flags);
+    const bool gated = (flags & ANELM_DN_GATED_NORM) != 0;
+    ANELM_REQUIRE(!gated || norm_w != nullptr, "deltanet_decode_from_proj: GATED_NORM needs norm_w");
+    uint32_t* ctr = counters((size_t)Hk);
+    if (!ctr) return set_error(ANELM_ERANGE, "deltanet_decode_from_proj: %d key heads exceed the counter pool", Hk);
+    const long qkv = 2L * Hk * kDK + (long)Hv * kDV;
+    DnParams p{};
+    p.y = y;
+    p.state = state;
+    p.z = proj + qkv;                       // [Hv][dv]
+    p.a = p.z + (long)Hv * kDV;             // [Hv]
+    p.b = p.a + Hv;                         // [Hv]
+    p.A = A;
+    p.dt_bias = dt_bias;
+    p.norm_w = norm_w;
+    p.Hk = Hk;
+    p.Hv = Hv;
+    p.w_heads = Hv;
+    p.flags = flags;
+    p.mix = proj;
+    p.conv_state = conv_state;
+    p.conv_w = conv_w;
+    p.conv_pos = *conv_pos;
+    p.conv_k = conv_kernel;
+    p.readers_done = ctr;
+    hipStream_t st = as_stream(stream);
+    if (gated) {
+        p.readers = Hv / Hk;
+        hipLaunchKernelGGL((deltanet_decode_kernel<128, 512, true, true>), dim3(1, Hv), dim3(512), 0, st, p);
+    } else {
+        p.readers = (Hv / Hk) * (kDV / 32);
+        hipLaunchKernelGGL((deltanet_decode_kernel<32, 256, false, true>), dim3(kDV / 32, Hv), dim3(256), 0, st,
+                           p);
+    }
+    ANELM_LAUNCHED("deltanet_decode_kernel (conv prologue)");
+    int np = *conv_pos + 1;
+    if (np == conv_kernel - 1) np = 0;
+    *conv_pos = np;
+    return ANELM_OK;
+}
 
 extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, const float* k,
                                       const float* v, const float* a, const float* b,

@@ -759,9 +759,10 @@ int gate_up(float* g, float* u, float* h, const float* x, const float* norm_w, f
     return ANELM_OK;
 }
 
-// y = W x, or y += W x with `residual`.
+// y = W x, or y += W x with `residual`; with norm_w, x is first replaced by
+// rmsnorm(x, norm_w, eps) (cpu_ops.cpp:24-30).
 int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int out_dim, int in_dim,
-         int residual, hipStream_t st) {
+         int residual, hipStream_t st, const float* norm_w = nullptr, float eps = 0.f) {
     TileGeom geo;
     if (tile_geom(in_dim, 1, geo)) {
         TileArgs a{};
@@ -769,6 +770,8 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
         a.lut[0] = lut;
         a.y[0] = y;
         a.x = x;
+        a.nw = norm_w;
+        a.eps = eps;
         a.n_mat = 1;
         a.mode = kOutY;
         a.residual = residual;
@@ -782,8 +785,10 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
     a.out_dim = out_dim;
     a.in_dim = in_dim;
     a.x = x;
+    a.nw = norm_w;
+    a.eps = eps;
     a.residual = residual;
-    return gemv_dispatch<kStageCopy>(a, 1, st);
+    return norm_w ? gemv_dispatch<kStageNorm>(a, 1, st) : gemv_dispatch<kStageCopy>(a, 1, st);
 }
 
 // Y[b] (+)= W X[b] for b < batch: the MFMA GEMM over tiles of 32 inputs.  The
@@ -843,6 +848,15 @@ int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x
 
 using namespace anelm;
 
+namespace anelm {
+int lut6_gemv_impl(float* y, const uint8_t* w, const uint16_t* lut, const float* x, const float* norm_w,
+                   float eps, int out_dim, int in_dim, int residual, hipStream_t st) {
+    int rc = check_shape(out_dim, in_dim);
+    if (rc) return rc;
+    return gemv(y, w, lut, x, out_dim, in_dim, residual, st, norm_w, eps);
+}
+}  // namespace anelm
+
 extern "C" {
 
 int anelm_lut6_unpack(uint8_t* idx, const uint8_t* packed, int64_t n, void* stream) {
@@ -866,6 +880,17 @@ int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
     return gemv(y, w, lut, x, out_dim, in_dim, 0, as_stream(stream));
+}
+
+int anelm_lut6_proj(float* y, const uint8_t* w, const uint16_t* lut, const float* x, const float* norm_w,
+                    float eps, int out_dim, int in_dim, int accumulate, void* stream) {
+    ANELM_NONNULL(y);
+    ANELM_NONNULL(w);
+    ANELM_NONNULL(lut);
+    ANELM_NONNULL(x);
+    ANELM_REQUIRE(accumulate == 0 || accumulate == 1, "lut6_proj: accumulate %d", accumulate);
+    ANELM_REQUIRE(!(accumulate && norm_w && y == x), "lut6_proj: y aliases the normalised input");
+    return lut6_gemv_impl(y, w, lut, x, norm_w, eps, out_dim, in_dim, accumulate, as_stream(stream));
 }
 
 int anelm_lut6_gate_up(float* g, float* u, const float* x, const float* norm_w, float eps,

@@ -26,15 +26,33 @@ struct anelm_hybrid_step {
 namespace anelm {
 namespace {
 
+// Rows of a layer's first projection: attention q_gate | k | v
+// (qwen3_5.cpp:948-950), DeltaNet mixed qkv | z | a | b (:849-860).
+int first_out(const anelm_hybrid_dims& d, bool attn) {
+    if (attn) return d.n_heads * 2 * d.head_dim + 2 * d.n_kv_heads * d.head_dim;
+    return 2 * d.lin_k_heads * d.lin_dim + 2 * d.lin_v_heads * d.lin_dim + 2 * d.lin_v_heads;
+}
+
 // One eager pass over all layers; `advance` moves every attention ring one
 // token forward (the host-side KVCache bookkeeping of qwen3_5.cpp:973-983).
 int launch_all(anelm_hybrid_step* s, hipStream_t st, bool advance) {
     const anelm_hybrid_dims& d = s->dims;
     for (auto& L : s->layers) {
         int rc;
-        if (L.kind == ANELM_LAYER_ATTENTION) {
+        const bool proj = L.first_w != nullptr;
+        const bool attn = L.kind == ANELM_LAYER_ATTENTION;
+        if (proj) {
+            // proj = first_w rmsnorm(x, in_norm_w) (qwen3_5.cpp:1287-1300, 1004-1011)
+            rc = lut6_gemv_impl(L.proj, L.first_w, L.first_lut, s->x, L.in_norm_w, d.eps, first_out(d, attn),
+                                d.hidden, 0, st);
+            if (rc) return rc;
+        }
+        if (attn) {
             int start = L.cache_start, len = L.cache_len;
-            rc = full_attn_decode_impl(L.core_out, L.q_gate, L.k, L.v, L.k_cache, L.v_cache, L.q_norm_w,
+            const float* q_gate = proj ? L.proj : L.q_gate;
+            const float* k = proj ? L.proj + (size_t)d.n_heads * 2 * d.head_dim : L.k;
+            const float* v = proj ? k + (size_t)d.n_kv_heads * d.head_dim : L.v;
+            rc = full_attn_decode_impl(L.core_out, q_gate, k, v, L.k_cache, L.v_cache, L.q_norm_w,
                                        L.k_norm_w, d.n_heads, d.n_kv_heads, d.head_dim, d.rot_dim, L.pos,
                                        d.theta, d.eps, d.rope_mode, 1, nullptr, nullptr, &start, &len,
                                        L.cache_capacity, st, s->part, s->part_bytes);
@@ -44,10 +62,24 @@ int launch_all(anelm_hybrid_step* s, hipStream_t st, bool advance) {
                 L.cache_len = len;
                 L.pos++;
             }
+        } else if (proj) {
+            // conv ring + SiLU + split + recurrence from the projection (:849-908)
+            int pos = L.conv_pos;
+            rc = anelm_deltanet_decode_from_proj(L.core_out, L.state, L.conv_state, &pos, L.proj, L.conv_w,
+                                                 L.dn_A, L.dn_dt_bias, L.dn_norm_w, d.lin_k_heads, d.lin_v_heads,
+                                                 d.lin_dim, d.lin_dim, d.conv_kernel, L.dn_flags, st);
+            if (rc) return rc;
+            if (advance) L.conv_pos = pos;
         } else {
             rc = anelm_deltanet_decode(L.core_out, L.state, L.dn_q, L.dn_k, L.dn_v, L.dn_a, L.dn_b,
                                        L.dn_A, L.dn_dt_bias, L.dn_z, L.dn_norm_w, d.lin_k_heads,
                                        d.lin_v_heads, d.lin_dim, d.lin_dim, L.dn_flags, st);
+            if (rc) return rc;
+        }
+        if (proj) {
+            // x += o_proj(core_out) (:1310-1327)
+            const int attn_dim = attn ? d.n_heads * d.head_dim : d.lin_v_heads * d.lin_dim;
+            rc = lut6_gemv_impl(s->x, L.o_w, L.o_lut, L.core_out, nullptr, 0.f, d.hidden, attn_dim, 1, st);
             if (rc) return rc;
         }
         rc = anelm_lut6_ffn(s->x, s->h, L.ffn_norm_w, d.eps, L.gate_w, L.gate_lut, L.up_w, L.up_lut,
@@ -76,9 +108,23 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
                   "hybrid_step: mode %d unknown", mode);
     const bool use_graph = mode == ANELM_STEP_GRAPH;
     ANELM_REQUIRE(!use_graph || stream != nullptr, "hybrid_step: graph capture needs a non-null stream");
-    for (int i = 0; i < n_layers; i++)
-        ANELM_REQUIRE(layers[i].kind == ANELM_LAYER_ATTENTION || layers[i].kind == ANELM_LAYER_DELTANET,
-                      "hybrid_step: layer %d kind %d", i, layers[i].kind);
+    bool any_proj = false;
+    for (int i = 0; i < n_layers; i++) {
+        const anelm_hybrid_layer& L = layers[i];
+        ANELM_REQUIRE(L.kind == ANELM_LAYER_ATTENTION || L.kind == ANELM_LAYER_DELTANET,
+                      "hybrid_step: layer %d kind %d", i, L.kind);
+        if (!L.first_w) continue;
+        any_proj = true;
+        ANELM_REQUIRE(L.first_lut && L.o_w && L.o_lut && L.proj,
+                      "hybrid_step: layer %d has a first projection but no o_proj / proj scratch", i);
+        ANELM_REQUIRE(L.kind == ANELM_LAYER_ATTENTION ||
+                          (L.conv_state && L.conv_w && dims->conv_kernel >= 2 && L.conv_pos >= 0 &&
+                           L.conv_pos < dims->conv_kernel - 1),
+                      "hybrid_step: DeltaNet layer %d needs the conv ring (kernel %d, pos %d)", i,
+                      dims->conv_kernel, L.conv_pos);
+    }
+    ANELM_REQUIRE(!(any_proj && (mode & ANELM_STEP_PERSISTENT)),
+                  "hybrid_step: the persistent step runs core + FFN layers only (no projections)");
     auto* s = new anelm_hybrid_step();
     s->dims = *dims;
     s->layers.assign(layers, layers + n_layers);

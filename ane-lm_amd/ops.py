@@ -223,6 +223,19 @@ def deltanet_decode_batched(state, q, k, v, a, b, A, dt_bias, flags, z, norm_w, 
     return out
 
 
+def deltanet_decode_from_proj(state, conv_state, conv_pos, proj, conv_w, A, dt_bias, norm_w, Hk, flags,
+                              conv_kernel=4, out=None):
+    """qwen3_5.cpp:849-908 from the norm-fused first projection
+    proj = [q|k|v mixed | z | a | b]; conv_state [qkv][K-1] and state
+    [Hv][dk][dv] are updated in place; conv_pos is a ctypes.c_int advanced
+    here."""
+    Hv, dk, dv = state.shape
+    out = torch.empty(Hv, dv, device=state.device, dtype=_F32) if out is None else out
+    call("anelm_deltanet_decode_from_proj", _p(out), _p(state), _p(conv_state), ctypes.byref(conv_pos),
+         _p(proj), _p(conv_w), _p(A), _p(dt_bias), _p(norm_w), Hk, Hv, dk, dv, conv_kernel, flags, _s())
+    return out
+
+
 def deltanet_prefill(state, q, k, v, a, b, A, dt_bias, flags, chunk=64):
     """Chunked prefill; q,k [S][Hk][dk], v [S][Hv][dv], a,b [S][Hv]."""
     S, Hk, dk = q.shape
@@ -238,6 +251,14 @@ def lut6_unpack(packed, n):
     idx = torch.empty(n, device=packed.device, dtype=torch.uint8)
     call("anelm_lut6_unpack", _p(idx), _p(packed), n, _s())
     return idx
+
+
+def lut6_proj(w, lut, x, out_dim, in_dim, norm_w=None, eps=1e-6, y=None, accumulate=False):
+    """y = W rmsnorm(x, norm_w) (norm_w None: W x); with accumulate, y += W n."""
+    y = torch.empty(out_dim, device=x.device, dtype=_F32) if y is None else y
+    call("anelm_lut6_proj", _p(y), _p(w), _p(lut), _p(x), _p(norm_w), eps, out_dim, in_dim,
+         1 if accumulate else 0, _s())
+    return y
 
 
 def lut6_gemv(w, lut, x, out_dim, in_dim, out=None):
@@ -299,3 +320,15 @@ def lut6_topk(w, lut, x, out_dim, in_dim, k):
     call("anelm_lut6_topk", _p(idx), _p(val), _p(w), _p(lut), _p(x), batch, out_dim, in_dim, k,
          _s())
     return idx, val
+
+
+# --------------------------------------------------------------- sampling
+def sample_token(logits, recent, temperature, repetition_penalty=1.2, repetition_context_size=256,
+                 frequency_penalty=0.1, r=0.5, out=None):
+    """core/sampling.cpp:11-66 on the device; recent is a device int32 tensor
+    (or None), r the uniform draw.  Returns a device int32 [1] tensor."""
+    out = torch.empty(1, device=logits.device, dtype=torch.int32) if out is None else out
+    n = 0 if recent is None else recent.numel()
+    call("anelm_sample_token", _p(out), _p(logits), logits.numel(), _p(recent), n, temperature,
+         repetition_penalty, repetition_context_size, frequency_penalty, r, _s())
+    return out

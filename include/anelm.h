@@ -233,6 +233,20 @@ int anelm_deltanet_decode_batched(float* y, float* state, const float* q, const 
                                   const float* z, const float* norm_w,
                                   int n_seqs, int Hk, int Hv, int dk, int dv, int flags, void* stream);
 
+/* Qwen35Model::forward_deltanet_from_proj (models/llm/qwen3_5.cpp:849-908) in
+ * one launch: conv1d_update + SiLU (cpu_ops.cpp:89-129, :6-13) over the
+ * mixed q|k|v channels of the norm-fused first projection, the Q | K | V
+ * split, then the composition of anelm_deltanet_decode.
+ *   proj = [mixed_qkv (2*Hk*dk + Hv*dv) | z (Hv*dv) | a (Hv) | b (Hv)];
+ *   conv_state [2*Hk*dk + Hv*dv][conv_kernel-1] device ring, conv_w
+ *   [2*Hk*dk + Hv*dv][conv_kernel]; *conv_pos is a HOST int advanced here
+ *   (the reference's DeltaNetState::conv_pos, qwen3_5.h:158-162).
+ * Flags as anelm_deltanet_decode; dk, dv = 128. */
+int anelm_deltanet_decode_from_proj(float* y, float* state, float* conv_state, int* conv_pos,
+                                    const float* proj, const float* conv_w, const float* A,
+                                    const float* dt_bias, const float* norm_w, int Hk, int Hv,
+                                    int dk, int dv, int conv_kernel, int flags, void* stream);
+
 /* Chunked DeltaNet prefill over S tokens (no reference kernel: the reference
  * runs ssm_step per token, qwen3_5.cpp:1204-1217).  q,k [S][Hk][dk],
  * v [S][Hv][dv], a,b [S][Hv]; y [S][Hv][dv]; state [Hv][dk][dv] updated to the
@@ -256,6 +270,14 @@ int anelm_lut6_unpack(uint8_t* idx, const uint8_t* packed, int64_t n, void* stre
 /* y = W x (matvec, cpu_ops.cpp:77-80, on the dequantised weights). */
 int anelm_lut6_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x,
                     int out_dim, int in_dim, void* stream);
+
+/* A layer projection around the cores on LUT6 weights: y = W n, or y += W n
+ * with accumulate (the residual add of o_proj, qwen3_5.cpp:1310-1327), where
+ * n = rmsnorm(x, norm_w, eps) (the input norm fused into the first
+ * projection, :1287-1300, 1004-1011) or x when norm_w is NULL.  The
+ * activations enter the dot products as fp16, as in anelm_lut6_gemv. */
+int anelm_lut6_proj(float* y, const uint8_t* w, const uint16_t* lut, const float* x, const float* norm_w,
+                    float eps, int out_dim, int in_dim, int accumulate, void* stream);
 
 /* SwiGLU FFN block with residual (qwen3_5.cpp:1335-1354 with the MLP of
  * :1118-1130): n = rmsnorm(x, norm_w, eps) (skipped when norm_w is NULL);
@@ -310,6 +332,22 @@ int anelm_swiglu_rows(float* h, const float* gu, int rows, int n, void* stream);
 int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const uint16_t* lut,
                     const float* x, int batch, int out_dim, int in_dim, int k, void* stream);
 
+/* ------------------------------------------------------------- sampling */
+
+/* sample_token, core/sampling.h:15-17 / sampling.cpp:11-66, on device logits
+ * [vocab]: penalties of the distinct tokens among the last
+ * repetition_context_size entries of recent [n_recent] (device int32;
+ * repetition penalty if > 1, frequency penalty * count if > 0), then
+ * temperature <= 0: the first index of the maximum; else softmax(logits / T)
+ * and the first index whose running sum reaches r, or vocab-1.  r is the
+ * uniform draw in [0, 1) the reference takes from drand48() (:57): the caller
+ * owns the random stream.  *token (device int32) receives the result; logits
+ * are not modified (the adjusted copy lives in the library workspace).
+ * At most 4096 tokens in the penalty window.  NaN logits never win. */
+int anelm_sample_token(int32_t* token, const float* logits, int vocab, const int32_t* recent,
+                       int n_recent, float temperature, float repetition_penalty,
+                       int repetition_context_size, float frequency_penalty, float r, void* stream);
+
 /* ------------------------------------------------- hybrid decode step */
 /* The layer loop of Qwen35Model::forward (models/llm/qwen3_5.cpp:1278-1356)
  * over the compute cores: per layer the DeltaNet core (:849-910) or the
@@ -353,6 +391,24 @@ typedef struct {
     const uint16_t* up_lut;
     const uint8_t* down_w;
     const uint16_t* down_lut;
+    /* Projections around the core (qwen3_5.cpp:1287-1327).  first_w NULL:
+     * the core inputs above are given and the layer is core + FFN.  With
+     * them the layer is the whole of qwen3_5.cpp:1287-1354:
+     *   proj = first_w rmsnorm(x, in_norm_w) -- DeltaNet [mixed qkv | z | a | b]
+     *   (:849-860), attention [q_gate | k | v] (:948-950);
+     *   the core from proj (DeltaNet through the conv ring, :867-874; the
+     *   dn_q..dn_z / q_gate, k, v pointers are ignored);
+     *   x += o_w core_out (:1310-1323); then the FFN block.
+     * Eager runs advance conv_pos with the rings. */
+    const float* in_norm_w;      /* [hidden] (NULL: no input norm) */
+    const uint8_t* first_w;      /* LUT6 [first_out][hidden] */
+    const uint16_t* first_lut;
+    const uint8_t* o_w;          /* LUT6 [hidden][Hq*D or Hv*dv] */
+    const uint16_t* o_lut;
+    float* proj;                 /* scratch [first_out] */
+    float* conv_state;           /* DeltaNet [2*Hk*dk + Hv*dv][conv_kernel-1] */
+    const float* conv_w;         /* DeltaNet [2*Hk*dk + Hv*dv][conv_kernel] */
+    int conv_pos;
 } anelm_hybrid_layer;
 
 typedef struct {
@@ -360,6 +416,7 @@ typedef struct {
     int n_heads, n_kv_heads, head_dim, rot_dim, rope_mode;
     float theta, eps;
     int lin_k_heads, lin_v_heads, lin_dim;
+    int conv_kernel;             /* DeltaNet conv1d width (qwen3_5.h: 4); used with projections */
 } anelm_hybrid_dims;
 
 typedef struct anelm_hybrid_step anelm_hybrid_step;
@@ -381,8 +438,9 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          replays like GRAPH when combined with
  *                          ANELM_STEP_STATIC.  Supported for hidden/inter
  *                          sizes that tile over the device's compute units
- *                          (the Qwen3.5-4B shape on 256 CUs); other shapes
- *                          return ANELM_EINVAL from create. */
+ *                          (the Qwen3.5-4B shape on 256 CUs) and layers
+ *                          without projections (first_w NULL); other
+ *                          shapes return ANELM_EINVAL from create. */
 #define ANELM_STEP_EAGER 0
 #define ANELM_STEP_GRAPH 1
 #define ANELM_STEP_PERSISTENT 2

@@ -574,3 +574,71 @@ int orc_argmax(const float* logits, int n) {
     for (int i = 1; i < n; i++) if (logits[i] > logits[m]) m = i;
     return m;
 }
+
+/* models/llm/qwen3_5.cpp:849-908 (forward_deltanet_from_proj, norm-fused
+ * first-projection layout, :853-860): proj = [mixed_qkv | z | a | b] with
+ * mixed_qkv = 2*Hk*dk + Hv*dv channels, z [Hv][dv], a, b [Hv].
+ * conv1d_update over mixed_qkv with the layer's ring state (:867-868), SiLU
+ * (:869, silu_vec_inplace), the Q | K | V split (:872-874), then the per-head
+ * recurrence and the gated norm of orc_deltanet_decode (:876-908). */
+void orc_deltanet_from_proj(float* y, float* state, float* conv_state, int* conv_pos,
+                            const float* proj, const float* conv_w, const float* A,
+                            const float* dt_bias, const float* norm_w,
+                            int Hk, int Hv, int dk, int dv, int kernel_size, int flags) {
+    int qkv = 2 * Hk * dk + Hv * dv;
+    float* co = (float*)malloc(sizeof(float) * (size_t)qkv);
+    orc_conv1d_update(co, conv_state, conv_pos, proj, conv_w, qkv, kernel_size);
+    orc_silu_vec_inplace(co, qkv);
+    const float* z = proj + qkv;
+    const float* a = z + (long)Hv * dv;
+    const float* b = a + Hv;
+    orc_deltanet_decode(y, state, co, co + (long)Hk * dk, co + 2L * Hk * dk, a, b, A, dt_bias,
+                        z, norm_w, Hk, Hv, dk, dv, flags);
+    free(co);
+}
+
+/* core/sampling.cpp:11-66 (sample_token) with the uniform draw r passed in
+ * (the reference draws it with drand48(), :55).  Penalties over the last
+ * repetition_context_size tokens of recent[0..n_recent): each distinct token
+ * in range once -- repetition penalty (divide positive / multiply
+ * non-positive logits) if > 1, then minus frequency_penalty * count if > 0
+ * (:18-44).  temperature <= 0: first index of the maximum (:46-53).  Else
+ * logits * (1/T), softmax, and the first index whose running fp32 sum reaches
+ * r; vocab-1 if none (:55-66).  `adjusted` receives the penalised (and, with
+ * sampling, softmax) values. */
+int orc_sample_token(float* adjusted, const float* logits, int vocab, const int32_t* recent,
+                     int n_recent, float temperature, float repetition_penalty,
+                     int repetition_context_size, float frequency_penalty, float r) {
+    memcpy(adjusted, logits, sizeof(float) * (size_t)vocab);
+    if (n_recent > 0) {
+        int start = n_recent - repetition_context_size;
+        if (start < 0) start = 0;
+        for (int j = start; j < n_recent; j++) {
+            int tok = recent[j];
+            if (tok < 0 || tok >= vocab) continue;
+            int seen = 0, count = 0;
+            for (int i = start; i < n_recent; i++) {
+                if (recent[i] == tok) {
+                    if (i < j) seen = 1;
+                    count++;
+                }
+            }
+            if (seen) continue;   /* one adjustment per distinct token */
+            if (repetition_penalty > 1.0f) {
+                if (adjusted[tok] > 0.0f) adjusted[tok] = adjusted[tok] / repetition_penalty;
+                else adjusted[tok] = adjusted[tok] * repetition_penalty;
+            }
+            if (frequency_penalty > 0.0f) adjusted[tok] = adjusted[tok] - frequency_penalty * (float)count;
+        }
+    }
+    if (temperature <= 0.0f) return orc_argmax(adjusted, vocab);
+    float inv_t = 1.0f / temperature;
+    for (int i = 0; i < vocab; i++) adjusted[i] = adjusted[i] * inv_t;
+    orc_softmax(adjusted, vocab);
+    float cum = 0.0f;
+    for (int i = 0; i < vocab; i++) {
+        cum += adjusted[i];
+        if (cum >= r) return i;
+    }
+    return vocab - 1;
+}

@@ -105,6 +105,19 @@ void orc_lut6_ffn(float* y, const uint8_t* gate_w, const uint16_t* gate_lut,
 void orc_topk(int32_t* idx, float* val, const float* logits, long n, int k);
 int  orc_argmax(const float* logits, int n);
 
+/* models/llm/qwen3_5.cpp:849-908: conv1d ring + SiLU + split of the norm-fused
+ * first projection proj = [mixed_qkv | z | a | b], then orc_deltanet_decode.
+ * conv_state [2*Hk*dk + Hv*dv][kernel_size-1] and *conv_pos advance. */
+void orc_deltanet_from_proj(float* y, float* state, float* conv_state, int* conv_pos,
+                            const float* proj, const float* conv_w, const float* A,
+                            const float* dt_bias, const float* norm_w,
+                            int Hk, int Hv, int dk, int dv, int kernel_size, int flags);
+
+/* core/sampling.cpp:11-66 with the uniform draw r given; returns the token. */
+int orc_sample_token(float* adjusted, const float* logits, int vocab, const int32_t* recent,
+                     int n_recent, float temperature, float repetition_penalty,
+                     int repetition_context_size, float frequency_penalty, float r);
+
 #ifdef __cplusplus
 }
 #endif

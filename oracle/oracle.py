@@ -51,6 +51,8 @@ _SIGS = {
     "orc_lut6_ffn": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "orc_topk": (None, [_P, _P, _P, _L, _I]),
     "orc_argmax": (_I, [_P, _I]),
+    "orc_deltanet_from_proj": (None, [_P, _P, _P, _IP, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+    "orc_sample_token": (_I, [_P, _P, _I, _P, _I, _F, _F, _I, _F, _F]),
 }
 
 _lib = None
@@ -340,3 +342,32 @@ def topk(logits, k):
 def argmax(logits):
     logits = _f32(logits)
     return int(lib().orc_argmax(_p(logits), logits.size))
+
+
+def deltanet_from_proj(state, conv_state, conv_pos, proj, conv_w, A, dt_bias, norm_w, Hk, Hv,
+                       kernel_size, flags):
+    """orc_deltanet_from_proj (qwen3_5.cpp:849-908) on copies.
+    Returns (y, state, conv_state, conv_pos)."""
+    S = _f32(state).copy()
+    cs = _f32(conv_state).copy()
+    dk, dv = S.shape[1], S.shape[2]
+    y = np.empty((Hv, dv), np.float32)
+    pos = ctypes.c_int(conv_pos)
+    nw = None if norm_w is None else _f32(norm_w)
+    lib().orc_deltanet_from_proj(_p(y), _p(S), _p(cs), ctypes.byref(pos), _p(_f32(proj)), _p(_f32(conv_w)),
+                                 _p(_f32(A)), _p(_f32(dt_bias)), _p(nw), Hk, Hv, dk, dv, kernel_size,
+                                 flags)
+    return y, S, cs, pos.value
+
+
+def sample_token(logits, recent, temperature, repetition_penalty, repetition_context_size,
+                 frequency_penalty, r):
+    """orc_sample_token (core/sampling.cpp:11-66, draw r given).
+    Returns (token, adjusted values)."""
+    lg = _f32(logits)
+    adj = np.empty_like(lg)
+    rec = np.ascontiguousarray(recent, np.int32)
+    tok = lib().orc_sample_token(_p(adj), _p(lg), lg.size, _p(rec) if rec.size else None, rec.size,
+                                 temperature, repetition_penalty, repetition_context_size,
+                                 frequency_penalty, r)
+    return int(tok), adj

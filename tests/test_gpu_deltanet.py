@@ -138,3 +138,38 @@ def test_deltanet_prefill_rejects_other_chunks(anelm, dev):
     with pytest.raises(anelm.AnelmError):
         anelm.ops.deltanet_prefill(d["state"], d["q"], d["k"], d["v"], d["a"], d["b"], d["A"],
                                    d["dt_bias"], 1, chunk=32)
+
+
+@pytest.mark.parametrize("Hk,Hv,flags", [
+    (16, 32, 5),      # 4B layer as the model runs it: l2 norm, gated norm, 2 value heads per key head
+    (16, 16, 5),      # 0.8B layer (one value head per key head)
+    (4, 16, 1),       # ungated: 4 column slabs x 4 value heads read each key head's ring
+    (16, 32, 7),      # transformers order
+])
+def test_deltanet_decode_from_proj(anelm, orc, dev, Hk, Hv, flags):
+    """Conv ring + SiLU + split + recurrence from the raw first projection
+    (qwen3_5.cpp:849-908), six steps in a row so the ring position cycles
+    twice; outputs, states and the conv ring are compared every step."""
+    import ctypes
+    rng = np.random.default_rng(700 + Hk + Hv + flags)
+    d, K = 128, 4
+    qkv = 2 * Hk * d + Hv * d
+    S = (0.1 * rng.standard_normal((Hv, d, d))).astype(np.float32)
+    conv_w = (0.5 * rng.standard_normal((qkv, K))).astype(np.float32)
+    cs = (0.5 * rng.standard_normal((qkv, K - 1))).astype(np.float32)
+    A = np.exp(rng.uniform(0, np.log(16), Hv)).astype(np.float32)
+    dtb = rng.standard_normal(Hv).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    Sd, csd = to_dev(S, dev), to_dev(cs, dev)
+    cwd, Ad, dtd, nwd = (to_dev(a, dev) for a in (conv_w, A, dtb, nw))
+    pos_ref, pos_gpu = 1, ctypes.c_int(1)
+    for t in range(6):
+        proj = rng.standard_normal(qkv + Hv * d + 2 * Hv).astype(np.float32)
+        y = anelm.ops.deltanet_decode_from_proj(Sd, csd, pos_gpu, to_dev(proj, dev), cwd, Ad, dtd,
+                                                nwd if flags & 4 else None, Hk, flags, K)
+        yw, S, cs, pos_ref = orc.deltanet_from_proj(S, cs, pos_ref, proj, conv_w, A, dtb, nw, Hk, Hv,
+                                                    K, flags)
+        assert pos_gpu.value == pos_ref
+        assert_close(to_host(y), yw, what=f"y step {t}")
+        assert_close(to_host(Sd), S, what=f"state step {t}")
+        assert np.array_equal(to_host(csd), cs), f"conv ring step {t}"

@@ -242,3 +242,28 @@ def test_topk_ties_prefer_lower_index(anelm, orc, dev):
         assert idx[0] == min(top, twin)
         if k > 1:
             assert idx[1] == max(top, twin) and val[0] == val[1]
+
+
+@pytest.mark.parametrize("out_dim,in_dim,norm,acc", [
+    (12352, 2560, True, False),     # DeltaNet first projection (qkv | z | a | b) at the 4B shape
+    (10240, 2560, True, False),     # attention first projection (q_gate | k | v)
+    (2560, 4096, False, True),      # o_proj with the residual add
+    (8224, 1024, True, False),      # 0.8B-like DeltaNet first projection with 16/16 heads
+    (1024, 2048, False, True),
+])
+def test_layer_projections(anelm, orc, dev, out_dim, in_dim, norm, acc):
+    """The projections around the cores (qwen3_5.cpp:1287-1327) at the model
+    shapes: first_proj of the RMS-normalised x, o_proj accumulated onto x."""
+    packed, lut, _ = lut6_matrix(660 + out_dim, out_dim, in_dim)
+    rng = np.random.default_rng(661 + in_dim)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(in_dim)).astype(np.float32) if norm else None
+    y0 = rng.standard_normal(out_dim).astype(np.float32)
+    yd = to_dev(y0, dev)
+    anelm.ops.lut6_proj(to_dev(packed, dev), to_dev(lut, dev), to_dev(x, dev), out_dim, in_dim,
+                        norm_w=None if w is None else to_dev(w, dev), y=yd, accumulate=acc)
+    n = orc.rmsnorm(x, w, 1e-6) if norm else x
+    want = orc.lut6_matvec(packed, lut, n, out_dim, in_dim)
+    if acc:
+        want = y0 + want
+    assert_close(to_host(yd), want, what=f"{out_dim}x{in_dim}")
