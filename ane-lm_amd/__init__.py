@@ -26,6 +26,8 @@ ROPE_HALF_SPLIT = 1
 DN_L2NORM = 1
 DN_ORDER_TRANSFORMERS = 2
 DN_GATED_NORM = 4
+KV_TOKEN_MAJOR = 0
+KV_HEAD_MAJOR = 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -50,6 +52,8 @@ SIGNATURES = {
     "anelm_gqa_attention": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "anelm_full_attn_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F,
                                _I, _I, _FP, _FP, _IP, _IP, _I, _P],
+    "anelm_full_attn_decode_kv": [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _F, _F,
+                                  _I, _I, _FP, _FP, _IP, _IP, _I, _P],
     "anelm_full_attn_decode_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F,
                                        _I, _I, _FP, _FP, _IP, _IP, _I, _P],
     "anelm_attn_decode_paged": [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],

@@ -96,6 +96,13 @@ int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const
                           int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
                           int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
 size_t full_attn_part_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
+// The same over either cache element type (ANELM_F16 / ANELM_F32) and layout
+// (ANELM_KV_TOKEN_MAJOR / ANELM_KV_HEAD_MAJOR).
+int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, const float* v, void* k_cache,
+                             void* v_cache, int kv_dtype, int layout, const float* q_norm_w, const float* k_norm_w,
+                             int n_heads, int n_kv_heads, int head_dim, int rot_dim, int pos, float theta, float eps,
+                             int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                             int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
 
 // `n` zeroed counters on the current device; nullptr if n exceeds the pool.
 uint32_t* counters(size_t n);

@@ -30,6 +30,10 @@ struct DecodeParams {
     const void* v_cache;
     int n_kv_heads;
     int start, len, cap;       // ring mode
+    // ring mode: element offsets of consecutive slots and of consecutive kv
+    // heads -- token-major [cap][Hkv][D] (Hkv*D, D) or head-major
+    // [Hkv][cap][D] (D, cap*D)
+    long tok_stride, head_stride;
     float scale;
     int kps, max_splits;
     float* part;       // partials [seq][Hkv][max_splits][G][D+2]: m, l, o[D]
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     constexpr int KPS = KPB * KB;     // keys per split (= 256 / G)
     const int t0 = split * KPS;
     const int nk = min(KPS, sv.len - t0);
-    const size_t tok_stride = (size_t)Hkv * D;
+    const size_t tok_stride = (size_t)p.tok_stride, head_off = (size_t)kvh * p.head_stride;
     const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
     const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
     const bool owner = p.fused && split == sv.n_splits - 1;   // holds the newest key
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         }
         int phys = p.start + lt;
         if (phys >= p.cap) phys -= p.cap;
-        return base + (size_t)phys * tok_stride + (size_t)kvh * D + dl * 8;
+        return base + (size_t)phys * tok_stride + head_off + dl * 8;
     };
     Raw8<KV> rk[KB], rv[KB];
 #pragma unroll
@@ -271,8 +275,8 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
             for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
             __syncthreads();
             norm_rope_row<D>(kn_s, p.k_norm_w, p, red, p.cs, p.sn);
-            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
-            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + (size_t)kvh * D;
+            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
+            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
             for (int d = tid; d < D; d += kNT) {
                 store_kv(kw + d, kn_s[d]);
                 store_kv(vw + d, p.v_new[(size_t)kvh * D + d]);
@@ -816,6 +820,10 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
     p.kps = kps;
     p.max_splits = max_splits;
     p.n_seqs = n_seqs;
+    if (p.tok_stride == 0) {   // token-major ring
+        p.tok_stride = (long)Hkv * D;
+        p.head_stride = D;
+    }
     const size_t need = part_bytes(n_heads, Hkv, D, n_seqs, max_len, p.paged != 0);
     if (need > 0 && part != nullptr) {
         if (need > part_cap)
@@ -905,6 +913,21 @@ int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const
                           int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
                           int* cache_len, int cache_capacity, hipStream_t stream, float* part,
                           size_t part_cap) {
+    return full_attn_decode_kv_impl(out, q_gate, k, v, k_cache, v_cache, ANELM_F16, ANELM_KV_TOKEN_MAJOR, q_norm_w,
+                                    k_norm_w, n_heads, n_kv_heads, head_dim, rot_dim, pos, theta, eps, rope_mode,
+                                    gate, cos_row, sin_row, cache_start, cache_len, cache_capacity, stream, part,
+                                    part_cap);
+}
+
+int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, const float* v, void* k_cache,
+                             void* v_cache, int kv_dtype, int layout, const float* q_norm_w, const float* k_norm_w,
+                             int n_heads, int n_kv_heads, int head_dim, int rot_dim, int pos, float theta, float eps,
+                             int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                             int* cache_len, int cache_capacity, hipStream_t stream, float* part,
+                             size_t part_cap) {
+    ANELM_REQUIRE(kv_dtype == ANELM_F16 || kv_dtype == ANELM_F32, "kv_dtype %d unknown", kv_dtype);
+    ANELM_REQUIRE(layout == ANELM_KV_TOKEN_MAJOR || layout == ANELM_KV_HEAD_MAJOR, "cache layout %d unknown",
+                  layout);
     ANELM_NONNULL(out);
     ANELM_NONNULL(q_gate);
     ANELM_NONNULL(k);
@@ -947,6 +970,10 @@ int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const
     p.start = start;
     p.len = len;
     p.cap = cache_capacity;
+    if (layout == ANELM_KV_HEAD_MAJOR) {
+        p.tok_stride = head_dim;
+        p.head_stride = (long)cache_capacity * head_dim;
+    }
     p.scale = 1.0f / sqrtf((float)head_dim);
     p.fused = 1;
     p.q_norm_w = q_norm_w;
@@ -965,7 +992,7 @@ int full_attn_decode_impl(float* out, const float* q_gate, const float* k, const
     } else {
         rope_row(p.cs, p.sn, rot_dim, pos, theta);
     }
-    rc = run_decode(p, ANELM_F16, n_heads, head_dim, 1, len, stream, part, part_cap);
+    rc = run_decode(p, kv_dtype, n_heads, head_dim, 1, len, stream, part, part_cap);
     if (rc == ANELM_OK) {
         *cache_start = start;
         *cache_len = len;
@@ -990,6 +1017,18 @@ extern "C" int anelm_full_attn_decode(float* out, const float* q_gate, const flo
     return full_attn_decode_impl(out, q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, n_heads, n_kv_heads,
                                  head_dim, rot_dim, pos, theta, eps, rope_mode, gate, cos_row, sin_row,
                                  cache_start, cache_len, cache_capacity, as_stream(stream), nullptr, 0);
+}
+
+extern "C" int anelm_full_attn_decode_kv(float* out, const float* q_gate, const float* k, const float* v,
+                                         void* k_cache, void* v_cache, int kv_dtype, int layout,
+                                         const float* q_norm_w, const float* k_norm_w, int n_heads, int n_kv_heads,
+                                         int head_dim, int rot_dim, int pos, float theta, float eps, int rope_mode,
+                                         int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                                         int* cache_len, int cache_capacity, void* stream) {
+    return full_attn_decode_kv_impl(out, q_gate, k, v, k_cache, v_cache, kv_dtype, layout, q_norm_w, k_norm_w,
+                                    n_heads, n_kv_heads, head_dim, rot_dim, pos, theta, eps, rope_mode, gate,
+                                    cos_row, sin_row, cache_start, cache_len, cache_capacity, as_stream(stream),
+                                    nullptr, 0);
 }
 
 extern "C" int anelm_attn_decode_paged(float* out, const float* q, int q_head_stride,

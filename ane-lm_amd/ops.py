@@ -143,6 +143,22 @@ def full_attn_decode(q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, ring: K
     return out
 
 
+def full_attn_decode_kv(q_gate, k, v, k_cache, v_cache, layout, q_norm_w, k_norm_w, ring: KVRing,
+                        n_heads, n_kv_heads, head_dim, rot_dim, pos, theta=1e7, eps=1e-6,
+                        rope_mode=ROPE_INTERLEAVED, gate=True, cos_row=None, sin_row=None, out=None):
+    """full_attn_decode over an fp16 or fp32 cache, token-major (layout 0) or
+    head-major [Hkv][cap][D] (layout 1)."""
+    kv_dtype = ANELM_F16 if k_cache.dtype == _F16 else ANELM_F32
+    out = torch.empty(n_heads, head_dim, device=q_gate.device, dtype=_F32) if out is None else out
+    c = _floats(cos_row)
+    s = _floats(sin_row)
+    call("anelm_full_attn_decode_kv", _p(out), _p(q_gate), _p(k), _p(v), _p(k_cache), _p(v_cache), kv_dtype,
+         layout, _p(q_norm_w), _p(k_norm_w), n_heads, n_kv_heads, head_dim, rot_dim, pos, theta, eps,
+         rope_mode, 1 if gate else 0, c[0] if c else None, s[0] if s else None,
+         ctypes.byref(ring.start), ctypes.byref(ring.len), ring.capacity, _s())
+    return out
+
+
 def attn_decode_paged(q, k_pages, v_pages, page_table, seq_lens, max_seq_len, n_heads,
                       n_kv_heads, head_dim, page_size, q_head_stride=None, out=None):
     n_seqs = seq_lens.numel()

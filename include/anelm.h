@@ -45,6 +45,12 @@ enum {
 #define ANELM_F32 0
 #define ANELM_F16 1
 
+/* KV cache layouts: the reference's token-major ring [capacity][Hkv][D]
+ * (models/llm/qwen3_5.cpp:335-336) and the head-major cache [Hkv][ctx][D] of
+ * scripts/serve_hybrid.py:232-235. */
+#define ANELM_KV_TOKEN_MAJOR 0
+#define ANELM_KV_HEAD_MAJOR 1
+
 const char* anelm_last_error(void);
 int anelm_version(void);
 /* Number of compute units of the current device (0 on error). */
@@ -123,6 +129,20 @@ int anelm_full_attn_decode(float* out, const float* q_gate, const float* k, cons
                            int pos, float theta, float eps, int rope_mode, int gate,
                            const float* cos_row, const float* sin_row,
                            int* cache_start, int* cache_len, int cache_capacity, void* stream);
+
+/* anelm_full_attn_decode over a cache of element type kv_dtype (ANELM_F16 or
+ * ANELM_F32, the reference's fp32 cache) and layout ANELM_KV_TOKEN_MAJOR or
+ * ANELM_KV_HEAD_MAJOR.  With q_norm_w = k_norm_w = NULL, rope_mode
+ * ANELM_ROPE_HALF_SPLIT, a head-major fp32 cache, cache_start 0 and
+ * cache_len = pos this is scripts/serve_hybrid.py:85-132 (cpu_attention):
+ * RoPE at pos, k and v written at slot pos, attention over keys 0..pos,
+ * sigmoid gate. */
+int anelm_full_attn_decode_kv(float* out, const float* q_gate, const float* k, const float* v,
+                              void* k_cache, void* v_cache, int kv_dtype, int layout,
+                              const float* q_norm_w, const float* k_norm_w, int n_heads, int n_kv_heads,
+                              int head_dim, int rot_dim, int pos, float theta, float eps, int rope_mode,
+                              int gate, const float* cos_row, const float* sin_row, int* cache_start,
+                              int* cache_len, int cache_capacity, void* stream);
 
 /* anelm_full_attn_decode without any device allocation, for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,

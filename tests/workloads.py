@@ -527,3 +527,27 @@ class OracleBatch:
             self.x = (self.x + orc.lut6_ffn_batch(n, (gu[:I], gl[:I // 32]), (gu[I:], gl[I // 32:]),
                                                   (L["down_w"], L["down_lut"]), H, I)).astype(np.float32)
         return outs
+
+
+# ------------------------------------------- serve_hybrid.py CPU attention
+def oracle_serve_attention(orc, q_gate16, k16, v16, pos, k_cache, v_cache, cos_row, sin_row,
+                           Hq=16, Hkv=4, D=256, rot=64, kv_f16=False):
+    """scripts/serve_hybrid.py:85-132 (cpu_attention) as a composition of the
+    oracle's cpu_ops functions: widen the fp16 inputs; half-split RoPE of the
+    query half of each q_gate row and of k with the given cos/sin row
+    (:91-103); k, v into the head-major caches [Hkv][ctx][D] at slot pos
+    (:105-106); attention over keys 0..pos (:108-126) -- gqa_attention over
+    the token-major view of the caches; the sigmoid gate (:128-130); fp16
+    result [1][Hq*D].  Updates k_cache / v_cache (fp32 numpy) in place; with
+    kv_f16 the appended rows are stored rounded to fp16 (an fp16 cache)."""
+    qg = widen(np.ascontiguousarray(q_gate16, np.uint16)).reshape(Hq, 2 * D)
+    k = widen(np.ascontiguousarray(k16, np.uint16)).reshape(Hkv, D)
+    v = widen(np.ascontiguousarray(v16, np.uint16)).reshape(Hkv, D)
+    qg, k = orc.apply_rope(qg, k, Hq, Hkv, D, 2 * D, D, rot, pos, 1e7, cos_row, sin_row, 1)
+    k_cache[:, pos, :] = widen(f16(k)) if kv_f16 else k
+    v_cache[:, pos, :] = widen(f16(v)) if kv_f16 else v
+    kc = np.ascontiguousarray(k_cache[:, :pos + 1, :].transpose(1, 0, 2))
+    vc = np.ascontiguousarray(v_cache[:, :pos + 1, :].transpose(1, 0, 2))
+    out = orc.gqa_attention(qg, kc, vc, Hq, Hkv, D, 2 * D, 0, pos + 1, pos + 1)
+    out = orc.mul_sigmoid(out, qg[:, D:])
+    return f16(out.reshape(1, Hq * D))
