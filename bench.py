@@ -68,8 +68,32 @@ def gateup_bytes(c=CFG):
     return 2 * (I * H * 3 // 4 + (I // 32) * 64 * 2) + 2 * H * 4 + 2 * I * 4
 
 
-def build_step(anelm, torch, dev, seed=0, mode=None):
-    """Allocates the synthetic 4B-shaped model state and returns (step, keep, x)."""
+def proj_bytes(c=CFG):
+    """Algorithmic bytes the projections around the cores add to a step: the
+    LUT6 first projections (DeltaNet 2560 -> 12352: qkv | z | a | b;
+    attention 2560 -> 10240: q_gate | k | v), o_proj 4096 -> 2560, their LUTs,
+    the input norm weights and the DeltaNet conv rings (read + write) and
+    conv weights."""
+    n_attn = c["layers"] // 4
+    n_dn = c["layers"] - n_attn
+    H = c["hidden"]
+    f_dn = 2 * c["lin_k_heads"] * 128 + 2 * c["lin_v_heads"] * 128 + 2 * c["lin_v_heads"]
+    f_at = c["n_heads"] * 2 * c["head_dim"] + 2 * c["n_kv_heads"] * c["head_dim"]
+    o_in = c["n_heads"] * c["head_dim"]
+    qkv = 2 * c["lin_k_heads"] * 128 + c["lin_v_heads"] * 128
+
+    def lut6(out, inp):
+        return out * inp * 3 // 4 + (out // 32) * 128
+
+    w = n_dn * lut6(f_dn, H) + n_attn * lut6(f_at, H) + c["layers"] * (lut6(H, o_in) + H * 4)
+    conv = n_dn * qkv * (3 * 4 * 2 + 4 * 4)
+    return w + conv
+
+
+def build_step(anelm, torch, dev, seed=0, mode=None, proj=False):
+    """Allocates the synthetic 4B-shaped model state and returns (step, keep, x).
+    With proj, every layer also carries its projections (input norm + first
+    projection, DeltaNet conv ring, o_proj) and the step runs whole layers."""
     c = CFG
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -123,13 +147,26 @@ def build_step(anelm, torch, dev, seed=0, mode=None):
         t["up_lut"] = lut(I)
         t["down_w"] = randbytes(H, I * 3 // 4)
         t["down_lut"] = lut(H)
+        if proj:
+            attn = (i + 1) % 4 == 0
+            f_out = Hq * 2 * D + 2 * Hkv * D if attn else 2 * Hk * dl + 2 * Hv * dl + 2 * Hv
+            t["in_norm_w"] = 1 + randn(H, std=0.02)
+            t["first_w"] = randbytes(f_out, H * 3 // 4)
+            t["first_lut"] = lut(f_out)
+            t["o_w"] = randbytes(H, (Hq * D if attn else Hv * dl) * 3 // 4)
+            t["o_lut"] = lut(H)
+            t["proj"] = torch.empty(f_out, device=dev)
+            if not attn:
+                qkv = 2 * Hk * dl + Hv * dl
+                t["conv_state"] = randn(qkv, 3, std=0.5)
+                t["conv_w"] = randn(qkv, 4, std=0.5)
         for name, ten in t.items():
             setattr(L, name, ten.data_ptr())
         keep.append(t)
     x = randn(H)
     h = torch.empty(2 * I, device=dev)
     keep.append({"x": x, "h": h})
-    dims = anelm.HybridDims(H, I, Hq, Hkv, D, c["rot_dim"], 0, c["theta"], c["eps"], Hk, Hv, dl)
+    dims = anelm.HybridDims(H, I, Hq, Hkv, D, c["rot_dim"], 0, c["theta"], c["eps"], Hk, Hv, dl, 4)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     modes = [mode] if mode is not None else [anelm.STEP_PERSISTENT | anelm.STEP_STATIC, anelm.STEP_GRAPH]
@@ -443,6 +480,101 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
     return r
 
 
+def measure_complete_step(anelm, torch, dev, reps=20):
+    """The same 32-layer step with the projections around the cores inside
+    (qwen3_5.cpp:1287-1354 per layer: input norm + LUT6 first projection, the
+    DeltaNet conv ring, the core, o_proj + residual, the FFN), as a HIP-graph
+    replay of the per-layer launches."""
+    handle, keep, x, mode = build_step(anelm, torch, dev, seed=3, mode=anelm.STEP_GRAPH, proj=True)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        anelm.call("anelm_hybrid_step_run", handle, s)
+    us = _gpu_us(torch, lambda: anelm.call("anelm_hybrid_step_run", handle, s), reps, warm=0)
+    assert torch.isfinite(x).all(), "non-finite hidden state (complete step)"
+    anelm.call("anelm_hybrid_step_destroy", handle)
+    del keep
+    nbytes = step_bytes()["total"] + proj_bytes()
+    r = _hbm(us, nbytes)
+    r["execution"] = "hip graph replay of the per-layer launches"
+    r["composition"] = ("per layer: input norm + LUT6 first projection (2560->12352 DeltaNet, 2560->10240 "
+                        "attention), conv ring + DeltaNet core or attention core, LUT6 o_proj 4096->2560 + "
+                        "residual, LUT6 SwiGLU FFN")
+    return r
+
+
+def cpu_baselines_per_config(seconds=1.0):
+    """The oracle (single-threaded C restatement of cpu_ops) on each other
+    workload, each on a bounded sample of about `seconds`:
+    C1 one 0.8B-shaped attention decode over 513 keys; C2 one 16-head DeltaNet
+    step; C3a causal prefill at 4096 tokens from the last 16 rows (cost per
+    (row, key) pair x S(S+1)/2); C3b chunked-DeltaNet prefill from a 128-token
+    prefix (x 32: the recurrence is sequential per token); C5 the 32-sequence
+    step composed from timed units (attention per cached key, one 32-head
+    DeltaNet step, one FFN block, one 8192-row LM-head slice) over the drawn
+    lengths."""
+    import numpy as np
+    from workloads import attn_decode_case, deltanet_case, load_oracle, lut6_matrix, prefill_inputs
+    orc = load_oracle()
+    orc.use_timing_build()
+
+    def med(fn):
+        fn()
+        ts = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(ts) < 3:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e6, len(ts)
+
+    res = {}
+    c = attn_decode_case(11)
+    kc32 = np.ascontiguousarray(c.k_cache[:c.length + 1].astype(np.float32))   # the reference's fp32 ring
+    vc32 = np.ascontiguousarray(c.v_cache[:c.length + 1].astype(np.float32))
+    qg = c.q_gate.reshape(8, 2, 256)
+
+    def c1():   # qwen3_5.cpp:944-1002 on an fp32 ring of 513 keys
+        qn = orc.rmsnorm(qg[:, 0], c.q_norm_w)
+        kn = orc.rmsnorm(c.k, c.k_norm_w)
+        qn, kn = orc.apply_rope(qn, kn, 8, 2, 256, 256, 256, 64, c.pos, c.theta)
+        kc32[c.length] = kn
+        o = orc.gqa_attention(qn, kc32, vc32, 8, 2, 256, 256, 0, c.length + 1, c.length + 1)
+        return orc.mul_sigmoid(o, qg[:, 1])
+    us, n = med(c1)
+    res["decode_attention_0.8b"] = {"us": round(us, 1), "sample": f"median of {n} calls (fp32 ring, 513 keys)"}
+    d = deltanet_case(12, Hk=16, Hv=16)
+    us, n = med(lambda: orc.deltanet_decode(d.state, d.q, d.k, d.v, d.a, d.b, d.A, d.dt_bias, 0))
+    res["deltanet_decode"] = {"us": round(us, 1), "sample": f"median of {n} calls"}
+    S = 4096
+    q, k, v = prefill_inputs(13, S, 16, 4, 256)
+    us, n = med(lambda: orc.prefill_attention(q, k, v, S - 16, S))
+    pairs = sum(t + 1 for t in range(S - 16, S))
+    res["prefill_attention_4096"] = {"us": round(us / pairs * S * (S + 1) / 2, 1),
+                                     "sample": f"rows {S - 16}..{S - 1} (median of {n}), x S(S+1)/2 pairs"}
+    d = deltanet_case(14, Hk=16, Hv=32, S=128)
+    us, n = med(lambda: orc.deltanet_prefill(d.state, d.q, d.k, d.v, d.a, d.b, d.A, d.dt_bias, 1))
+    res["deltanet_prefill_4096"] = {"us": round(us * S / 128, 1), "sample": f"128 tokens (median of {n}) x 32"}
+    # C5 units
+    L0 = 4096
+    kc = np.random.default_rng(15).standard_normal((L0, 4, 256)).astype(np.float32)
+    qq = np.random.default_rng(16).standard_normal((16, 512)).astype(np.float32)
+    u_key, _ = med(lambda: orc.gqa_attention(qq, kc, kc, 16, 4, 256, 512, 0, L0, L0))
+    d = deltanet_case(17, Hk=16, Hv=32)
+    u_dn, _ = med(lambda: orc.deltanet_decode(d.state, d.q, d.k, d.v, d.a, d.b, d.A, d.dt_bias, 5, d.z, d.norm_w))
+    g, u, dn = lut6_matrix(18, 9216, 2560), lut6_matrix(19, 9216, 2560), lut6_matrix(20, 2560, 9216)
+    xx = np.random.default_rng(21).standard_normal(2560).astype(np.float32)
+    u_ffn, _ = med(lambda: orc.lut6_ffn(xx, g[:2], u[:2], dn[:2], 2560, 9216))
+    lm = lut6_matrix(22, 8192, 2560)
+    u_lm, _ = med(lambda: orc.lut6_matvec(lm[0], lm[1], xx, 8192, 2560))
+    lens = np.random.default_rng(12).integers(256, 16385, 32)   # the GPU step's draw
+    step = (8 * u_key / L0 * float(lens.sum()) + 24 * 32 * u_dn + 32 * 32 * u_ffn + 32 * (262144 / 8192) * u_lm)
+    res["batch32_decode_step"] = {"us": round(step, 1),
+                                  "sample": "units timed (attention over 4096 fp32 keys, 32-head DeltaNet step, "
+                                            "one FFN block, 8192-row LM-head slice), composed over the drawn "
+                                            "lengths x 32 sequences x 32 layers"}
+    return res
+
+
 def cpu_baseline(seconds=12.0):
     """The oracle (a single-threaded C restatement of the reference cpu_ops
     path) on a bounded sample of the same step: one block of four layers
@@ -452,6 +584,7 @@ def cpu_baseline(seconds=12.0):
     import numpy as np
     from workloads import load_oracle
     orc = load_oracle()
+    orc.use_timing_build()
     c = CFG
     rng = np.random.default_rng(7)
     H, I, D, ctx = c["hidden"], c["inter"], c["head_dim"], c["ctx"]
@@ -505,7 +638,8 @@ def cpu_baseline(seconds=12.0):
     return {"value": round(per_step_us, 1), "unit": "us/step", "cores": 1, "kind": "port",
             "sample": f"{len(reps)} runs of one 4-layer block (1 attention over 8192 fp32 keys, "
                       f"3 DeltaNet, 4 LUT6 FFN as dequant+matvec), median x8 layers-blocks; "
-                      f"oracle/anelm_oracle.c, 1 thread, {cpu_model}, nproc {os.cpu_count()}"}
+                      f"oracle/anelm_oracle.c built -O3 -march=x86-64-v3 with vectorised reductions "
+                      f"(liboracle_timing.so), 1 thread, {cpu_model}, nproc {os.cpu_count()}"}
 
 
 def main():
@@ -573,6 +707,8 @@ def main():
         if cores is not None:
             torch.cuda.empty_cache()
             cores["batch32_decode_step"] = measure_batch32_step(anelm, torch, dev)
+            torch.cuda.empty_cache()
+            cores["complete_step_graph"] = measure_complete_step(anelm, torch, dev)
 
     b = step_bytes()
     gbps = b["total"] / (us_step * 1e-6) / 1e9
@@ -620,6 +756,13 @@ def main():
         result["cores"] = cores
     if not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if cores is not None:
+            # the same oracle, one thread, beside each other workload's GPU time
+            per = cpu_baselines_per_config()
+            for name, v in per.items():
+                if name in cores:
+                    cores[name]["cpu_us"] = v["us"]
+                    cores[name]["cpu_sample"] = v["sample"]
     print(json.dumps(result))
 
 

@@ -56,6 +56,17 @@ _SIGS = {
 }
 
 _lib = None
+TIMING_LIB_PATH = os.path.join(_HERE, "liboracle_timing.so")
+
+
+def use_timing_build() -> None:
+    """Switches this module to liboracle_timing.so: the same C sources built
+    with vectorised (reassociated) reductions, for the CPU-baseline timing in
+    bench.py only -- never for checking results."""
+    global _lib, LIB_PATH
+    LIB_PATH = TIMING_LIB_PATH
+    _lib = None
+    lib()
 
 
 def build() -> None:
@@ -68,7 +79,11 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            build()
+            if LIB_PATH == TIMING_LIB_PATH:
+                subprocess.run(["make", "-B", "-C", _HERE, "liboracle_timing.so"], check=True,
+                               stdout=subprocess.DEVNULL)
+            else:
+                build()
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in _SIGS.items():
             f = getattr(L, name)
