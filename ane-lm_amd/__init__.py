@@ -81,6 +81,7 @@ SIGNATURES = {
     "anelm_hybrid_step_run": [_P, _P],
     "anelm_hybrid_step_status": [_P, _IP],
     "anelm_hybrid_step_destroy": [_P],
+    "anelm_hybrid_step_trace": [_P, _P, ctypes.c_size_t, _IP, _IP],
     "anelm_batch_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P],
     "anelm_batch_step_run": [_P, _I, _P],
     "anelm_batch_step_destroy": [_P],

@@ -124,6 +124,7 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* dims,
                       hipStream_t stream);
 int persistent_run(PersistentStep* s, bool advance, hipStream_t stream);
 int persistent_status(PersistentStep* s, int* status);
+int persistent_trace(PersistentStep* s, unsigned long long* host, size_t n_words, int* grid, int* row);
 void persistent_destroy(PersistentStep* s);
 
 // ------------------------------------------------------------- device code

@@ -199,6 +199,16 @@ extern "C" int anelm_hybrid_step_status(anelm_hybrid_step* step, int* status) {
     return step->ps ? persistent_status(step->ps, status) : ANELM_OK;
 }
 
+extern "C" int anelm_hybrid_step_trace(anelm_hybrid_step* step, uint64_t* host, size_t n_words, int* grid,
+                                       int* phases) {
+    ANELM_NONNULL(step);
+    ANELM_NONNULL(host);
+    ANELM_NONNULL(grid);
+    ANELM_NONNULL(phases);
+    ANELM_REQUIRE(step->ps != nullptr, "step trace: only the persistent step records a timeline");
+    return persistent_trace(step->ps, reinterpret_cast<unsigned long long*>(host), n_words, grid, phases);
+}
+
 extern "C" int anelm_hybrid_step_destroy(anelm_hybrid_step* step) {
     if (!step) return ANELM_OK;
     if (step->ps) persistent_destroy(step->ps);

@@ -40,6 +40,13 @@
 
 struct anelm_hybrid_step;
 
+// Phase timeline (diagnostic build only, -DANELM_STEP_TRACE=1): every
+// workgroup stamps the 100 MHz real-time clock at four events of each phase.
+// The default build compiles the stamps out.
+#ifndef ANELM_STEP_TRACE
+#define ANELM_STEP_TRACE 0
+#endif
+
 namespace anelm {
 namespace pk {
 
@@ -132,7 +139,27 @@ struct PArgs {
     int Hkv, splits, kps, rot_pairs, rope_mode, cap;
     float eps, scale;
     int Hk, Hv;
+    unsigned long long* trace;        // [grid][kMaxPhases + 1][kTrEv] (trace build), else null
 };
+
+// Trace events of phase p (p = 3*layer + {0 core, 1 gate/up, 2 down}):
+// compute start and end (compute wave 0), barrier arrival issued and release
+// observed (control wave); for the GEMV phases, compute wave 0 also stamps
+// the end of its first weight issue (X0), of the pair-table build (X1), of the
+// lookups made ahead of the input (X2) and of its second weight issue (X3).
+// Row kMaxPhases holds kernel entry and exit.
+enum : int { kTrStart = 0, kTrEnd = 1, kTrArrive = 2, kTrRelease = 3, kTrX0 = 4, kTrX1 = 5, kTrX2 = 6,
+             kTrX3 = 7, kTrEv = 8 };
+__device__ __forceinline__ void trace_stamp(const PArgs& a, int p, int ev, bool who) {
+#if ANELM_STEP_TRACE
+    if (who) {
+        const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+        a.trace[((size_t)blockIdx.x * (kMaxPhases + 1) + p) * kTrEv + ev] = t;
+    }
+#else
+    (void)a; (void)p; (void)ev; (void)who;
+#endif
+}
 
 // ------------------------------------------------------------- primitives
 __device__ __forceinline__ unsigned ld_sc(const unsigned* p) {
@@ -288,6 +315,13 @@ __device__ bool bar_wait(unsigned* sync, int p) {
     return false;
 }
 
+// An unspecified value: defines a register on a path that never reads it,
+// without tying it to a constant the allocator would have to keep.
+__device__ __forceinline__ uint32_t undef_u32() {
+    uint32_t v;
+    return __builtin_nondeterministic_value(v);
+}
+
 // Per-wave register buffer for a phase's bulk data (one type per phase kind,
 // so the allocator never has to merge buffers of different phases).
 template <int N>
@@ -328,7 +362,18 @@ template <int NI, int LO, int HI, bool LUTS>
 __device__ __forceinline__ void gemv_issue(Buf<3 * NI>& b, LutRegs& lr, const GemvGeo& q,
                                            const uint8_t* const (&W)[2], const uint16_t* const (&LUT)[2],
                                            int n_mat, int wave, int lane) {
-    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    if (wave >= n_mat * q.P || q.nrows <= 0) {
+        // defined on every path: the buffers live across layers, and an
+        // undefined path would keep the previous layer's values alive
+#pragma unroll
+        for (int m = LO; m < HI; m++) {
+            b.v[3 * m] = undef_u32();
+            b.v[3 * m + 1] = undef_u32();
+            b.v[3 * m + 2] = undef_u32();
+        }
+        if constexpr (LUTS) lr.v[0] = lr.v[1] = lr.v[2] = undef_u32();
+        return;
+    }
     const int mt = wave / q.P, wl = wave - mt * q.P;
     if constexpr (LUTS) {
         // buffer loads: generic (flat) loads would also count on the LDS wait
@@ -378,7 +423,11 @@ __device__ __forceinline__ void gemv_tables(const LutRegs& lr, const GemvGeo& q,
 template <int NI, int NA>
 __device__ __forceinline__ void gemv_decode(const Buf<3 * NI>& b, Buf<8 * NA>& d, const GemvGeo& q, int n_mat,
                                             int wave, int lane, char* lds) {
-    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    if (wave >= n_mat * q.P || q.nrows <= 0) {
+#pragma unroll
+        for (int k = 0; k < 8 * NA; k++) d.v[k] = undef_u32();
+        return;
+    }
     const int mt = wave / q.P;
 #pragma unroll
     for (int m = 0; m < NA; m++) {
@@ -470,10 +519,13 @@ constexpr int kAkOff = kLdsTab;                        // K rows [20*NKJ][256] f
 template <int NKJ>
 __device__ __forceinline__ void attn_prefetch(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, int wave,
                                               int lane, char* lds) {
-    if (wave >= kCW) return;
     const int wg = blockIdx.x;
     const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
-    if (kvh >= a.Hkv) return;
+    if (wave >= kCW || kvh >= a.Hkv) {
+#pragma unroll
+        for (int k = 0; k < 4 * NKJ; k++) b.v[k] = undef_u32();   // defined on every path (lives across layers)
+        return;
+    }
     const int hw = wave * 2 + (lane >> 5), dl = lane & 31;
     const int t0 = sp * a.kps;
     const uint32_t bytes = (uint32_t)a.cap * a.Hkv * kAttnD * 2;
@@ -822,7 +874,10 @@ constexpr int kDnCols = kDnD / kDnSlabs;     // 16
 constexpr int kDnBuf = 4;
 __device__ __forceinline__ void dn_prefetch(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane) {
     const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
-    if (hd >= a.Hv || wave >= 8) return;
+    if (hd >= a.Hv || wave >= 8) {
+        b.v[0] = b.v[1] = b.v[2] = b.v[3] = undef_u32();   // defined on every path (lives across layers)
+        return;
+    }
     const int Lg = wave * 64 + lane, r = Lg >> 2, cq = Lg & 3;
     const __amdgpu_buffer_rsrc_t rs = rsrc(L.state + (size_t)hd * kDnD * kDnD, kDnD * kDnD * 4);
     const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rs, (r * kDnD + kDnCols * c + 4 * cq) * 4, 0, 0);
@@ -894,7 +949,9 @@ __device__ __forceinline__ float sum_rows16(float v) {
 // the gated norm they go to core_out; with it the slab's sum of squares is
 // published (dnss) and the control wave returns y (lane j: column 16c + j)
 // for dn_finish after the next barrier.
-__device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds) {
+__device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds,
+                            int p) {
+    const bool tw0 = wave == 0 && lane == 0;
     const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
     const bool active = hd < a.Hv;
     const float* s = reinterpret_cast<const float*>(lds + kDqOff);
@@ -906,6 +963,10 @@ __device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int
     float yp[4] = {0.f, 0.f, 0.f, 0.f};
     float beta = 0.f, decay = 0.f, kr = 0.f;
     if (holder) {
+#if ANELM_STEP_TRACE
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // state landed (trace build only)
+#endif
+        trace_stamp(a, p, kTrX0, tw0);
         beta = s[384];
         decay = s[385];
         kr = s[128 + r];
@@ -922,6 +983,7 @@ __device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int
         }
     }
     wg_sync();
+    trace_stamp(a, p, kTrX1, tw0);
     if (holder) {
         const float qr = s[r];
 #pragma unroll
@@ -940,11 +1002,13 @@ __device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int
         *reinterpret_cast<f32x4*>(L.state + (size_t)hd * kDnD * kDnD + (size_t)r * kDnD + kDnCols * c + 4 * cq) = o;
     }
     wg_sync();   // Sk partials consumed
+    trace_stamp(a, p, kTrX2, tw0);
     if (holder && lane < 4) {
 #pragma unroll
         for (int j = 0; j < 4; j++) red[wave * kDnCols + 4 * cq + j] = yp[j];
     }
     wg_sync();
+    trace_stamp(a, p, kTrX3, tw0);
     float y = 0.f;
     if (active && wave == kCtl) {
         if (lane < kDnCols) {
@@ -1093,12 +1157,37 @@ __device__ __forceinline__ bool ctl_wait(const PArgs& a, int p, int ln) {
 
 enum : int { kDN = 0, kATT = 1, kNONE = 2 };
 
+constexpr int kNDG = 5;              // gate/up instructions decoded before the input (registers)
+
+// Compute waves: first half of layer l's gate/up weights with its LUTs, the
+// pair tables, and the lookups of the first kNDG instructions -- none of it
+// needs the input, so it runs while a barrier is pending.
+template <int NIG>
+__device__ __forceinline__ void gu_first(Buf<3 * NIG>& gb, LutRegs& glr, Buf<8 * kNDG>& gd, const GemvGeo& gu,
+                                         const PArgs& a, const PLayer& L, int l, int wave, int ln, char* lds) {
+    const uint8_t* const GW[2] = {L.w[0], L.w[1]};
+    const uint16_t* const GLU[2] = {L.lut[0], L.lut[1]};
+    const int p = 3 * l + 1;
+    const bool tw0 = wave == 0 && ln == 0;
+    gemv_issue<NIG, 0, NIG / 2, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
+    trace_stamp(a, p, kTrX0, tw0);
+    gemv_tables(glr, gu, 2, wave, ln, lds, ctl_ints(lds) + 8, gu.P * (l + 1));
+    trace_stamp(a, p, kTrX1, tw0);
+    gemv_decode<NIG, kNDG>(gb, gd, gu, 2, wave, ln, lds);
+    trace_stamp(a, p, kTrX2, tw0);
+}
+
 // One layer: core (KIND), gate/up, down; the end of the down phase prefetches
 // the next layer's core (NEXT).  core_buf holds this layer's prefetched core
-// data; next_buf receives the next layer's.  Returns false on abort.
-template <int KIND, int NEXT, int NIG, int NID, int NKJ, int JH, int JI, class BC, class BN>
-__device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& next_buf, int wave,
-                                          int lane, char* lds) {
+// data; next_buf receives the next layer's.  gb / glr / gd carry the gate/up
+// weights: with GUP the first half of this layer's was issued (and its tables
+// built) by the previous layer, and when NEXT is a DeltaNet layer this layer
+// issues the next one's while the down -> core barrier and the DeltaNet core
+// run (the attention core needs the table region of LDS, so a layer after an
+// attention core issues its own).  Returns false on abort.
+template <int KIND, int NEXT, bool GUP, int NIG, int NID, int NKJ, int JH, int JI, class BC, class BN>
+__device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& next_buf, Buf<3 * NIG>& gb,
+                                          LutRegs& glr, Buf<8 * kNDG>& gd, int wave, int lane, char* lds) {
     CArgs* ap = opaque_args(pa);
     const PArgs a = *ap;
     CLayer* layers = (CLayer*)a.layers;
@@ -1107,27 +1196,29 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     int ln = opaque(lane);
     float ydn = 0.f;
     const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
-    Buf<3 * NIG> gb;
-    LutRegs glr;
     constexpr int NAG = NIG / 2;     // weights issued before the barrier
-    constexpr int NDG = 5;           // of them decoded before the input (registers)
+    constexpr int NDG = kNDG;
     const uint8_t* const GW[2] = {L.w[0], L.w[1]};
     const uint16_t* const GLU[2] = {L.lut[0], L.lut[1]};
+    const int p0 = 3 * l;
+    const bool tw0 = wave == 0 && lane == 0, twc = wave == kCtl && lane == 0;
     // ------------------------------------------------------------ core
+    trace_stamp(a, p0, kTrStart, tw0);
     if constexpr (KIND == kATT) {
         attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
         vm_drain();
         wg_sync();
         attn_combine(a, L, l, lds, wave * 64 + ln);
     } else {
-        ydn = dn_compute(core_buf, a, L, wave, ln, lds);
+        ydn = dn_compute(core_buf, a, L, wave, ln, lds, p0);
     }
     // core outputs and DeltaNet states are read after the launch only; the
     // DeltaNet slab sums of squares are read after the barrier
     wg_sync();
-    const int p0 = 3 * l;
+    trace_stamp(a, p0, kTrEnd, tw0);
     if (wave == kCtl) {
         ln = opaque(lane);
+        trace_stamp(a, p0, kTrArrive, twc);
         ctl_arrive(a, p0, ln, KIND == kDN);
         // x and the norm weight were staged while the core ran (their loads
         // completed with the arrival's drain): the normalised input is ready
@@ -1135,25 +1226,31 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         stage_x_fin<JH>(a, ln, lds);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
-    Buf<8 * NDG> gd;
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0, ln);
+        trace_stamp(a, p0, kTrRelease, twc);
         if (ln == 0) ctl[0] = okw;
+    }
+    // (the control wave takes no share: it only defines its copies)
+    if constexpr (GUP) {
+        // the first half landed during the core: the second half goes out now
+        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        trace_stamp(a, p0 + 1, kTrX3, tw0);
     } else {
         // first half of the weights, the tables, and their lookups while the
         // barrier is pending
-        gemv_issue<NIG, 0, NAG, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
-        gemv_tables(glr, gu, 2, wave, ln, lds, ctl + 8, gu.P * (l + 1));
-        gemv_decode<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
+        gu_first<NIG>(gb, glr, gd, gu, a, L, l, wave, ln, lds);
+        wg_sync();
+        ln = opaque(lane);
+        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        trace_stamp(a, p0 + 1, kTrX3, tw0);
     }
-    wg_sync();
-    ln = opaque(lane);
-    if (wave != kCtl) gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
     wg_sync();
     if (!ctl[0]) return false;
     // --------------------------------------------------------- gate/up
     ln = opaque(lane);
+    trace_stamp(a, p0 + 1, kTrStart, tw0);
     gemv_compute<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
     // the control wave is idle during the gate/up products: finish the
     // DeltaNet outputs there, off the staging path
@@ -1161,6 +1258,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         if (wave == kCtl) dn_finish(a, L, ydn, ln);
     }
     wg_sync();
+    trace_stamp(a, p0 + 1, kTrEnd, tw0);
     const GemvGeo dg = gemv_geo(a.d_C, a.d_P, a.d_RP, a.d_rows, a.H);
     Buf<3 * NID> db;
     float x_old = 0.f;
@@ -1176,6 +1274,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         const float hn = __shfl_down(hv, 1, 64);
         if (ln < gu.nrows && (ln & 1) == 0)
             st_sc(reinterpret_cast<unsigned*>(a.h) + ((gu.R0 + ln) >> 1), pack_h2(hv, hn));
+        trace_stamp(a, p0 + 1, kTrArrive, twc);
         ctl_arrive(a, p0 + 1, ln, true);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
@@ -1185,6 +1284,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     ln = opaque(lane);
     if (wave == kCtl) {
         const int okw = ctl_wait(a, p0 + 1, ln);
+        trace_stamp(a, p0 + 1, kTrRelease, twc);
         if (ln == 0) ctl[0] = okw;
         if (okw) {
             stage_h_load<JI>(a, ln, lds);
@@ -1195,8 +1295,11 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
         LutRegs dlr;
         gemv_issue<NID, 0, NAD, true>(db, dlr, dg, W, LU, 1, wave, ln);
+        trace_stamp(a, p0 + 2, kTrX0, tw0);
         gemv_tables(dlr, dg, 1, wave, ln, lds, ctl + 10, dg.P * (l + 1));
+        trace_stamp(a, p0 + 2, kTrX1, tw0);
         gemv_decode<NID, NDD>(db, dd, dg, 1, wave, ln, lds);
+        trace_stamp(a, p0 + 2, kTrX2, tw0);
     }
     wg_sync();   // the h loads were issued ahead of the second half of the weights
     ln = opaque(lane);
@@ -1212,17 +1315,21 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         // not queue behind it
         if constexpr (NEXT == kDN) dn_prefetch(next_buf, a, layers[l + 1], wave, ln);
     }
+    trace_stamp(a, p0 + 2, kTrX3, tw0);
     wg_sync();
     if (!ctl[0]) return false;
     // ------------------------------------------------------------ down
     ln = opaque(lane);
+    trace_stamp(a, p0 + 2, kTrStart, tw0);
     gemv_compute<NID, NDD>(db, dd, dg, 1, wave, ln, lds);
     wg_sync();
+    trace_stamp(a, p0 + 2, kTrEnd, tw0);
     ln = opaque(lane);
     constexpr bool more = NEXT != kNONE;
     const PLayer Ln = layers[more ? l + 1 : l];
     if (wave == kCtl) {
         if (ln < dg.nrows) stf_sc(a.x + dg.R0 + ln, x_old + gemv_row_sum<NID>(dg, 0, ln, lds));
+        trace_stamp(a, p0 + 2, kTrArrive, twc);
         ctl_arrive(a, p0 + 2, ln, true);
     }
     if constexpr (more) wg_sync();   // the bulk loads below queue behind the arrival
@@ -1234,6 +1341,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         if constexpr (NEXT == kATT) attn_stage_load(a, Ln, ln, as);
         else if constexpr (NEXT == kDN) dn_stage_load(a, Ln, ln, ds);
         const int okw = more ? (int)ctl_wait(a, p0 + 2, ln) : 1;
+        trace_stamp(a, p0 + 2, kTrRelease, twc);
         if (ln == 0) ctl[0] = okw;
         if (more && okw) {
             // x is final now: stage it (and the next norm weight) for the next gate/up
@@ -1244,6 +1352,12 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         }
     } else if constexpr (NEXT == kATT) {
         attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
+    }
+    if constexpr (NEXT == kDN) {
+        // the next layer's gate/up weights stream in during this barrier and
+        // the next core (the down tables in LDS are dead now); the control
+        // wave takes no share and only defines its copies
+        gu_first<NIG>(gb, glr, gd, gu, a, Ln, l + 1, wave, ln, lds);
     }
     if constexpr (more) {
         wg_sync();
@@ -1267,6 +1381,10 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     int* ctl = ctl_ints(lds);
     Buf<kDnBuf> cdn;
     Buf<4 * NKJ> cat;
+    Buf<3 * NIG> gb;
+    LutRegs glr;
+    Buf<8 * kNDG> gd;
+    trace_stamp(a, kMaxPhases, 0, tid == 0);
     // phase 0: core of layer 0 (inputs are ready at launch)
     dn_prefetch(cdn, a, L0, wave, lane);
     if (wave == kCtl) {
@@ -1281,19 +1399,26 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
         ctl[8] = ctl[9] = ctl[10] = 0;   // table-build counters (gate, up, down)
     }
     wg_sync();
+    // layer 0's gate/up weights start streaming with its core
+    gu_first<NIG>(gb, glr, gd, gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I), a, L0, 0, wave, lane, lds);
     const int groups = a.n_layers / 4;
     for (int gr = 0; gr < groups; gr++) {
         const int l0 = 4 * gr;
-        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0, cdn, cdn, wave, lane, lds)) break;
-        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 1, cdn, cdn, wave, lane, lds)) break;
-        if (!run_layer<kDN, kATT, NIG, NID, NKJ, JH, JI>(pa, l0 + 2, cdn, cat, wave, lane, lds)) break;
+        if (!run_layer<kDN, kDN, true, NIG, NID, NKJ, JH, JI>(pa, l0, cdn, cdn, gb, glr, gd, wave, lane, lds)) break;
+        if (!run_layer<kDN, kDN, true, NIG, NID, NKJ, JH, JI>(pa, l0 + 1, cdn, cdn, gb, glr, gd, wave, lane, lds))
+            break;
+        if (!run_layer<kDN, kATT, true, NIG, NID, NKJ, JH, JI>(pa, l0 + 2, cdn, cat, gb, glr, gd, wave, lane, lds))
+            break;
         if (gr + 1 < groups) {
-            if (!run_layer<kATT, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, wave, lane, lds)) break;
+            if (!run_layer<kATT, kDN, false, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane,
+                                                                   lds))
+                break;
         } else {
-            run_layer<kATT, kNONE, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, wave, lane, lds);
+            run_layer<kATT, kNONE, false, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane, lds);
         }
     }
     // ------------------------------------------------------------ finish
+    trace_stamp(a, kMaxPhases, 1, tid == 0);
     vm_drain();
     wg_sync();
     if (tid == 0) ctl[3] = add_sc(a.sync + kFinOff, 1u) == gridDim.x - 1u;
@@ -1405,6 +1530,7 @@ void persistent_destroy(PersistentStep* s) {
     if (s->args.gpart) (void)hipFree(s->args.gpart);
     if (s->args.dnss) (void)hipFree(s->args.dnss);
     if (s->args.sync) (void)hipFree(s->args.sync);
+    if (s->args.trace) (void)hipFree(s->args.trace);
     delete s;
 }
 
@@ -1497,6 +1623,11 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     if (e == hipSuccess) e = hipMalloc(&s->args.dnss, sizeof(float) * (size_t)nwg);
     if (e == hipSuccess) e = hipMalloc(&s->args.sync, sizeof(unsigned) * pk::kSyncWords);
     if (e == hipSuccess) e = hipMemset(s->args.sync, 0, sizeof(unsigned) * pk::kSyncWords);
+#if ANELM_STEP_TRACE
+    const size_t trace_words = (size_t)nwg * (pk::kMaxPhases + 1) * pk::kTrEv;
+    if (e == hipSuccess) e = hipMalloc(&s->args.trace, sizeof(unsigned long long) * trace_words);
+    if (e == hipSuccess) e = hipMemset(s->args.trace, 0, sizeof(unsigned long long) * trace_words);
+#endif
     if (e == hipSuccess)
         e = hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize, pk::kLdsBytes);
     // every workgroup must be resident at once (they wait on each other)
@@ -1602,6 +1733,19 @@ int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
         ANELM_HIP(hipStreamSynchronize(st));
         return upload(s, st);
     }
+    return ANELM_OK;
+}
+
+// Copies the phase timeline of the last run (trace build only):
+// [grid][kMaxPhases + 1][8] real-time clock stamps (100 MHz), 0 where an event
+// was not reached.
+int persistent_trace(PersistentStep* s, unsigned long long* host, size_t n_words, int* grid, int* row) {
+    *grid = s->grid;
+    *row = pk::kMaxPhases + 1;
+    if (!s->args.trace) return set_error(ANELM_EINVAL, "step trace: library built without ANELM_STEP_TRACE");
+    const size_t need = (size_t)s->grid * (pk::kMaxPhases + 1) * pk::kTrEv;
+    ANELM_REQUIRE(n_words >= need, "step trace: %zu words needed", need);
+    ANELM_HIP(hipMemcpy(host, s->args.trace, need * sizeof(unsigned long long), hipMemcpyDeviceToHost));
     return ANELM_OK;
 }
 

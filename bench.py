@@ -642,6 +642,94 @@ def cpu_baseline(seconds=12.0):
                       f"(liboracle_timing.so), 1 thread, {cpu_model}, nproc {os.cpu_count()}"}
 
 
+def trace_step(runs=3, save=None):
+    """Phase timeline of the persistent step from libanelm_trace.so (the same
+    library built with the step's clock stamps compiled in): per phase kind
+    (DeltaNet core, attention core, gate/up, down) the median over layers of
+    the workgroup-median compute time, the spread of barrier arrivals, and the
+    time from the last arrival to the median workgroup seeing the release
+    (plus the gap from release to the next phase's compute start)."""
+    import numpy as np
+    import torch
+    from workloads import load_package
+    pkg_dir = os.path.join(ROOT, "ane-lm_amd")
+    trace_lib = os.path.join(pkg_dir, "libanelm_trace.so")
+    if not os.path.exists(trace_lib):
+        raise SystemExit(f"{trace_lib} not built (make -C ane-lm_amd/csrc)")
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "ane_lm_amd", os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["ane_lm_amd"] = mod
+    spec.loader.exec_module(mod)
+    mod.LIB_PATH = trace_lib
+    anelm = load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    out = []
+    with torch.cuda.stream(stream):
+        handle, keep, x, mode = build_step(anelm, torch, dev, mode=anelm.STEP_PERSISTENT | anelm.STEP_STATIC)
+        s = ctypes.c_void_p(stream.cuda_stream)
+        for _ in range(5):
+            anelm.call("anelm_hybrid_step_run", handle, s)
+        grid, rows = 256, 193
+        for r in range(runs):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            anelm.call("anelm_hybrid_step_run", handle, s)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            buf = np.zeros(1024 * 193 * 8, dtype=np.uint64)
+            g, ph = ctypes.c_int(0), ctypes.c_int(0)
+            anelm.call("anelm_hybrid_step_trace", handle, ctypes.c_void_p(buf.ctypes.data), buf.size,
+                       ctypes.byref(g), ctypes.byref(ph))
+            grid, rows = g.value, ph.value
+            out.append((e0.elapsed_time(e1) * 1e3, buf[: grid * rows * 8].reshape(grid, rows, 8).astype(np.int64)))
+        st = ctypes.c_int(0)
+        anelm.call("anelm_hybrid_step_status", handle, ctypes.byref(st))
+        assert st.value == 0, "a grid barrier of the persistent step timed out"
+        anelm.call("anelm_hybrid_step_destroy", handle)
+    n_layers = CFG["layers"]
+    tick_us = 0.01   # 100 MHz real-time clock
+    kinds = {"deltanet_core": [], "attention_core": [], "gate_up": [], "down": []}
+    runs_out = []
+    for us, tr in out:
+        t0 = tr[:, rows - 1, 0].min()
+        t_end = tr[:, rows - 1, 1].max()
+        S, E, A, R = (tr[:, :3 * n_layers, k] - t0 for k in range(4))
+        for p in range(3 * n_layers):
+            layer, k = divmod(p, 3)
+            kind = ["attention_core" if (layer + 1) % 4 == 0 else "deltanet_core", "gate_up", "down"][k]
+            comp = np.median(E[:, p] - S[:, p]) * tick_us
+            arr_spread = (A[:, p].max() - np.median(A[:, p])) * tick_us
+            last_arr = A[:, p].max()
+            if p + 1 < 3 * n_layers:
+                rel = (np.median(R[:, p]) - last_arr) * tick_us
+                nxt = (np.median(S[:, p + 1]) - np.median(R[:, p])) * tick_us
+            else:
+                rel, nxt = 0.0, 0.0
+            period = ((np.median(S[:, p + 1]) if p + 1 < 3 * n_layers else t_end - t0) - np.median(S[:, p])) * tick_us
+            kinds[kind].append((comp, arr_spread, rel, nxt, period))
+        runs_out.append({"event_us": round(us, 2), "clock_us": round((t_end - t0) * tick_us, 2)})
+    summary = {}
+    for kind, v in kinds.items():
+        a = np.array(v)
+        summary[kind] = {"phases": int(len(a) // runs),
+                         "compute_us": round(float(np.median(a[:, 0])), 2),
+                         "arrival_spread_us": round(float(np.median(a[:, 1])), 2),
+                         "last_arrival_to_release_us": round(float(np.median(a[:, 2])), 2),
+                         "release_to_next_start_us": round(float(np.median(a[:, 3])), 2),
+                         "phase_period_us": round(float(np.median(a[:, 4])), 2)}
+    per_layer = {k: round(summary[k]["phase_period_us"], 2) for k in summary}
+    if save:
+        import numpy as np
+        np.savez_compressed(save, *[tr for _, tr in out])
+    print(json.dumps({"trace": "persistent step phase timeline (median over layers of each phase kind)",
+                      "runs": runs_out, "phases": summary, "period_us": per_layer}, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -656,7 +744,14 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="after the timed steps, copy MB MiB device-to-device once (a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--trace-step", action="store_true",
+                    help="print the persistent step's phase timeline from libanelm_trace.so instead")
+    ap.add_argument("--trace-save", default=None, metavar="NPZ",
+                    help="with --trace-step: also save the raw stamps [grid][phases+1][4] per run")
     args = ap.parse_args()
+    if args.trace_step:
+        trace_step(save=args.trace_save)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark measures one GPU; the decode step does not "
                                    "shard across GPUs here (run with --gpus 1)"}))

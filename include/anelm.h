@@ -16,6 +16,7 @@
 #ifndef ANELM_H
 #define ANELM_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -476,6 +477,16 @@ int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream);
  * run gave up waiting at a grid barrier (its outputs are then invalid);
  * clears the flag.  Always 0 for the eager and graph modes. */
 int anelm_hybrid_step_status(anelm_hybrid_step* step, int* status);
+/* Diagnostic (no counterpart in the reference): copies the phase timeline of
+ * the last persistent run to host memory -- per workgroup, per phase
+ * (3 per layer: core, gate/up, down; then one row of kernel entry/exit),
+ * eight 100 MHz real-time clock stamps: compute start, compute end, barrier
+ * arrival, barrier release observed, then (GEMV phases) first weight issue
+ * done, pair tables built, early lookups done, second weight issue done.  Only libanelm_trace.so (the same
+ * library built with ANELM_STEP_TRACE=1) records it; libanelm.so returns
+ * ANELM_EINVAL.  *grid and *phases receive the buffer's dimensions. */
+int anelm_hybrid_step_trace(anelm_hybrid_step* step, uint64_t* host, size_t n_words, int* grid,
+                            int* phases);
 int anelm_hybrid_step_destroy(anelm_hybrid_step* step);
 
 /* ------------------------------------------------ batched decode step */
