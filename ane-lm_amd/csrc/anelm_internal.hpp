@@ -104,10 +104,14 @@ int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, co
                              int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
                              int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
 
-// `n` zeroed counters on the current device; nullptr if n exceeds the pool.
-uint32_t* counters(size_t n);
+// `n` counters of the current device's pool, in the range reserved for one
+// user (ranges never overlap, so no user sees another's values); nullptr if n
+// exceeds the range.  Every range starts zeroed.
+enum CounterUser : int { kCtrPrefill = 0, kCtrDeltaNetConv = 1, kCtrUsers = 2 };
+uint32_t* counters(size_t n, CounterUser user);
 
 constexpr size_t kCounterPool = 1 << 16;
+constexpr size_t kCounterRange = kCounterPool / 4;   // counters per user
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -239,6 +239,18 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
 #pragma unroll
     for (int g = 0; g < G; g++)
         qv[g] = tid < D ? sv.q[(size_t)(kvh * G + g) * p.q_stride + tid] : 0.f;
+    // the newest key and value (split holding them) are requested now too, so
+    // the owner's prologue waits for one memory round trip, not two
+    float kn_reg = 0.f, vn_reg = 0.f;
+    float vn8[8];
+    if (owner) {
+        if (tid < D) {
+            kn_reg = p.k_new[(size_t)kvh * D + tid];
+            vn_reg = p.v_new[(size_t)kvh * D + tid];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) vn8[i] = p.v_new[(size_t)kvh * D + dl * 8 + i];   // any alignment
+    }
     const int32_t* ptab = p.paged ? p.page_table + (size_t)seq * p.max_pages : nullptr;
     auto row_ptr = [&](const KV* base, int t) -> const KV* {
         const int lt = t0 + t;
@@ -272,14 +284,14 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         // the by-value arrays directly expands into a select over every entry
         norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, p.cs, p.sn);
         if (owner) {
-            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[(size_t)kvh * D + d];
+            if (tid < D) kn_s[tid] = kn_reg;
             __syncthreads();
             norm_rope_row<D>(kn_s, p.k_norm_w, p, red, p.cs, p.sn);
             KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
             KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
-            for (int d = tid; d < D; d += kNT) {
-                store_kv(kw + d, kn_s[d]);
-                store_kv(vw + d, p.v_new[(size_t)kvh * D + d]);
+            if (tid < D) {
+                store_kv(kw + tid, kn_s[tid]);
+                store_kv(vw + tid, vn_reg);
             }
             // The row loads above ran before the append: the newest key and
             // value come from the prologue instead, rounded as stored.
@@ -287,7 +299,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
             for (int b = 0; b < KB; b++) {
                 if (b * KPB + w * KPI + sub == nk - 1) {
                     rk[b] = make_raw<KV>(kn_s + dl * 8);
-                    rv[b] = make_raw<KV>(p.v_new + (size_t)kvh * D + dl * 8);
+                    rv[b] = make_raw<KV>(vn8);
                 }
             }
         }

@@ -751,7 +751,7 @@ extern "C" int anelm_deltanet_decode_from_proj(float* y, float* state, float* co
     ANELM_REQUIRE((flags & ~7) == 0, "deltanet_decode_from_proj: unknown flags 0x%x", flags);
     const bool gated = (flags & ANELM_DN_GATED_NORM) != 0;
     ANELM_REQUIRE(!gated || norm_w != nullptr, "deltanet_decode_from_proj: GATED_NORM needs norm_w");
-    uint32_t* ctr = counters((size_t)Hk);
+    uint32_t* ctr = counters((size_t)Hk, kCtrDeltaNetConv);
     if (!ctr) return set_error(ANELM_ERANGE, "deltanet_decode_from_proj: %d key heads exceed the counter pool", Hk);
     const long qkv = 2L * Hk * kDK + (long)Hv * kDV;
     DnParams p{};

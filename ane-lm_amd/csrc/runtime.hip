@@ -87,14 +87,15 @@ void* workspace2(size_t bytes, hipStream_t stream) {
     return grow(d->ws2, d->ws2_bytes, bytes, stream);
 }
 
-uint32_t* counters(size_t n) {
+uint32_t* counters(size_t n, CounterUser user) {
+    static_assert((size_t)kCtrUsers * kCounterRange <= kCounterPool, "counter ranges exceed the pool");
     Device* d = device();
     if (!d) return nullptr;
-    if (n > d->n_counters) {
-        set_error(ANELM_ERANGE, "%zu counters requested, pool holds %zu", n, d->n_counters);
+    if (n > kCounterRange) {
+        set_error(ANELM_ERANGE, "%zu counters requested, a range holds %zu", n, kCounterRange);
         return nullptr;
     }
-    return d->counters;
+    return d->counters + (size_t)user * kCounterRange;
 }
 
 void rope_row(float* cos_out, float* sin_out, int rot_dim, int pos, float theta) {
