@@ -68,15 +68,20 @@ __device__ __forceinline__ uint32_t pair_off(const uint32_t (&wd)[NWD], int p, u
     return (v & 0x3FFCu) | tb;
 }
 
+// Group g's weights of this lane (buffer loads over the matrix, streaming
+// cache policy).  A group past the last one lies outside the buffer: its
+// loads return zeros without touching memory, so the pipeline's prefetch
+// after a workgroup's last group costs no traffic.
 template <int NP>
 __device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w,
                                              int lane) {
     const int m = lane & 31, hh = lane >> 5;
-    const u32x4* p = reinterpret_cast<const u32x4*>(a.w + ((size_t)g * 32 + m) * (size_t)a.ldw +
-                                                    (size_t)w * 96 * NP + hh * 48 * NP);
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, (int)((long)a.out_dim * a.ldw), 0x00020000);
+    const int off = (int)(((long)g * 32 + m) * a.ldw) + w * 96 * NP + hh * 48 * NP;
 #pragma unroll
     for (int i = 0; i < 3 * NP; i++) {
-        const u32x4 v = __builtin_nontemporal_load(p + i);
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 2));
         wd[4 * i] = v.x;
         wd[4 * i + 1] = v.y;
         wd[4 * i + 2] = v.z;
@@ -213,9 +218,9 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
     // registers wa (table slot 0), group gn's LUT and weights are in flight
     // into lr / wb, its table is built into slot 1 after the products, and the
     // roles swap for the next group.  The LUT load is issued before the
-    // weights, so waiting for it never waits for them; loads past the last
-    // group repeat the last group (clamped, never used).
-    const int stride = gridDim.x, last = n_groups - 1;
+    // weights, so waiting for it never waits for them; weight loads past the
+    // last group read nothing (out of the buffer's range) and are never used.
+    const int stride = gridDim.x;
     uint32_t wa[12 * NP], wb[12 * NP];
     load_weights<NP>(wa, a, g, w, lane);
     stage_luts<nt>(a, lds, 0, tid);
@@ -233,7 +238,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
         reduce_store<NW, ACC>(a, g, lds, tid);
         return;
     }
-    load_weights<NP>(wb, a, min(g + stride, last), w, lane);
+    load_weights<NP>(wb, a, g + stride, w, lane);
     float* red = reinterpret_cast<float*>(lds + kRedOff);
     // j counts the workgroup's groups; LUTs are restaged every kLutSlots groups
     for (int j = 0;; j += 2) {
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
         reduce_store<NW, ACC>(a, g, lds, tid);
         g += stride;
         if (g >= n_groups) break;
-        load_weights<NP>(wa, a, min(g + stride, last), w, lane);
+        load_weights<NP>(wa, a, g + stride, w, lane);
         lds_barrier();                                 // table 1 ready; red free
         {
             float16_t c = float16_t{};
@@ -268,7 +273,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
         reduce_store<NW, ACC>(a, g, lds, tid);
         g += stride;
         if (g >= n_groups) break;
-        load_weights<NP>(wb, a, min(g + stride, last), w, lane);
+        load_weights<NP>(wb, a, g + stride, w, lane);
     }
 }
 
@@ -313,7 +318,7 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
                      int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st) {
     int np = 0, waves = 0;
     if (!lut6_gemm_geometry(in_dim, np, waves) || batch < 1 || batch > 32 || out_dim % 32 ||
-        (long long)batch * out_dim * 4 >= (1LL << 31))
+        (long long)batch * out_dim * 4 >= (1LL << 31) || (long long)(out_dim + 32 * 1024) * ldw >= (1LL << 31))
         return set_error(ANELM_EINVAL, "lut6_gemm: unsupported shape batch %d out %d in %d", batch, out_dim,
                          in_dim);
     Device* dev = device();
