@@ -13,8 +13,9 @@
 //
 // Phase order is the model's dependency chain, per layer L:
 //   core(L) -> barrier -> gate/up(L) -> barrier -> down(L) -> barrier -> core(L+1)
-// (the projections around the cores are not part of the step; the chain keeps
-// the order they would impose).
+// where an attention core is two phases, the key splits and the merge of their
+// records, with a barrier between them (the projections around the cores are
+// not part of the step; the chain keeps the order they would impose).
 //
 // Workgroup = 10 compute waves + 1 control wave.  Compute waves only stream
 // bulk data (weights, KV rows, state) and compute.  The control wave does all
@@ -67,17 +68,15 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------- sync words
 constexpr int kPad = 64;              // 256 bytes per slot
 constexpr int kNG = 16;               // barrier groups
-constexpr int kMaxPhases = 192;       // 3 per layer -> up to 64 layers
+constexpr int kMaxPhases = 208;       // 3 per layer + 1 per attention layer -> up to 64 layers
 constexpr int kMaxLayers = 64;
 constexpr int kMaxKvh = 8;
-constexpr int kSplitGroups = 8;       // two-level split combine
-constexpr int kSplitsPerGroup = 8;    // splits per group (64 splits per kv head)
+constexpr int kAttnSplits = 64;      // key splits per kv head (one workgroup each)
+constexpr int kAttnRec = 256 + 4;     // split record per q head: o[256], m, l, 2 pad (16-byte aligned)
 constexpr long kGrpOff = 0;
 constexpr long kRootOff = kGrpOff + (long)kMaxPhases * kNG * kPad;
 constexpr long kRelOff = kRootOff + (long)kMaxPhases * kPad;
-constexpr long kGcOff = kRelOff + (long)kMaxPhases * kNG * kPad;          // [layer][kvh][group]
-constexpr long kHcOff = kGcOff + (long)kMaxLayers * kMaxKvh * kSplitGroups * kPad;  // [layer][kvh]
-constexpr long kFinOff = kHcOff + (long)kMaxLayers * kMaxKvh * kPad;
+constexpr long kFinOff = kRelOff + (long)kMaxPhases * kNG * kPad;
 constexpr long kAbortOff = kFinOff + kPad;
 constexpr long kStatusOff = kAbortOff + kPad;
 constexpr long kSyncWords = kStatusOff + kPad;
@@ -131,7 +130,6 @@ struct PArgs {
     float* h;                         // [I]
     float* part;                      // [Hkv][splits][G][D+2]
     float* dnss;                      // [Hv][8] DeltaNet slab sums of squares
-    float* gpart;                     // [Hkv][8][G][D+2]
     unsigned* sync;
     int H, I;
     int gu_C, gu_P, gu_RP, gu_rows;
@@ -652,7 +650,7 @@ __device__ void attn_stage_fin(const PArgs& a, const PLayer& L, int lane, char* 
     }
 }
 
-// Attention core for one split; writes the split record (m, l, o[256]) per q head.
+// Attention core for one split; writes the split record (o[256], m, l) per q head.
 template <int NKJ>
 __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, int wave, int lane, char* lds,
                              int layer) {
@@ -782,85 +780,23 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
         }
     }
     wg_sync();
-    // -- split record: m, l, o[256] per q head (device-coherent stores)
+    // -- split record: o[256], m, l per q head (device-coherent stores)
     if (active) {
-        const int rec = kAttnD + 2;
+        const int rec = kAttnRec;
         float* pr = a.part + ((size_t)kvh * a.splits + sp) * kAttnG * rec;
         for (int e = tid; e < kAttnG * kAttnD; e += kNT) {
             const int g = e / kAttnD, d = e - g * kAttnD;
             float o = 0.f;
 #pragma unroll
             for (int w = 0; w < kCW; w++) o += red[(w * kAttnG + g) * kAttnD + d];
-            stf_sc(pr + g * rec + 2 + d, o);
+            stf_sc(pr + g * rec + d, o);
         }
         if (tid < kAttnG) {
-            stf_sc(pr + tid * rec, nk > 0 ? ml[tid] : -INFINITY);
-            stf_sc(pr + tid * rec + 1, nk > 0 ? ml[kAttnG + tid] : 0.f);
+            stf_sc(pr + tid * rec + kAttnD, nk > 0 ? ml[tid] : -INFINITY);
+            stf_sc(pr + tid * rec + kAttnD + 1, nk > 0 ? ml[kAttnG + tid] : 0.f);
         }
     }
     (void)layer;
-}
-
-// Log-sum-exp merge of N records (stride rstride floats, layout m, l, o[256]
-// per q head, 4 heads per record) into out_rec (same layout) or, when
-// `final`, the gated output.  All threads of the workgroup; every record value
-// a thread needs is loaded before the first is used (one round trip).
-template <int N>
-__device__ void attn_merge(const float* recs, int rstride, float* out_rec, bool final, const PLayer& L,
-                           int kvh, float* lds_m, int tid) {
-    static_assert(N <= 64, "one wave reduces the records of a head");
-    const int rec = kAttnD + 2;
-    // per head: M and the weights e^(m_s - M) in LDS
-    float* wgt = lds_m;                 // [4][64]
-    float* tot = lds_m + 4 * 64;        // M[4], Lsum[4]
-    if (tid < 64 * kAttnG) {
-        const int g = tid >> 6, s = tid & 63;
-        float m = -INFINITY, l = 0.f;
-        if (s < N) {
-            m = ldf_sc(recs + (size_t)s * rstride + g * rec);
-            l = ldf_sc(recs + (size_t)s * rstride + g * rec + 1);
-        }
-        const float M = wave_max(m);
-        const float w = (s < N && m != -INFINITY) ? __expf(m - M) : 0.f;
-        const float Ls = wave_sum(l * w);
-        wgt[g * 64 + s] = w;
-        if (s == 0) {
-            tot[g] = M;
-            tot[4 + g] = Ls;
-        }
-    }
-    wg_sync();
-    constexpr int E = kAttnG * kAttnD;
-    constexpr int PER = (E + kNT - 1) / kNT;
-    float v[PER][N];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int e = min(tid + k * kNT, E - 1);
-        const int g = e / kAttnD, d = e - g * kAttnD;
-#pragma unroll
-        for (int s = 0; s < N; s++) v[k][s] = ldf_sc(recs + (size_t)s * rstride + g * rec + 2 + d);
-    }
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int e = tid + k * kNT;
-        if (e >= E) continue;
-        const int g = e / kAttnD, d = e - g * kAttnD;
-        float o = 0.f;
-#pragma unroll
-        for (int s = 0; s < N; s++) o += wgt[g * 64 + s] * v[k][s];
-        if (final) {
-            const int hq = kvh * kAttnG + g;
-            float y = o / tot[4 + g];
-            y = y / (1.0f + expf(-L.q_gate[(size_t)hq * 2 * kAttnD + kAttnD + d]));
-            L.core_out[(size_t)hq * kAttnD + d] = y;
-        } else {
-            stf_sc(out_rec + g * rec + 2 + d, o);
-        }
-    }
-    if (!final && tid < kAttnG) {
-        stf_sc(out_rec + tid * rec, tot[tid]);
-        stf_sc(out_rec + tid * rec + 1, tot[4 + tid]);
-    }
 }
 
 // ================================================================= DeltaNet
@@ -1047,38 +983,63 @@ __device__ void dn_finish(const PArgs& a, const PLayer& L, float y, int lane) {
     }
 }
 
-constexpr int kMergeOff = 131072;           // merge weights [4][64] + M[4], L[4]
-
-// Two-level split combine (all threads; after the split record is stored):
-// the last split of each group of 8 merges its group, the last group merges
-// the head and writes the gated output.  Counters are per (layer, kv head).
-__device__ void attn_combine(const PArgs& a, const PLayer& L, int layer, char* lds, int tid) {
-    const int wg = blockIdx.x;
-    const int kvh = wg / a.splits, sp = wg - kvh * a.splits;
+// Merge phase of an attention layer (control wave, after the barrier that
+// follows the split phase): workgroup w merges one slice of the layer's
+// output -- kv head w / 64, q head g = (w % 64) / 16 of its group, output
+// dims [16 j, 16 j + 16), j = w % 16 -- over the 64 split records of that kv
+// head (device-coherent loads, one round trip): M = max m_s,
+// L = sum l_s e^(m_s - M), y = sum o_s e^(m_s - M) / L, then the sigmoid gate
+// (models/llm/qwen3_5.cpp:944-1002 after core/cpu_ops.cpp:148-204).  Lane s
+// holds split s.  attn_merge_load issues every load, attn_merge_fin merges.
+struct MergeRegs {
+    float m, l, gate_in;
+    float o[16];
+};
+__device__ __forceinline__ void attn_merge_load(const PArgs& a, const PLayer& L, int lane, MergeRegs& r) {
+    const int w = blockIdx.x;
+    const int kvh = w / kAttnSplits, rr = w - kvh * kAttnSplits;
+    r.m = -INFINITY;
+    r.l = r.gate_in = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) r.o[k] = 0.f;
     if (kvh >= a.Hkv) return;
-    int* ctl = reinterpret_cast<int*>(lds + kLdsCtl);
-    const int spg = a.splits / kSplitGroups, sg = sp / spg;
-    const int rec = kAttnG * (kAttnD + 2);
-    if (tid == 0) {
-        unsigned* gc = a.sync + kGcOff + (((long)layer * kMaxKvh + kvh) * kSplitGroups + sg) * kPad;
-        ctl[1] = add_sc(gc, 1u) == (unsigned)spg - 1u;
+    const int g = rr / (kAttnD / 16), j = rr - g * (kAttnD / 16);
+    // 16-byte device-coherent loads: the slice and (m, l) are 16-byte aligned
+    const __amdgpu_buffer_rsrc_t rp =
+        rsrc(a.part, (uint32_t)((size_t)a.Hkv * a.splits * kAttnG * kAttnRec * sizeof(float)));
+    const int base = (int)((((size_t)kvh * a.splits + lane) * kAttnG + g) * kAttnRec * sizeof(float));
+    const f32x4 ml = ld4_sc(rp, base + kAttnD * 4);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const f32x4 v = ld4_sc(rp, base + (16 * j + 4 * k) * 4);
+        r.o[4 * k] = v.x; r.o[4 * k + 1] = v.y; r.o[4 * k + 2] = v.z; r.o[4 * k + 3] = v.w;
     }
-    wg_sync();
-    if (!ctl[1]) return;
-    float* grec = a.gpart + ((size_t)kvh * kSplitGroups + sg) * rec;
-    attn_merge<kSplitsPerGroup>(a.part + ((size_t)kvh * a.splits + sg * spg) * rec, rec, grec, false, L, kvh,
-                                reinterpret_cast<float*>(lds + kMergeOff), tid);
-    vm_drain();
-    wg_sync();
-    if (tid == 0) {
-        unsigned* hc = a.sync + kHcOff + ((long)layer * kMaxKvh + kvh) * kPad;
-        ctl[2] = add_sc(hc, 1u) == (unsigned)kSplitGroups - 1u;
+    r.m = ml.x;
+    r.l = ml.y;
+    if (lane < 16) r.gate_in = L.q_gate[(size_t)(kvh * kAttnG + g) * 2 * kAttnD + kAttnD + 16 * j + lane];
+}
+__device__ __forceinline__ void attn_merge_fin(const PArgs& a, const PLayer& L, int lane, MergeRegs& r) {
+    const int w = blockIdx.x;
+    const int kvh = w / kAttnSplits, rr = w - kvh * kAttnSplits;
+    if (kvh >= a.Hkv) return;
+    const int g = rr / (kAttnD / 16), j = rr - g * (kAttnD / 16);
+    const int hq = kvh * kAttnG + g;
+    const float M = wave_max(r.m);
+    const float wt = r.m != -INFINITY ? __expf(r.m - M) : 0.f;
+    const float Ls = wave_sum(r.l * wt);
+#pragma unroll
+    for (int k = 0; k < 16; k++) r.o[k] *= wt;
+    // 16 sums over the 64 lanes: lane li < 16 of each 16-lane row ends with
+    // its row's total of value li, then the four rows are added
+    transpose_reduce<16, 16>(r.o, lane & 15);
+    float y = r.o[0];
+    y += partner<16>(y);
+    y += partner<32>(y);
+    if (lane < 16) {
+        y = y / Ls;
+        y = y / (1.0f + expf(-r.gate_in));
+        L.core_out[(size_t)hq * kAttnD + 16 * j + lane] = y;
     }
-    wg_sync();
-    if (!ctl[2]) return;
-    attn_merge<kSplitGroups>(a.gpart + (size_t)kvh * kSplitGroups * rec, rec, nullptr, true, L, kvh,
-                             reinterpret_cast<float*>(lds + kMergeOff), tid);
-    vm_drain();
 }
 
 // Control wave: GEMV input staging.  LDS holds the input as fp16 pairs in
@@ -1177,15 +1138,16 @@ __device__ __forceinline__ void gu_first(Buf<3 * NIG>& gb, LutRegs& glr, Buf<8 *
     trace_stamp(a, p, kTrX2, tw0);
 }
 
-// One layer: core (KIND), gate/up, down; the end of the down phase prefetches
-// the next layer's core (NEXT).  core_buf holds this layer's prefetched core
-// data; next_buf receives the next layer's.  gb / glr / gd carry the gate/up
-// weights: with GUP the first half of this layer's was issued (and its tables
-// built) by the previous layer, and when NEXT is a DeltaNet layer this layer
-// issues the next one's while the down -> core barrier and the DeltaNet core
-// run (the attention core needs the table region of LDS, so a layer after an
-// attention core issues its own).  Returns false on abort.
-template <int KIND, int NEXT, bool GUP, int NIG, int NID, int NKJ, int JH, int JI, class BC, class BN>
+// One layer: core (KIND; an attention core is a split phase and a merge
+// phase), gate/up, down; the end of the down phase prefetches the next
+// layer's core (NEXT).  core_buf holds this layer's prefetched core data;
+// next_buf receives the next layer's.  gb / glr / gd carry the gate/up
+// weights: a DeltaNet layer's first half was issued (and its tables built) by
+// the previous layer while the down -> core barrier and the DeltaNet core ran
+// (NEXT == kDN below); an attention layer issues its own during its merge
+// phase, once the split phase has left the table region of LDS free.
+// Returns false on abort.
+template <int KIND, int NEXT, int NIG, int NID, int NKJ, int JH, int JI, class BC, class BN>
 __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& next_buf, Buf<3 * NIG>& gb,
                                           LutRegs& glr, Buf<8 * kNDG>& gd, int wave, int lane, char* lds) {
     CArgs* ap = opaque_args(pa);
@@ -1206,9 +1168,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     trace_stamp(a, p0, kTrStart, tw0);
     if constexpr (KIND == kATT) {
         attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
-        vm_drain();
-        wg_sync();
-        attn_combine(a, L, l, lds, wave * 64 + ln);
+        vm_drain();   // this thread's part of the split record has been stored
     } else {
         ydn = dn_compute(core_buf, a, L, wave, ln, lds, p0);
     }
@@ -1227,27 +1187,71 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     }
     wg_sync();   // the bulk loads below queue behind the arrival
     ln = opaque(lane);
-    if (wave == kCtl) {
-        const int okw = ctl_wait(a, p0, ln);
-        trace_stamp(a, p0, kTrRelease, twc);
-        if (ln == 0) ctl[0] = okw;
-    }
-    // (the control wave takes no share: it only defines its copies)
-    if constexpr (GUP) {
-        // the first half landed during the core: the second half goes out now
-        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
-        trace_stamp(a, p0 + 1, kTrX3, tw0);
-    } else {
-        // first half of the weights, the tables, and their lookups while the
-        // barrier is pending
-        gu_first<NIG>(gb, glr, gd, gu, a, L, l, wave, ln, lds);
-        wg_sync();
+    if constexpr (KIND == kATT) {
+        // ------------------------------------------------- attention merge
+        // The merge is a phase of its own: every split record is complete
+        // when it starts, and the FFN waits for the merged output as it would
+        // for the projection of it.  The split phase left the table region of
+        // LDS free: the LUTs and pair tables of this layer's gate/up are built
+        // while the split barrier resolves; the first half of its weights is
+        // issued once the merge's record loads are out (flag in LDS), so those
+        // loads are the first memory requests after the barrier.
+        const int pm = 3 * a.n_layers + l / 4;
+        if (wave == kCtl) {
+            const int okw = ctl_wait(a, p0, ln);
+            trace_stamp(a, p0, kTrRelease, twc);
+            if (ln == 0) ctl[0] = okw;
+            MergeRegs mr;
+            if (okw) {
+                trace_stamp(a, pm, kTrStart, twc);
+                attn_merge_load(a, L, ln, mr);
+            }
+            if (ln == 0) __hip_atomic_store(ctl + 12, l + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (okw) {
+                attn_merge_fin(a, L, ln, mr);
+                trace_stamp(a, pm, kTrEnd, twc);
+                trace_stamp(a, pm, kTrArrive, twc);
+                ctl_arrive(a, pm, ln, false);
+            }
+        } else {
+            gemv_issue<NIG, 0, 0, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
+            trace_stamp(a, p0 + 1, kTrX0, tw0);
+            gemv_tables(glr, gu, 2, wave, ln, lds, ctl + 8, gu.P * (l + 1));
+            trace_stamp(a, p0 + 1, kTrX1, tw0);
+            for (int it = 0; it < (1 << 20); it++) {
+                if (__hip_atomic_load(ctl + 12, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == l + 1) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        // (the control wave takes no share: it only defines its copies)
+        gemv_issue<NIG, 0, NAG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        gemv_decode<NIG, NDG>(gb, gd, gu, 2, wave, ln, lds);
+        trace_stamp(a, p0 + 1, kTrX2, tw0);
+        wg_sync();   // the bulk loads below queue behind the merge's arrival
+        if (!ctl[0]) return false;
         ln = opaque(lane);
+        if (wave == kCtl) {
+            const int okw = ctl_wait(a, pm, ln);
+            trace_stamp(a, pm, kTrRelease, twc);
+            if (ln == 0) ctl[0] = okw;
+        }
         gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
         trace_stamp(a, p0 + 1, kTrX3, tw0);
+        wg_sync();
+        if (!ctl[0]) return false;
+    } else {
+        if (wave == kCtl) {
+            const int okw = ctl_wait(a, p0, ln);
+            trace_stamp(a, p0, kTrRelease, twc);
+            if (ln == 0) ctl[0] = okw;
+        }
+        // the first half landed during the core: the second half goes out now
+        // (the control wave takes no share: it only defines its copies)
+        gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        trace_stamp(a, p0 + 1, kTrX3, tw0);
+        wg_sync();
+        if (!ctl[0]) return false;
     }
-    wg_sync();
-    if (!ctl[0]) return false;
     // --------------------------------------------------------- gate/up
     ln = opaque(lane);
     trace_stamp(a, p0 + 1, kTrStart, tw0);
@@ -1397,6 +1401,7 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     if (tid == 0) {
         ctl[0] = 1;
         ctl[8] = ctl[9] = ctl[10] = 0;   // table-build counters (gate, up, down)
+        ctl[12] = 0;                     // merge loads issued (attention layer + 1)
     }
     wg_sync();
     // layer 0's gate/up weights start streaming with its core
@@ -1404,17 +1409,17 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     const int groups = a.n_layers / 4;
     for (int gr = 0; gr < groups; gr++) {
         const int l0 = 4 * gr;
-        if (!run_layer<kDN, kDN, true, NIG, NID, NKJ, JH, JI>(pa, l0, cdn, cdn, gb, glr, gd, wave, lane, lds)) break;
-        if (!run_layer<kDN, kDN, true, NIG, NID, NKJ, JH, JI>(pa, l0 + 1, cdn, cdn, gb, glr, gd, wave, lane, lds))
+        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0, cdn, cdn, gb, glr, gd, wave, lane, lds)) break;
+        if (!run_layer<kDN, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 1, cdn, cdn, gb, glr, gd, wave, lane, lds))
             break;
-        if (!run_layer<kDN, kATT, true, NIG, NID, NKJ, JH, JI>(pa, l0 + 2, cdn, cat, gb, glr, gd, wave, lane, lds))
+        if (!run_layer<kDN, kATT, NIG, NID, NKJ, JH, JI>(pa, l0 + 2, cdn, cat, gb, glr, gd, wave, lane, lds))
             break;
         if (gr + 1 < groups) {
-            if (!run_layer<kATT, kDN, false, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane,
+            if (!run_layer<kATT, kDN, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane,
                                                                    lds))
                 break;
         } else {
-            run_layer<kATT, kNONE, false, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane, lds);
+            run_layer<kATT, kNONE, NIG, NID, NKJ, JH, JI>(pa, l0 + 3, cat, cdn, gb, glr, gd, wave, lane, lds);
         }
     }
     // ------------------------------------------------------------ finish
@@ -1425,17 +1430,12 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     wg_sync();
     if (ctl[3]) {
         // last workgroup out: every other one has finished all sync accesses
-        const int np = 3 * a.n_layers;
+        const int np = 3 * a.n_layers + a.n_layers / 4;
         for (int i = tid; i < np * (2 * kNG + 1); i += kNT) {
             const int p = i / (2 * kNG + 1), k = i - p * (2 * kNG + 1);
             if (k < kNG) st_sc(a.sync + kGrpOff + ((long)p * kNG + k) * kPad, 0u);
             else if (k < 2 * kNG) st_sc(a.sync + kRelOff + ((long)p * kNG + (k - kNG)) * kPad, 0u);
             else st_sc(a.sync + kRootOff + (long)p * kPad, 0u);
-        }
-        for (int i = tid; i < a.n_layers * kMaxKvh * (kSplitGroups + 1); i += kNT) {
-            const int lk = i / (kSplitGroups + 1), k = i - lk * (kSplitGroups + 1);
-            if (k < kSplitGroups) st_sc(a.sync + kGcOff + ((long)lk * kSplitGroups + k) * kPad, 0u);
-            else st_sc(a.sync + kHcOff + (long)lk * kPad, 0u);
         }
         if (tid == 0) {
             st_sc(a.sync + kFinOff, 0u);
@@ -1527,7 +1527,6 @@ void persistent_destroy(PersistentStep* s) {
     if (s->d_args) (void)hipFree(s->d_args);
     if (s->d_rope) (void)hipFree(s->d_rope);
     if (s->args.part) (void)hipFree(s->args.part);
-    if (s->args.gpart) (void)hipFree(s->args.gpart);
     if (s->args.dnss) (void)hipFree(s->args.dnss);
     if (s->args.sync) (void)hipFree(s->args.sync);
     if (s->args.trace) (void)hipFree(s->args.trace);
@@ -1579,7 +1578,7 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
                           d->n_kv_heads <= pk::kMaxKvh && nwg % d->n_kv_heads == 0,
                       "persistent step: attention needs head_dim 256 and 4 q heads per kv head");
         splits = nwg / d->n_kv_heads;
-        ANELM_REQUIRE(splits == pk::kSplitGroups * pk::kSplitsPerGroup,
+        ANELM_REQUIRE(splits == pk::kAttnSplits && pk::kAttnSplits == pk::kAttnG * (pk::kAttnD / 16),
                       "persistent step: %d splits per kv head", splits);
         kps = (cap + splits - 1) / splits;
         nkj = (kps + 19) / 20;
@@ -1617,9 +1616,8 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     hipError_t e = hipMalloc(&s->d_layers, sizeof(pk::PLayer) * n_layers);
     if (e == hipSuccess) e = hipMalloc(&s->d_args, sizeof(pk::PArgs));
     if (e == hipSuccess) e = hipMalloc(&s->d_rope, sizeof(float) * (size_t)n_layers * (s->rot > 0 ? s->rot : 2));
-    const size_t rec = (size_t)pk::kAttnG * (pk::kAttnD + 2);
+    const size_t rec = (size_t)pk::kAttnG * pk::kAttnRec;
     if (e == hipSuccess) e = hipMalloc(&s->args.part, sizeof(float) * rec * (n_attn ? d->n_kv_heads * splits : 1));
-    if (e == hipSuccess) e = hipMalloc(&s->args.gpart, sizeof(float) * rec * (n_attn ? d->n_kv_heads * pk::kSplitGroups : 1));
     if (e == hipSuccess) e = hipMalloc(&s->args.dnss, sizeof(float) * (size_t)nwg);
     if (e == hipSuccess) e = hipMalloc(&s->args.sync, sizeof(unsigned) * pk::kSyncWords);
     if (e == hipSuccess) e = hipMemset(s->args.sync, 0, sizeof(unsigned) * pk::kSyncWords);

@@ -694,24 +694,33 @@ def trace_step(runs=3, save=None):
         anelm.call("anelm_hybrid_step_destroy", handle)
     n_layers = CFG["layers"]
     tick_us = 0.01   # 100 MHz real-time clock
-    kinds = {"deltanet_core": [], "attention_core": [], "gate_up": [], "down": []}
+    kinds = {"deltanet_core": [], "attention_split": [], "attention_merge": [], "gate_up": [], "down": []}
+    # phases in execution order: core, (attention: merge), gate/up, down
+    seq = []
+    for layer in range(n_layers):
+        att = (layer + 1) % 4 == 0
+        seq.append((3 * layer, "attention_split" if att else "deltanet_core"))
+        if att:
+            seq.append((3 * n_layers + layer // 4, "attention_merge"))
+        seq.append((3 * layer + 1, "gate_up"))
+        seq.append((3 * layer + 2, "down"))
     runs_out = []
     for us, tr in out:
         t0 = tr[:, rows - 1, 0].min()
         t_end = tr[:, rows - 1, 1].max()
-        S, E, A, R = (tr[:, :3 * n_layers, k] - t0 for k in range(4))
-        for p in range(3 * n_layers):
-            layer, k = divmod(p, 3)
-            kind = ["attention_core" if (layer + 1) % 4 == 0 else "deltanet_core", "gate_up", "down"][k]
+        S, E, A, R = (tr[:, :rows - 1, k] - t0 for k in range(4))
+        for q, (p, kind) in enumerate(seq):
             comp = np.median(E[:, p] - S[:, p]) * tick_us
             arr_spread = (A[:, p].max() - np.median(A[:, p])) * tick_us
             last_arr = A[:, p].max()
-            if p + 1 < 3 * n_layers:
+            if q + 1 < len(seq):
+                pn = seq[q + 1][0]
                 rel = (np.median(R[:, p]) - last_arr) * tick_us
-                nxt = (np.median(S[:, p + 1]) - np.median(R[:, p])) * tick_us
+                nxt = (np.median(S[:, pn]) - np.median(R[:, p])) * tick_us
+                period = (np.median(S[:, pn]) - np.median(S[:, p])) * tick_us
             else:
                 rel, nxt = 0.0, 0.0
-            period = ((np.median(S[:, p + 1]) if p + 1 < 3 * n_layers else t_end - t0) - np.median(S[:, p])) * tick_us
+                period = (t_end - t0 - np.median(S[:, p])) * tick_us
             kinds[kind].append((comp, arr_spread, rel, nxt, period))
         runs_out.append({"event_us": round(us, 2), "clock_us": round((t_end - t0) * tick_us, 2)})
     summary = {}
