@@ -417,10 +417,13 @@ __device__ __forceinline__ void gemv_tables(const LutRegs& lr, const GemvGeo& q,
 }
 
 // Table lookups of instructions m < NA ahead of the input (they need only
-// the weights and the tables): decoded fp16 pairs into d.
+// the weights and the tables): decoded fp16 pairs into d.  Only instructions
+// already issued may be decoded: a lookup of an unissued one reads undefined
+// registers.
 template <int NI, int NA>
 __device__ __forceinline__ void gemv_decode(const Buf<3 * NI>& b, Buf<8 * NA>& d, const GemvGeo& q, int n_mat,
                                             int wave, int lane, char* lds) {
+    static_assert(NA <= NI, "decode range");
     if (wave >= n_mat * q.P || q.nrows <= 0) {
 #pragma unroll
         for (int k = 0; k < 8 * NA; k++) d.v[k] = undef_u32();
@@ -1118,7 +1121,7 @@ __device__ __forceinline__ bool ctl_wait(const PArgs& a, int p, int ln) {
 
 enum : int { kDN = 0, kATT = 1, kNONE = 2 };
 
-constexpr int kNDG = 5;              // gate/up instructions decoded before the input (registers)
+constexpr int kNDG = 4;              // gate/up instructions decoded before the input (registers)
 
 // Compute waves: first half of layer l's gate/up weights with its LUTs, the
 // pair tables, and the lookups of the first kNDG instructions -- none of it
@@ -1134,6 +1137,7 @@ __device__ __forceinline__ void gu_first(Buf<3 * NIG>& gb, LutRegs& glr, Buf<8 *
     trace_stamp(a, p, kTrX0, tw0);
     gemv_tables(glr, gu, 2, wave, ln, lds, ctl_ints(lds) + 8, gu.P * (l + 1));
     trace_stamp(a, p, kTrX1, tw0);
+    static_assert(kNDG <= NIG / 2, "decode-ahead covers the issued first half only");
     gemv_decode<NIG, kNDG>(gb, gd, gu, 2, wave, ln, lds);
     trace_stamp(a, p, kTrX2, tw0);
 }
@@ -1283,7 +1287,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     }
     wg_sync();   // the bulk loads below queue behind the arrival
     constexpr int NAD = NID / 2;     // weights issued before the barrier
-    constexpr int NDD = 5;           // of them decoded before the input
+    constexpr int NDD = NAD;         // of them decoded before the input (all that were issued)
     Buf<8 * NDD> dd;
     ln = opaque(lane);
     if (wave == kCtl) {
