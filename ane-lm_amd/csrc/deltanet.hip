@@ -316,162 +316,276 @@ __global__ __launch_bounds__(kScanNT) void dn_scan_kernel(float* y, float* state
 //                         P_ti = exp(lg_t - lg_i) (q_t . k_i), i <= t
 //   S_end = gC S0 + Kh^T U,  Kh = diag(exp(lg_L - lg)) K,  gC = exp(lg_L)
 // Everything but the three products with S0 is independent of the state and
-// is computed for all chunks at once (dn_chunk_pre_kernel); dn_chunk_seq_kernel
-// then carries the state through the chunks.  Decay ratios are formed in log
-// space (all exponents <= 0).  Rows past the sequence end are zero (beta 0,
-// log decay 0), so they change nothing.
+// is computed for all chunks at once (dn_chunk_prep_mfma_kernel), and
+// dn_chunk_mfma_kernel then carries the state through the chunks.  Decay
+// ratios are formed in log space (all exponents <= 0).  Rows past the
+// sequence end are zero (beta 0, log decay 0), so they change nothing.
 constexpr int kChunk = 64;
 constexpr int kCMat = kChunk * kDK;             // floats per chunk matrix
 constexpr int kCRec = 5 * kCMat + 64;           // Ut, Wm, Op, Qh, Kh, gC
-constexpr int kPreNT = 256;
-constexpr int kTS = kChunk + 4;                 // row stride of the transposed tiles
+
+// ------------------------------------------- chunk preparation on fp32 MFMA
+// The per-chunk matrices above, on v_mfma_f32_16x16x4_f32.
+// One workgroup (8 waves) per (chunk, key head); the key head's G = Hv / Hk
+// value heads share its key and query rows, so the Gram tiles K K^T and Q K^T
+// (the 10 lower 16x16 tiles of each) are computed once and kept in registers.
+// Per value head:
+//   Am = -A (strictly lower, row-major) and P (lower) go to LDS;
+//   wave 0 turns the diagonal 16x16 blocks of Am into T_rr = (I + A_rr)^-1
+//   by substitution, in place;
+//   B = [beta V | beta exp(lgT) K] (64 x 256) is stored transposed, and the
+//   blocked forward substitution and the product with P run per 16-column
+//   tile of B (wave w owns tiles 2w, 2w + 1):
+//     X_r = T_rr (B_r + sum_{s<r} Am_rs X_s),  Y_r = sum_{s<=r} P_rs X_s
+//   with X = [Ut | Wm] and Y = [Op | P Wm] (Qh = diag(exp(lg)) Q - P Wm).
+// MFMA operand layouts as in dn_chunk_mfma_kernel: A[m][k] in lane m + 16 k,
+// B[k][n] in lane n + 16 k, D[m][n] in lane n + 16 (m / 4), element m % 4.
+// The contraction index of k-step e is 4 k + e in both operands, so an A
+// operand is one 16-byte LDS read per lane for four MFMAs, and a result tile
+// in the D layout is already the B operand of the next product: X stays in
+// registers from its substitution to its product with P.
+// LDS matrices are row-major with 16-byte chunks XOR-swizzled by (row & 15).
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kPmNT = 512;
+constexpr int kPmK = 0;                        // K rows [64][128]
+constexpr int kPmR = kCMat;                    // Q rows [64][128] (Gram), then B^T [256][64]
+constexpr int kPmA = kPmR + 2 * kCMat;         // Am [64][64] (T_rr on its diagonal blocks)
+constexpr int kPmP = kPmA + kChunk * kChunk;   // P [64][64]
+constexpr int kPmLg = kPmP + kChunk * kChunk;  // lg[65] (+3 pad)
+constexpr int kPmBt = kPmLg + 68;              // beta[64]
+constexpr int kPmLds = (kPmBt + kChunk) * 4;
+
+__device__ __forceinline__ int sw128(int t, int d) { return t * kDK + 4 * ((d >> 2) ^ (t & 15)) + (d & 3); }
+__device__ __forceinline__ int sw64(int r, int c) { return r * kChunk + 4 * ((c >> 2) ^ (r & 15)) + (c & 3); }
 
 template <bool TF>
-__global__ __launch_bounds__(kPreNT, 2) void dn_chunk_pre_kernel(float* __restrict__ rec, const float* __restrict__ qn,
-                                                                  const float* __restrict__ kn,
-                                                                  const float* __restrict__ v,
-                                                                  const float* __restrict__ beta,
-                                                                  const float* __restrict__ ldecay, int S, int Hk,
-                                                                  int Hv) {
-    // K^T and Q^T tiles ([d][t]) for the dot products; afterwards the same
-    // space holds A and P ([t][i]), so two workgroups fit on a CU
-    __shared__ __attribute__((aligned(16))) float T0[kDK][kTS];
-    __shared__ __attribute__((aligned(16))) float T1[kDK][kTS];
-    __shared__ float lg[kChunk + 1];                                // lg[t + 1]; lg[0] = 0
-    __shared__ float bt[kChunk];
-    float (*KT)[kTS] = T0;
-    float (*QT)[kTS] = T1;
-    float (*Am)[kTS] = T0;   // rows 0..63 of T0, after the dot products
-    float (*Pm)[kTS] = T1;
-    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int kh = h / (Hv / Hk);
+__global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __restrict__ rec,
+                                                                   const float* __restrict__ qn,
+                                                                   const float* __restrict__ kn,
+                                                                   const float* __restrict__ v,
+                                                                   const float* __restrict__ beta,
+                                                                   const float* __restrict__ ldecay, int S,
+                                                                   int Hk, int Hv) {
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* Ks = sm + kPmK;
+    float* Rs = sm + kPmR;
+    float* Am = sm + kPmA;
+    float* Pm = sm + kPmP;
+    float* lg = sm + kPmLg;
+    float* bt = sm + kPmBt;
+    const int c = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lm = lane & 15, lk = lane >> 4;
+    const int G = Hv / Hk;
     const int t0 = c * kChunk, L = min(kChunk, S - t0);
+    // ---- key and query rows of the chunk (zero past the sequence end)
     {
-        // all 64 loads of this thread in flight together, then the transposed stores
-        constexpr int NE = kCMat / kPreNT;
-        float kv[NE], qv[NE];
+        float4 kv[4], qv[4];
 #pragma unroll
-        for (int k = 0; k < NE; k++) {
-            const int e = tid + kPreNT * k, t = e / kDK, d = e - t * kDK;
-            const size_t off = ((size_t)(t0 + min(t, L - 1)) * Hk + kh) * kDK + d;
-            kv[k] = kn[off];
-            qv[k] = qn[off];
+        for (int x = 0; x < 4; x++) {
+            const int e = tid + kPmNT * x, t = e >> 5, ch = e & 31;
+            const size_t off = ((size_t)(t0 + min(t, L - 1)) * Hk + kh) * kDK + 4 * ch;
+            kv[x] = *reinterpret_cast<const float4*>(kn + off);
+            qv[x] = *reinterpret_cast<const float4*>(qn + off);
         }
 #pragma unroll
-        for (int k = 0; k < NE; k++) {
-            const int e = tid + kPreNT * k, t = e / kDK, d = e - t * kDK;
-            KT[d][t] = t < L ? kv[k] : 0.f;
-            QT[d][t] = t < L ? qv[k] : 0.f;
-        }
-    }
-    if (tid < kChunk) bt[tid] = tid < L ? beta[(size_t)(t0 + tid) * Hv + h] : 0.f;
-    if (tid == 0) {
-        float acc = 0.f;
-        lg[0] = 0.f;
-        for (int t = 0; t < kChunk; t++) {
-            if (t < L) acc += ldecay[(size_t)(t0 + t) * Hv + h];
-            lg[t + 1] = acc;
+        for (int x = 0; x < 4; x++) {
+            const int e = tid + kPmNT * x, t = e >> 5, ch = e & 31;
+            const float m = t < L ? 1.f : 0.f;
+            *reinterpret_cast<float4*>(Ks + sw128(t, 4 * ch)) =
+                make_float4(kv[x].x * m, kv[x].y * m, kv[x].z * m, kv[x].w * m);
+            *reinterpret_cast<float4*>(Rs + sw128(t, 4 * ch)) =
+                make_float4(qv[x].x * m, qv[x].y * m, qv[x].z * m, qv[x].w * m);
         }
     }
-    __syncthreads();
-    // k_t . k_i and q_t . k_i for 4x4 blocks with i <= t
-    const int tb = tid >> 4, ib = tid & 15;
-    float kk[4][4], qk[4][4];
+    lds_barrier();
+    // ---- Gram tiles: 10 lower tiles of K K^T (ids 0..9) and of Q K^T (10..19);
+    // wave w takes ids w, w + 8, w + 16
+    v4f gram[3];
 #pragma unroll
-    for (int x = 0; x < 4; x++)
+    for (int u = 0; u < 3; u++) {
+        const int id = w + 8 * u;
+        gram[u] = v4f{0.f, 0.f, 0.f, 0.f};
+        if (id >= 20) continue;
+        const int pi = id % 10, ti = (pi >= 1) + (pi >= 3) + (pi >= 6), tj = pi - ti * (ti + 1) / 2;
+        const float* src = id < 10 ? Ks : Rs;
+        v4f a0 = gram[u], a1 = gram[u];
 #pragma unroll
-        for (int y = 0; y < 4; y++) kk[x][y] = qk[x][y] = 0.f;
-    if (ib <= tb) {
-#pragma unroll 4
-        for (int d = 0; d < kDK; d++) {
-            const float4 kt = *reinterpret_cast<const float4*>(&KT[d][4 * tb]);
-            const float4 ki = *reinterpret_cast<const float4*>(&KT[d][4 * ib]);
-            const float4 qt = *reinterpret_cast<const float4*>(&QT[d][4 * tb]);
-            const float a4[4] = {kt.x, kt.y, kt.z, kt.w}, b4[4] = {ki.x, ki.y, ki.z, ki.w};
-            const float q4[4] = {qt.x, qt.y, qt.z, qt.w};
+        for (int x = 0; x < 8; x++) {
+            const float4 a4 = *reinterpret_cast<const float4*>(src + sw128(16 * ti + lm, 16 * x + 4 * lk));
+            const float4 b4 = *reinterpret_cast<const float4*>(Ks + sw128(16 * tj + lm, 16 * x + 4 * lk));
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, a1, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, a1, 0, 0, 0);
+        }
+        gram[u] = a0 + a1;
+        __builtin_amdgcn_sched_barrier(0);   // one tile's operands live at a time
+    }
+    lds_barrier();   // the query rows are no longer read: their space takes B^T
+    // rows past the sequence end fall outside these ranges and load as zeros
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(v), 0,
+                                                                         (int)((size_t)S * Hv * kDV * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(qn), 0,
+                                                                         (int)((size_t)S * Hk * kDK * 4), 0x00020000);
+    for (int g = 0; g < G; g++) {
+        const int h = kh * G + g;
+        float* out = rec + ((size_t)c * Hv + h) * kCRec;
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, kCRec * 4, 0x00020000);
+        // lane-derived addresses are recomputed per value head, not held across the loop
+        int ltid = tid;
+        asm volatile("" : "+v"(ltid));
+        const int lane = ltid & 63, lm = lane & 15, lk = lane >> 4;
+        // ---- lg[t + 1] = sum_{j <= t} log decay_j, beta (wave 0)
+        if (w == 0) {
+            const bool in = lane < L;
+            float x = in ? ldecay[(size_t)(t0 + lane) * Hv + h] : 0.f;
 #pragma unroll
-            for (int x = 0; x < 4; x++)
+            for (int d = 1; d < 64; d <<= 1) {
+                const float y = __shfl_up(x, d, 64);
+                if (lane >= d) x += y;
+            }
+            lg[lane + 1] = x;
+            if (lane == 0) lg[0] = 0.f;
+            bt[lane] = in ? beta[(size_t)(t0 + lane) * Hv + h] : 0.f;
+        }
+        lds_barrier();
+        // ---- Am = -A and P from the Gram tiles
 #pragma unroll
-                for (int y = 0; y < 4; y++) {
-                    kk[x][y] = fmaf(a4[x], b4[y], kk[x][y]);
-                    qk[x][y] = fmaf(q4[x], b4[y], qk[x][y]);
+        for (int u = 0; u < 3; u++) {
+            const int id = w + 8 * u;
+            if (id >= 20) continue;
+            const int pi = id % 10, ti = (pi >= 1) + (pi >= 3) + (pi >= 6), tj = pi - ti * (ti + 1) / 2;
+            const int i = 16 * tj + lm;
+            const float lgi = lg[i + 1];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = 16 * ti + 4 * lk + e;
+                if (id < 10) {
+                    const float lgT = TF ? lg[t + 1] : lg[t];
+                    Am[sw64(t, i)] = i < t ? -(bt[t] * expf(lgT - lgi) * gram[u][e]) : 0.f;
+                } else {
+                    Pm[sw64(t, i)] = i <= t ? expf(lg[t + 1] - lgi) * gram[u][e] : 0.f;
                 }
+            }
         }
-    }
-    __syncthreads();   // the tiles are overwritten by A and P below
+        // ---- B^T: row col < 128 is beta V[., col]; row 128 + d is beta exp(lgT) K[., d]
 #pragma unroll
-    for (int x = 0; x < 4; x++) {
-        const int t = 4 * tb + x;
-        const float lgT = TF ? lg[t + 1] : lg[t];
+        for (int x = 0; x < 8; x++) {
+            const int e = ltid + kPmNT * x, col = e & 255, tq = e >> 8;
+            float b4[4];
 #pragma unroll
-        for (int y = 0; y < 4; y++) {
-            const int i = 4 * ib + y;
-            Am[t][i] = i < t ? bt[t] * expf(lgT - lg[i + 1]) * kk[x][y] : 0.f;
-            Pm[t][i] = i <= t ? expf(lg[t + 1] - lg[i + 1]) * qk[x][y] : 0.f;
+            for (int j = 0; j < 4; j++) {
+                const int t = 4 * tq + j;
+                float val;
+                if (col < kDV) {
+                    val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                        rv, (((t0 + t) * Hv + h) * kDV + col) * 4, 0, 0));
+                } else {
+                    val = Ks[sw128(t, col - kDV)] * expf(TF ? lg[t + 1] : lg[t]);
+                }
+                b4[j] = bt[t] * val;
+            }
+            *reinterpret_cast<float4*>(Rs + sw64(col, 4 * tq)) = make_float4(b4[0], b4[1], b4[2], b4[3]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-    __syncthreads();
-    // thread j < 128: column j of Ut (right-hand side beta V), then Op = P Ut;
-    // thread j >= 128: column j-128 of Wm (beta exp(lg) K), then Qh = exp(lg) Q - P Wm
-    const int j = tid & (kDK - 1);
-    const bool wpart = tid >= kDK;
-    float* out = rec + ((size_t)c * Hv + h) * kCRec;
-    const float* src = wpart ? kn : v;
-    float u[kChunk];
-    // right-hand sides first (all global loads in flight together), then the
-    // forward substitution in place
+        lds_barrier();
+        if (w == 0) {
+            // ---- T_rr = (I + A_rr)^-1 for the 4 diagonal blocks: lane 16 b + j
+            // computes column j of block b by substitution, then writes it over A_rr
+            const int b = lk, j = lm;
+            float x[16];
 #pragma unroll
-    for (int t = 0; t < kChunk; t++) {
-        const size_t off = wpart ? ((size_t)(t0 + min(t, L - 1)) * Hk + kh) * kDK + j
-                                 : ((size_t)(t0 + min(t, L - 1)) * Hv + h) * kDV + j;
-        u[t] = src[off];
-    }
+            for (int t = 0; t < 16; t++) {
+                float acc = t == j ? 1.f : 0.f;
 #pragma unroll
-    for (int t = 0; t < kChunk; t++) {
-        const float scale = t < L ? bt[t] * (wpart ? expf(TF ? lg[t + 1] : lg[t]) : 1.0f) : 0.f;
-        // four partial sums (shorter dependency chains); A row t read as
-        // float4s (same address in every lane: LDS broadcast)
-        float b0 = u[t] * scale, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+                for (int i4 = 0; i4 < t; i4 += 4) {
+                    const float4 a4 = *reinterpret_cast<const float4*>(Am + sw64(16 * b + t, 16 * b + i4));
+                    acc = fmaf(a4.x, x[i4], acc);
+                    if (i4 + 1 < t) acc = fmaf(a4.y, x[i4 + 1], acc);
+                    if (i4 + 2 < t) acc = fmaf(a4.z, x[i4 + 2], acc);
+                    if (i4 + 3 < t) acc = fmaf(a4.w, x[i4 + 3], acc);
+                }
+                x[t] = acc;
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
-        for (int i4 = 0; i4 < t; i4 += 4) {
-            const float4 a4 = *reinterpret_cast<const float4*>(&Am[t][i4]);
-            b0 = fmaf(-a4.x, u[i4], b0);
-            if (i4 + 1 < t) b1 = fmaf(-a4.y, u[i4 + 1], b1);
-            if (i4 + 2 < t) b2 = fmaf(-a4.z, u[i4 + 2], b2);
-            if (i4 + 3 < t) b3 = fmaf(-a4.w, u[i4 + 3], b3);
+            for (int t = 0; t < 16; t++) Am[sw64(16 * b + t, 16 * b + j)] = x[t];
+        } else {
+            // ---- Kh = diag(exp(lg_L - lg)) K, gC (waves 1..7)
+            const float lgL = lg[kChunk];
+            for (int e = ltid - 64; e < kCMat / 4; e += kPmNT - 64) {
+                const int t = e >> 5, ch = e & 31;
+                const float sc = expf(lgL - lg[t + 1]);
+                const float4 k4 = *reinterpret_cast<const float4*>(Ks + sw128(t, 4 * ch));
+                const float4 o4 = make_float4(k4.x * sc, k4.y * sc, k4.z * sc, k4.w * sc);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o4), ro,
+                                                       (4 * kCMat + t * kDK + 4 * ch) * 4, 0, 0);
+            }
+            if (ltid == 64)
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, expf(lgL)), ro, 5 * kCMat * 4, 0, 0);
         }
-        u[t] = (b0 + b1) + (b2 + b3);
-        // row t is finished here (the data dependency keeps its arithmetic
-        // before this point) and the next rows' loads stay after it
-        asm volatile("" : "+v"(u[t]) :: "memory");
-    }
-    float* mu = out + (wpart ? kCMat : 0);              // Ut or Wm
-    float* mr = out + (wpart ? 3 * kCMat : 2 * kCMat);  // Op or Qh
-    float* kh_out = out + 4 * kCMat;
-    const float lgL = lg[kChunk];
+        lds_barrier();
+        // ---- X and Y for column tiles jt = 2w + u of B
+        v4f X[2][4];
 #pragma unroll
-    for (int t = 0; t < kChunk; t++) {
-        float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+        for (int r = 0; r < 4; r++) {
 #pragma unroll
-        for (int i4 = 0; i4 <= t; i4 += 4) {
-            const float4 p4 = *reinterpret_cast<const float4*>(&Pm[t][i4]);
-            r0 = fmaf(p4.x, u[i4], r0);
-            if (i4 + 1 <= t) r1 = fmaf(p4.y, u[i4 + 1], r1);
-            if (i4 + 2 <= t) r2 = fmaf(p4.z, u[i4 + 2], r2);
-            if (i4 + 3 <= t) r3 = fmaf(p4.w, u[i4 + 3], r3);
+            for (int u = 0; u < 2; u++) {
+                const int jt = 2 * w + u;
+                const float4 c4 = *reinterpret_cast<const float4*>(Rs + sw64(16 * jt + lm, 16 * r + 4 * lk));
+                v4f acc = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                for (int s2 = 0; s2 < r; s2++) {
+                    const float4 a4 = *reinterpret_cast<const float4*>(Am + sw64(16 * r + lm, 16 * s2 + 4 * lk));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, X[u][s2][0], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, X[u][s2][1], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, X[u][s2][2], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, X[u][s2][3], acc, 0, 0, 0);
+                }
+                const float4 t4 = *reinterpret_cast<const float4*>(Am + sw64(16 * r + lm, 16 * r + 4 * lk));
+                v4f xr = {0.f, 0.f, 0.f, 0.f};
+                xr = __builtin_amdgcn_mfma_f32_16x16x4f32(t4.x, acc[0], xr, 0, 0, 0);
+                xr = __builtin_amdgcn_mfma_f32_16x16x4f32(t4.y, acc[1], xr, 0, 0, 0);
+                xr = __builtin_amdgcn_mfma_f32_16x16x4f32(t4.z, acc[2], xr, 0, 0, 0);
+                xr = __builtin_amdgcn_mfma_f32_16x16x4f32(t4.w, acc[3], xr, 0, 0, 0);
+                X[u][r] = xr;
+                // Y_r = sum_{s <= r} P_rs X_s
+                v4f y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s2 = 0; s2 <= r; s2++) {
+                    const float4 p4 = *reinterpret_cast<const float4*>(Pm + sw64(16 * r + lm, 16 * s2 + 4 * lk));
+                    y = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.x, X[u][s2][0], y, 0, 0, 0);
+                    y = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.y, X[u][s2][1], y, 0, 0, 0);
+                    y = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.z, X[u][s2][2], y, 0, 0, 0);
+                    y = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.w, X[u][s2][3], y, 0, 0, 0);
+                }
+                // rows t = 16 r + 4 lk + e, column 16 (jt % 8) + lm of Ut / Wm and Op / Qh
+                const int col = 16 * (jt & 7) + lm;
+                const bool wpart = jt >= 8;
+                const int ox = wpart ? kCMat : 0, oy = wpart ? 3 * kCMat : 2 * kCMat;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 16 * r + 4 * lk + e;
+                    // through a scalar: a bit_cast of a vector element is lowered as element 0
+                    const float xv = xr[e];
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ro, (ox + t * kDK + col) * 4,
+                                                          0, 0);
+                    float yv = y[e];
+                    if (wpart) {
+                        const float qv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                       rq, (((t0 + t) * Hk + kh) * kDK + col) * 4, 0, 0));
+                        yv = expf(lg[t + 1]) * qv - yv;
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv), ro, (oy + t * kDK + col) * 4,
+                                                          0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // bounds the loads hoisted ahead of this tile
+            }
         }
-        float r = (r0 + r1) + (r2 + r3);
-        mu[t * kDK + j] = u[t];
-        if (wpart) {
-            const size_t off = ((size_t)(t0 + min(t, L - 1)) * Hk + kh) * kDK + j;
-            const float qv = t < L ? qn[off] : 0.f, kv = t < L ? kn[off] : 0.f;
-            r = expf(lg[t + 1]) * qv - r;
-            kh_out[t * kDK + j] = expf(lgL - lg[t + 1]) * kv;
-        }
-        mr[t * kDK + j] = r;
-        asm volatile("" : "+v"(r) :: "memory");
+        lds_barrier();   // B^T, Am, P, lg and beta are rewritten for the next value head
     }
-    if (tid == 0) out[5 * kCMat] = expf(lgL);
 }
 
 // Sequential part: workgroup (slab of 16 state columns, value head) keeps its
@@ -498,7 +612,6 @@ constexpr int kSlabs = kDV / kSeqCB;
 // operands from LDS into registers.  Wm / Qh rows are stored with their
 // 16-byte chunks XOR-swizzled by the row (conflict-free operand reads).
 constexpr int kMsNT = 256;
-typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kScP = kDK + 4;                      // Sc row pitch (floats)
 constexpr int kOpWm = 0, kOpQh = kCMat, kOpKh = 2 * kCMat;   // operand buffer (floats)
 constexpr int kOpUt = 3 * kCMat, kOpOp = 3 * kCMat + kChunk * 16;
@@ -834,13 +947,21 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
         ANELM_LAUNCHED("dn_scan_kernel");
         return ANELM_OK;
     }
+    static bool pm_attr = false;
+    if (!pm_attr) {
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&dn_chunk_prep_mfma_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPmLds));
+        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&dn_chunk_prep_mfma_kernel<false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPmLds));
+        pm_attr = true;
+    }
     if (flags & ANELM_DN_ORDER_TRANSFORMERS)
-        hipLaunchKernelGGL(dn_chunk_pre_kernel<true>, dim3(n_chunks, Hv), dim3(kPreNT), 0, st, rec, qn, kn,
-                           v, beta, ldecay, S, Hk, Hv);
+        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<true>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, qn,
+                           kn, v, beta, ldecay, S, Hk, Hv);
     else
-        hipLaunchKernelGGL(dn_chunk_pre_kernel<false>, dim3(n_chunks, Hv), dim3(kPreNT), 0, st, rec, qn, kn,
-                           v, beta, ldecay, S, Hk, Hv);
-    ANELM_LAUNCHED("dn_chunk_pre_kernel");
+        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<false>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, qn,
+                           kn, v, beta, ldecay, S, Hk, Hv);
+    ANELM_LAUNCHED("dn_chunk_prep_mfma_kernel");
     // grid = Hv * kSlabs, a multiple of 8 (XCD mapping inside the kernel)
     static bool ms_attr = false;
     if (!ms_attr) {
