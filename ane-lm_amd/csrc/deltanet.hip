@@ -333,9 +333,10 @@ constexpr int kCRec = 5 * kCMat + 64;           // Ut, Wm, Op, Qh, Kh, gC
 //   Am = -A (strictly lower, row-major) and P (lower) go to LDS;
 //   wave 0 turns the diagonal 16x16 blocks of Am into T_rr = (I + A_rr)^-1
 //   by substitution, in place;
-//   B = [beta V | beta exp(lgT) K] (64 x 256) is stored transposed, and the
-//   blocked forward substitution and the product with P run per 16-column
-//   tile of B (wave w owns tiles 2w, 2w + 1):
+//   for B = [beta V | beta exp(lgT) K] (64 x 256) the blocked forward
+//   substitution and the product with P run per 16-column tile of B (wave w
+//   owns tiles 2w, 2w + 1; it loads its tiles of B straight into the
+//   accumulator layout: V columns from memory, K columns from LDS):
 //     X_r = T_rr (B_r + sum_{s<r} Am_rs X_s),  Y_r = sum_{s<=r} P_rs X_s
 //   with X = [Ut | Wm] and Y = [Op | P Wm] (Qh = diag(exp(lg)) Q - P Wm).
 // MFMA operand layouts as in dn_chunk_mfma_kernel: A[m][k] in lane m + 16 k,
@@ -344,15 +345,16 @@ constexpr int kCRec = 5 * kCMat + 64;           // Ut, Wm, Op, Qh, Kh, gC
 // operand is one 16-byte LDS read per lane for four MFMAs, and a result tile
 // in the D layout is already the B operand of the next product: X stays in
 // registers from its substitution to its product with P.
-// LDS matrices are row-major with 16-byte chunks XOR-swizzled by (row & 15).
+// LDS matrices are row-major with 16-byte chunks XOR-swizzled by (row & 15);
+// 66 KB, so two workgroups share a CU (one's serial phases overlap the other).
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kPmNT = 512;
 constexpr int kPmK = 0;                        // K rows [64][128]
-constexpr int kPmR = kCMat;                    // Q rows [64][128] (Gram), then B^T [256][64]
-constexpr int kPmA = kPmR + 2 * kCMat;         // Am [64][64] (T_rr on its diagonal blocks)
-constexpr int kPmP = kPmA + kChunk * kChunk;   // P [64][64]
-constexpr int kPmLg = kPmP + kChunk * kChunk;  // lg[65] (+3 pad)
+constexpr int kPmR = kCMat;                    // Q rows [64][128] for the Gram tiles, then:
+constexpr int kPmA = kPmR;                     //   Am [64][64] (T_rr on its diagonal blocks)
+constexpr int kPmP = kPmA + kChunk * kChunk;   //   P [64][64]
+constexpr int kPmLg = kPmR + kCMat;            // lg[65] (+3 pad)
 constexpr int kPmBt = kPmLg + 68;              // beta[64]
 constexpr int kPmLds = (kPmBt + kChunk) * 4;
 
@@ -360,7 +362,7 @@ __device__ __forceinline__ int sw128(int t, int d) { return t * kDK + 4 * ((d >>
 __device__ __forceinline__ int sw64(int r, int c) { return r * kChunk + 4 * ((c >> 2) ^ (r & 15)) + (c & 3); }
 
 template <bool TF>
-__global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __restrict__ rec,
+__global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __restrict__ rec,
                                                                    const float* __restrict__ qn,
                                                                    const float* __restrict__ kn,
                                                                    const float* __restrict__ v,
@@ -423,7 +425,7 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
         gram[u] = a0 + a1;
         __builtin_amdgcn_sched_barrier(0);   // one tile's operands live at a time
     }
-    lds_barrier();   // the query rows are no longer read: their space takes B^T
+    lds_barrier();   // the query rows are no longer read: their space takes Am and P
     // rows past the sequence end fall outside these ranges and load as zeros
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(v), 0,
                                                                          (int)((size_t)S * Hv * kDV * 4), 0x00020000);
@@ -437,6 +439,21 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
         int ltid = tid;
         asm volatile("" : "+v"(ltid));
         const int lane = ltid & 63, lm = lane & 15, lk = lane >> 4;
+        // this wave's memory operands, issued first: V rows of its B tiles
+        // (waves 0..3, tiles 0..7) or the q rows of its Qh tiles (waves 4..7)
+        const bool wpart = w >= 4;
+        float pre[2][4][4];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 16 * r + 4 * lk + e, col = 16 * ((2 * w + u) & 7) + lm;
+                    const int off = wpart ? ((t0 + t) * Hk + kh) * kDK + col : ((t0 + t) * Hv + h) * kDV + col;
+                    pre[u][r][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wpart ? rq : rv,
+                                                                                                 off * 4, 0, 0));
+                }
         // ---- lg[t + 1] = sum_{j <= t} log decay_j, beta (wave 0)
         if (w == 0) {
             const bool in = lane < L;
@@ -469,26 +486,6 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
                     Pm[sw64(t, i)] = i <= t ? expf(lg[t + 1] - lgi) * gram[u][e] : 0.f;
                 }
             }
-        }
-        // ---- B^T: row col < 128 is beta V[., col]; row 128 + d is beta exp(lgT) K[., d]
-#pragma unroll
-        for (int x = 0; x < 8; x++) {
-            const int e = ltid + kPmNT * x, col = e & 255, tq = e >> 8;
-            float b4[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int t = 4 * tq + j;
-                float val;
-                if (col < kDV) {
-                    val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                        rv, (((t0 + t) * Hv + h) * kDV + col) * 4, 0, 0));
-                } else {
-                    val = Ks[sw128(t, col - kDV)] * expf(TF ? lg[t + 1] : lg[t]);
-                }
-                b4[j] = bt[t] * val;
-            }
-            *reinterpret_cast<float4*>(Rs + sw64(col, 4 * tq)) = make_float4(b4[0], b4[1], b4[2], b4[3]);
-            __builtin_amdgcn_sched_barrier(0);
         }
         lds_barrier();
         if (w == 0) {
@@ -534,8 +531,14 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 const int jt = 2 * w + u;
-                const float4 c4 = *reinterpret_cast<const float4*>(Rs + sw64(16 * jt + lm, 16 * r + 4 * lk));
-                v4f acc = {c4.x, c4.y, c4.z, c4.w};
+                // B_r of this tile in the accumulator layout: rows 16 r + 4 lk + e, column lm
+                v4f acc;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 16 * r + 4 * lk + e;
+                    acc[e] = bt[t] * (wpart ? Ks[sw128(t, 16 * (jt - 8) + lm)] * expf(TF ? lg[t + 1] : lg[t])
+                                            : pre[u][r][e]);
+                }
 #pragma unroll
                 for (int s2 = 0; s2 < r; s2++) {
                     const float4 a4 = *reinterpret_cast<const float4*>(Am + sw64(16 * r + lm, 16 * s2 + 4 * lk));
@@ -563,7 +566,6 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
                 }
                 // rows t = 16 r + 4 lk + e, column 16 (jt % 8) + lm of Ut / Wm and Op / Qh
                 const int col = 16 * (jt & 7) + lm;
-                const bool wpart = jt >= 8;
                 const int ox = wpart ? kCMat : 0, oy = wpart ? 3 * kCMat : 2 * kCMat;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -573,18 +575,14 @@ __global__ __launch_bounds__(kPmNT) void dn_chunk_prep_mfma_kernel(float* __rest
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ro, (ox + t * kDK + col) * 4,
                                                           0, 0);
                     float yv = y[e];
-                    if (wpart) {
-                        const float qv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                       rq, (((t0 + t) * Hk + kh) * kDK + col) * 4, 0, 0));
-                        yv = expf(lg[t + 1]) * qv - yv;
-                    }
+                    if (wpart) yv = expf(lg[t + 1]) * pre[u][r][e] - yv;
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv), ro, (oy + t * kDK + col) * 4,
                                                           0, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);   // bounds the loads hoisted ahead of this tile
             }
         }
-        lds_barrier();   // B^T, Am, P, lg and beta are rewritten for the next value head
+        lds_barrier();   // Am, P, lg and beta are rewritten for the next value head
     }
 }
 
