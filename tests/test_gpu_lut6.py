@@ -112,6 +112,13 @@ def test_gemm_accumulate_and_batched_ffn(anelm, orc, dev):
     assert_close(to_host(yd)[3], y0[3] + orc.lut6_matvec(pk, lut, xs[3], 1024, 2560), what="accumulate")
 
 
+# Rows of the seeded full-size cases whose oracle top-k has two neighbours
+# closer than the fp32 summation-order bar (row 31 of the 32-row batch: gap
+# 1.4e-5 against a bar of 4.8e-5); every other full-size row checked is
+# tie-free, so its indices are compared exactly.
+_FULL_SIZE_NEAR_TIES = {(32, 31)}
+
+
 def _check_topk(orc, idx, val, logits, k):
     """Indices bit-exact against the oracle's top-k of the oracle logits
     wherever neighbouring values are separated by more than the fp32
@@ -152,7 +159,10 @@ def test_topk(anelm, orc, dev, out_dim, in_dim, batch, k):
         assert np.array_equal(val[b], ov), f"row {b}: selected values differ"
         logits = orc.lut6_matvec(packed, lut, x[b], out_dim, in_dim)
         assert_close(gpu_logits[b], logits, rel=1e-5, max_abs=1e-4, what=f"row {b} logits")
-        _check_topk(orc, idx[b], val[b], logits, k)
+        exact = _check_topk(orc, idx[b], val[b], logits, k)
+        if out_dim == 262144 and (batch, b) not in _FULL_SIZE_NEAR_TIES:
+            # seeded full-size rows: the indices must match the oracle's exactly
+            assert exact, f"row {b}: expected a tie-free top-{k} at this seed"
         if k == 1:
             assert idx[b, 0] == orc.argmax(gpu_logits[b])
 
