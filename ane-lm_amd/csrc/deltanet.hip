@@ -325,7 +325,10 @@ constexpr int kCMat = kChunk * kDK;             // floats per chunk matrix
 constexpr int kCRec = 5 * kCMat + 64;           // Ut, Wm, Op, Qh, Kh, gC
 
 // ------------------------------------------- chunk preparation on fp32 MFMA
-// The per-chunk matrices above, on v_mfma_f32_16x16x4_f32.
+// The per-chunk matrices above, on v_mfma_f32_16x16x4_f32, from the raw
+// inputs: the pre-pass of the token scan (dn_prep_kernel: l2 norm and q scale,
+// beta, log decay) is folded in, so q and k are read once and nothing is
+// staged through memory.
 // One workgroup (8 waves) per (chunk, key head); the key head's G = Hv / Hk
 // value heads share its key and query rows, so the Gram tiles K K^T and Q K^T
 // (the 10 lower 16x16 tiles of each) are computed once and kept in registers.
@@ -356,19 +359,17 @@ constexpr int kPmA = kPmR;                     //   Am [64][64] (T_rr on its dia
 constexpr int kPmP = kPmA + kChunk * kChunk;   //   P [64][64]
 constexpr int kPmLg = kPmR + kCMat;            // lg[65] (+3 pad)
 constexpr int kPmBt = kPmLg + 68;              // beta[64]
-constexpr int kPmLds = (kPmBt + kChunk) * 4;
+constexpr int kPmQs = kPmBt + kChunk;          // q row scale[64] (l2 norm and 1/sqrt(dk))
+constexpr int kPmLds = (kPmQs + kChunk) * 4;
 
 __device__ __forceinline__ int sw128(int t, int d) { return t * kDK + 4 * ((d >> 2) ^ (t & 15)) + (d & 3); }
 __device__ __forceinline__ int sw64(int r, int c) { return r * kChunk + 4 * ((c >> 2) ^ (r & 15)) + (c & 3); }
 
 template <bool TF>
-__global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __restrict__ rec,
-                                                                   const float* __restrict__ qn,
-                                                                   const float* __restrict__ kn,
-                                                                   const float* __restrict__ v,
-                                                                   const float* __restrict__ beta,
-                                                                   const float* __restrict__ ldecay, int S,
-                                                                   int Hk, int Hv) {
+__global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
+    float* __restrict__ rec, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ A,
+    const float* __restrict__ dt_bias, int S, int Hk, int Hv, int flags) {
     extern __shared__ __attribute__((aligned(16))) float sm[];
     float* Ks = sm + kPmK;
     float* Rs = sm + kPmR;
@@ -376,29 +377,46 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
     float* Pm = sm + kPmP;
     float* lg = sm + kPmLg;
     float* bt = sm + kPmBt;
+    float* qs = sm + kPmQs;
     const int c = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lm = lane & 15, lk = lane >> 4;
     const int G = Hv / Hk;
     const int t0 = c * kChunk, L = min(kChunk, S - t0);
-    // ---- key and query rows of the chunk (zero past the sequence end)
+    // ---- key and query rows of the chunk, l2-normalised (qwen3_5.cpp:879-887),
+    // q also scaled by 1/sqrt(dk); zero past the sequence end.  A row is 32
+    // float4 chunks held by 32 consecutive lanes (half a wave)
     {
         float4 kv[4], qv[4];
 #pragma unroll
         for (int x = 0; x < 4; x++) {
             const int e = tid + kPmNT * x, t = e >> 5, ch = e & 31;
             const size_t off = ((size_t)(t0 + min(t, L - 1)) * Hk + kh) * kDK + 4 * ch;
-            kv[x] = *reinterpret_cast<const float4*>(kn + off);
-            qv[x] = *reinterpret_cast<const float4*>(qn + off);
+            kv[x] = *reinterpret_cast<const float4*>(k + off);
+            qv[x] = *reinterpret_cast<const float4*>(q + off);
         }
+        const float qk_scale = 1.0f / sqrtf((float)kDK);
 #pragma unroll
         for (int x = 0; x < 4; x++) {
             const int e = tid + kPmNT * x, t = e >> 5, ch = e & 31;
-            const float m = t < L ? 1.f : 0.f;
+            float ik = 1.f, iq = 1.f;
+            if (flags & ANELM_DN_L2NORM) {
+                float sk = kv[x].x * kv[x].x + kv[x].y * kv[x].y + kv[x].z * kv[x].z + kv[x].w * kv[x].w;
+                float sq = qv[x].x * qv[x].x + qv[x].y * qv[x].y + qv[x].z * qv[x].z + qv[x].w * qv[x].w;
+#pragma unroll
+                for (int m = 1; m < 32; m <<= 1) {
+                    sk += __shfl_xor(sk, m, 64);
+                    sq += __shfl_xor(sq, m, 64);
+                }
+                ik = 1.0f / sqrtf(sk + 1e-12f);
+                iq = 1.0f / sqrtf(sq + 1e-12f);
+            }
+            const float mk = t < L ? ik : 0.f, mq = t < L ? iq * qk_scale : 0.f;
             *reinterpret_cast<float4*>(Ks + sw128(t, 4 * ch)) =
-                make_float4(kv[x].x * m, kv[x].y * m, kv[x].z * m, kv[x].w * m);
+                make_float4(kv[x].x * mk, kv[x].y * mk, kv[x].z * mk, kv[x].w * mk);
             *reinterpret_cast<float4*>(Rs + sw128(t, 4 * ch)) =
-                make_float4(qv[x].x * m, qv[x].y * m, qv[x].z * m, qv[x].w * m);
+                make_float4(qv[x].x * mq, qv[x].y * mq, qv[x].z * mq, qv[x].w * mq);
+            if (ch == 0) qs[t] = mq;
         }
     }
     lds_barrier();
@@ -429,7 +447,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
     // rows past the sequence end fall outside these ranges and load as zeros
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(v), 0,
                                                                          (int)((size_t)S * Hv * kDV * 4), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(qn), 0,
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(q), 0,
                                                                          (int)((size_t)S * Hk * kDK * 4), 0x00020000);
     for (int g = 0; g < G; g++) {
         const int h = kh * G + g;
@@ -440,7 +458,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
         asm volatile("" : "+v"(ltid));
         const int lane = ltid & 63, lm = lane & 15, lk = lane >> 4;
         // this wave's memory operands, issued first: V rows of its B tiles
-        // (waves 0..3, tiles 0..7) or the q rows of its Qh tiles (waves 4..7)
+        // (waves 0..3, tiles 0..7) or the raw q rows of its Qh tiles (waves 4..7)
         const bool wpart = w >= 4;
         float pre[2][4][4];
 #pragma unroll
@@ -454,10 +472,16 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
                     pre[u][r][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wpart ? rq : rv,
                                                                                                  off * 4, 0, 0));
                 }
-        // ---- lg[t + 1] = sum_{j <= t} log decay_j, beta (wave 0)
+        // ---- beta = sigmoid(b) and log decay = -A softplus(a + dt_bias)
+        // (qwen3_5.cpp:896-898); lg[t + 1] = sum_{j <= t} log decay_j (wave 0)
         if (w == 0) {
             const bool in = lane < L;
-            float x = in ? ldecay[(size_t)(t0 + lane) * Hv + h] : 0.f;
+            float x = 0.f, bv = 0.f;
+            if (in) {
+                const size_t gi = (size_t)(t0 + lane) * Hv + h;
+                bv = 1.0f / (1.0f + expf(-b[gi]));
+                x = -A[h] * logf(1.0f + expf(a[gi] + dt_bias[h]));
+            }
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
                 const float y = __shfl_up(x, d, 64);
@@ -465,7 +489,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
             }
             lg[lane + 1] = x;
             if (lane == 0) lg[0] = 0.f;
-            bt[lane] = in ? beta[(size_t)(t0 + lane) * Hv + h] : 0.f;
+            bt[lane] = bv;
         }
         lds_barrier();
         // ---- Am = -A and P from the Gram tiles
@@ -575,7 +599,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(float* __r
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ro, (ox + t * kDK + col) * 4,
                                                           0, 0);
                     float yv = y[e];
-                    if (wpart) yv = expf(lg[t + 1]) * pre[u][r][e] - yv;
+                    if (wpart) yv = expf(lg[t + 1]) * (qs[t] * pre[u][r][e]) - yv;
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv), ro, (oy + t * kDK + col) * 4,
                                                           0, 0);
                 }
@@ -924,27 +948,26 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
     ANELM_REQUIRE((flags & ~3) == 0, "deltanet_prefill: flags 0x%x (GATED_NORM is decode-only)", flags);
     if (S == 0) return ANELM_OK;
     hipStream_t st = as_stream(stream);
-    const size_t nqk = (size_t)S * Hk * kDK, ng = (size_t)S * Hv;
-    const int n_chunks = (S + kChunk - 1) / kChunk;
-    const size_t nrec = chunk == kChunk ? (size_t)n_chunks * Hv * kCRec : 0;
-    const size_t rec_off = (2 * nqk + 3 * ng + 63) & ~(size_t)63;   // 256-byte aligned records
-    float* ws = static_cast<float*>(workspace((rec_off + nrec) * sizeof(float), st));
-    if (!ws) return ANELM_ENOMEM;
-    float* qn = ws;
-    float* kn = qn + nqk;
-    float* beta = kn + nqk;
-    float* decay = beta + ng;
-    float* ldecay = decay + ng;
-    float* rec = ws + rec_off;
-    hipLaunchKernelGGL(dn_prep_kernel, dim3((S * Hk + kPrepRows - 1) / kPrepRows), dim3(64 * kPrepRows), 0, st, qn,
-                       kn, beta, decay, ldecay, q, k, a, b, A, dt_bias, S, Hk, Hv, flags);
-    ANELM_LAUNCHED("dn_prep_kernel");
     if (chunk == 1) {
+        const size_t nqk = (size_t)S * Hk * kDK, ng = (size_t)S * Hv;
+        float* ws = static_cast<float*>(workspace((2 * nqk + 3 * ng) * sizeof(float), st));
+        if (!ws) return ANELM_ENOMEM;
+        float* qn = ws;
+        float* kn = qn + nqk;
+        float* beta = kn + nqk;
+        float* decay = beta + ng;
+        float* ldecay = decay + ng;
+        hipLaunchKernelGGL(dn_prep_kernel, dim3((S * Hk + kPrepRows - 1) / kPrepRows), dim3(64 * kPrepRows), 0, st,
+                           qn, kn, beta, decay, ldecay, q, k, a, b, A, dt_bias, S, Hk, Hv, flags);
+        ANELM_LAUNCHED("dn_prep_kernel");
         hipLaunchKernelGGL(dn_scan_kernel, dim3(kDV / kScanCB, Hv), dim3(kScanNT), 0, st, y, state, qn,
                            kn, v, beta, decay, S, Hk, Hv, flags);
         ANELM_LAUNCHED("dn_scan_kernel");
         return ANELM_OK;
     }
+    const int n_chunks = (S + kChunk - 1) / kChunk;
+    float* rec = static_cast<float*>(workspace((size_t)n_chunks * Hv * kCRec * sizeof(float), st));
+    if (!rec) return ANELM_ENOMEM;
     static bool pm_attr = false;
     if (!pm_attr) {
         ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&dn_chunk_prep_mfma_kernel<true>),
@@ -954,11 +977,11 @@ extern "C" int anelm_deltanet_prefill(float* y, float* state, const float* q, co
         pm_attr = true;
     }
     if (flags & ANELM_DN_ORDER_TRANSFORMERS)
-        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<true>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, qn,
-                           kn, v, beta, ldecay, S, Hk, Hv);
+        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<true>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, q, k, v,
+                           a, b, A, dt_bias, S, Hk, Hv, flags);
     else
-        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<false>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, qn,
-                           kn, v, beta, ldecay, S, Hk, Hv);
+        hipLaunchKernelGGL(dn_chunk_prep_mfma_kernel<false>, dim3(n_chunks, Hk), dim3(kPmNT), kPmLds, st, rec, q, k,
+                           v, a, b, A, dt_bias, S, Hk, Hv, flags);
     ANELM_LAUNCHED("dn_chunk_prep_mfma_kernel");
     // grid = Hv * kSlabs, a multiple of 8 (XCD mapping inside the kernel)
     static bool ms_attr = false;
