@@ -72,13 +72,18 @@ __device__ __forceinline__ uint32_t pair_off(const uint32_t (&wd)[NWD], int p, u
 // cache policy).  A group past the last one lies outside the buffer: its
 // loads return zeros without touching memory, so the pipeline's prefetch
 // after a workgroup's last group costs no traffic.
+// The offset is computed in 32 bits (the launch bounds (out_dim + 32 * 1024) *
+// ldw below 2^31) from a laundered lane index: nothing of it is kept live
+// across the group loop, where a spilled address would be reloaded through
+// the vector-memory counter and the reload's wait would drain the prefetch.
 template <int NP>
 __device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w,
                                              int lane) {
+    asm volatile("" : "+v"(lane));
     const int m = lane & 31, hh = lane >> 5;
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, (int)((long)a.out_dim * a.ldw), 0x00020000);
-    const int off = (int)(((long)g * 32 + m) * a.ldw) + w * 96 * NP + hh * 48 * NP;
+    const int off = (g * 32 + m) * (int)a.ldw + w * 96 * NP + hh * 48 * NP;
 #pragma unroll
     for (int i = 0; i < 3 * NP; i++) {
         const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 2));
@@ -121,6 +126,7 @@ __device__ __forceinline__ void build_table(char* lds, int slot, int j, int w, i
 // one round trip.  Called with every wave between two barriers.
 template <int NT>
 __device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0, int tid) {
+    asm volatile("" : "+v"(tid));   // indices recomputed per staging, not held across the group loop
     constexpr int K = (kLutSlots * 64 + NT - 1) / NT;
     uint16_t* l = reinterpret_cast<uint16_t*>(lds + kLutOff);
     const int n_groups = a.out_dim / 32;
