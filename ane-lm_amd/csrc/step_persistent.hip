@@ -37,6 +37,7 @@
 
 #include <math.h>
 #include <string.h>
+#include <algorithm>
 #include <vector>
 
 struct anelm_hybrid_step;
@@ -116,7 +117,7 @@ struct PLayer {
     const float* dn_z;
     const float* dn_norm_w;
     int dn_flags;
-    int pad_;
+    int pos;                          // attention: position of the new token (rope = table row pos)
     float* core_out;
     const float* ffn_norm_w;
     const uint8_t* w[3];              // gate, up, down
@@ -138,6 +139,8 @@ struct PArgs {
     float eps, scale;
     int Hk, Hv;
     unsigned long long* trace;        // [grid][kMaxPhases + 1][kTrEv] (trace build), else null
+    const float* rope_tab;            // [rope_rows][2 rot_pairs]: cos then sin of position row
+    int rope_rows;
 };
 
 // Trace events of phase p (p = 3*layer + {0 core, 1 gate/up, 2 down}):
@@ -1379,7 +1382,7 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
 // Layer pattern: groups of 3 DeltaNet layers and 1 full-attention layer
 // (models/llm/qwen3_5.cpp:64-71: layer i is full attention iff (i+1) % 4 == 0).
 template <int NIG, int NID, int NKJ, int JH, int JI>
-__global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ gpa) {
+__global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ gpa, int advance) {
     CArgs* pa = (CArgs*)gpa;
     const PArgs a = *pa;
     const PLayer L0 = ((CLayer*)a.layers)[0];
@@ -1445,6 +1448,32 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
             st_sc(a.sync + kFinOff, 0u);
             st_sc(a.sync + kAbortOff, 0u);
         }
+        if (advance) {
+            // the next step's descriptors: every attention ring and position
+            // moves one token forward (the KVCache bookkeeping of
+            // qwen3_5.cpp:973-983), so consecutive launches need no host
+            // update; the host mirrors the same arithmetic
+            PLayer* lw = const_cast<PLayer*>(a.layers);
+            for (int i = tid; i < a.n_layers; i += kNT) {
+                if (lw[i].kind != ANELM_LAYER_ATTENTION) continue;
+                int start = lw[i].ring_start, len = lw[i].ring_len, slot;
+                if (len < a.cap) {
+                    slot = start + len;
+                    if (slot >= a.cap) slot -= a.cap;
+                    len++;
+                } else {
+                    slot = start;
+                    start++;
+                    if (start >= a.cap) start = 0;
+                }
+                const int pos = lw[i].pos + 1;
+                lw[i].ring_start = start;
+                lw[i].ring_len = len;
+                lw[i].slot = slot;
+                lw[i].pos = pos;
+                lw[i].rope = a.rope_tab + (size_t)pos * 2 * a.rot_pairs;
+            }
+        }
         vm_drain();
     }
 }
@@ -1464,8 +1493,9 @@ struct PersistentStep {
     float theta = 0.f;
     pk::PLayer* d_layers = nullptr;
     pk::PArgs* d_args = nullptr;
-    float* d_rope = nullptr;           // [n_layers][rot] (cos rot/2, sin rot/2)
-    void (*kernel)(const pk::PArgs*) = nullptr;
+    float* d_rope = nullptr;           // [rope_rows][rot]: cos rot/2, sin rot/2 of position row
+    int rope_rows = 0;
+    void (*kernel)(const pk::PArgs*, int) = nullptr;
     int grid = 0;
 };
 
@@ -1488,10 +1518,10 @@ bool geo(int K, int& C, int& P, int& RP) {
     return true;
 }
 
-// Fills the per-step ring fields (after the append) and RoPE rows.
-void plan_positions(PersistentStep* s, std::vector<float>& rope_host) {
+// Fills the per-step ring fields (after the append), positions and RoPE rows
+// of the host descriptors -- the same arithmetic as the kernel's advance.
+void plan_positions(PersistentStep* s) {
     const int n = (int)s->host_layers.size();
-    rope_host.assign((size_t)n * s->rot, 0.f);
     for (int i = 0; i < n; i++) {
         pk::PLayer& L = s->host_layers[i];
         if (L.kind != ANELM_LAYER_ATTENTION) continue;
@@ -1508,18 +1538,53 @@ void plan_positions(PersistentStep* s, std::vector<float>& rope_host) {
         L.ring_start = start;
         L.ring_len = len;
         L.slot = slot;
-        rope_row(&rope_host[(size_t)i * s->rot], &rope_host[(size_t)i * s->rot + s->rot / 2], s->rot,
-                 s->pos[i], s->theta);
+        L.pos = s->pos[i];
+        L.rope = s->d_rope + (size_t)s->pos[i] * s->rot;
     }
 }
 
-int upload(PersistentStep* s, hipStream_t st) {
-    std::vector<float> rope;
-    plan_positions(s, rope);
-    ANELM_HIP(hipMemcpy(s->d_rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice));
+// Largest position a launch may reach: the new token of this step, and with
+// `advance` the next step's (its descriptors are written by this launch).
+int max_position(const PersistentStep* s, bool advance) {
+    int m = 0;
+    for (size_t i = 0; i < s->host_layers.size(); i++)
+        if (s->host_layers[i].kind == ANELM_LAYER_ATTENTION) m = std::max(m, s->pos[i] + (advance ? 1 : 0));
+    return m;
+}
+
+// RoPE table for positions [0, rows), the reference formula per row
+// (cpu_ops.cpp:51-55, the same host computation as every other RoPE path).
+int build_rope_table(PersistentStep* s, int rows) {
+    std::vector<float> host((size_t)rows * s->rot);
+    for (int p = 0; p < rows; p++)
+        rope_row(&host[(size_t)p * s->rot], &host[(size_t)p * s->rot + s->rot / 2], s->rot, p, s->theta);
+    float* d = nullptr;
+    ANELM_HIP(hipMalloc(&d, host.size() * sizeof(float)));
+    const hipError_t e = hipMemcpy(d, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "hipMemcpy(rope table)");
+    }
+    if (s->d_rope) (void)hipFree(s->d_rope);
+    s->d_rope = d;
+    s->rope_rows = rows;
+    s->args.rope_tab = d;
+    s->args.rope_rows = rows;
+    return ANELM_OK;
+}
+
+// Descriptors and arguments to the device (synchronous copies: at creation,
+// and when the RoPE table has to grow).
+int upload(PersistentStep* s, bool advance) {
+    const int need = max_position(s, advance) + 1;
+    if (need > s->rope_rows) {
+        const int rc = build_rope_table(s, (need + 4095) / 4096 * 4096);   // 4096-position blocks
+        if (rc) return rc;
+    }
+    plan_positions(s);
     ANELM_HIP(hipMemcpy(s->d_layers, s->host_layers.data(), s->host_layers.size() * sizeof(pk::PLayer),
                         hipMemcpyHostToDevice));
-    (void)st;
+    ANELM_HIP(hipMemcpy(s->d_args, &s->args, sizeof(pk::PArgs), hipMemcpyHostToDevice));
     return ANELM_OK;
 }
 
@@ -1612,14 +1677,13 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     s->rot = d->rot_dim;
     s->theta = d->theta;
     s->grid = nwg;
-    s->kernel = reinterpret_cast<void (*)(const pk::PArgs*)>(kp);
+    s->kernel = reinterpret_cast<void (*)(const pk::PArgs*, int)>(kp);
     s->host_layers.resize(n_layers);
     s->pos.resize(n_layers);
     s->start.resize(n_layers);
     s->len.resize(n_layers);
     hipError_t e = hipMalloc(&s->d_layers, sizeof(pk::PLayer) * n_layers);
     if (e == hipSuccess) e = hipMalloc(&s->d_args, sizeof(pk::PArgs));
-    if (e == hipSuccess) e = hipMalloc(&s->d_rope, sizeof(float) * (size_t)n_layers * (s->rot > 0 ? s->rot : 2));
     const size_t rec = (size_t)pk::kAttnG * pk::kAttnRec;
     if (e == hipSuccess) e = hipMalloc(&s->args.part, sizeof(float) * rec * (n_attn ? d->n_kv_heads * splits : 1));
     if (e == hipSuccess) e = hipMalloc(&s->args.dnss, sizeof(float) * (size_t)nwg);
@@ -1655,7 +1719,6 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
         L.v_cache = S.v_cache;
         L.q_norm_w = S.q_norm_w;
         L.k_norm_w = S.k_norm_w;
-        L.rope = s->d_rope + (size_t)i * s->rot;
         L.state = S.state;
         L.dn_q = S.dn_q;
         L.dn_k = S.dn_k;
@@ -1704,11 +1767,7 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     a.scale = 1.0f / sqrtf((float)d->head_dim);
     a.Hk = d->lin_k_heads;
     a.Hv = d->lin_v_heads;
-    int rc = upload(s, st);
-    if (rc == ANELM_OK) {
-        const hipError_t e2 = hipMemcpy(s->d_args, &s->args, sizeof(pk::PArgs), hipMemcpyHostToDevice);
-        if (e2 != hipSuccess) rc = hip_fail(e2, "hipMemcpy(step args)");
-    }
+    const int rc = upload(s, true);
     if (rc) {
         persistent_destroy(s);
         return rc;
@@ -1718,22 +1777,28 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
 }
 
 // One step.  With `advance`, every attention ring and position moves one
-// token forward afterwards (the host KVCache bookkeeping of qwen3_5.cpp:973-983)
-// and the descriptors are re-uploaded before the next launch.
+// token forward afterwards (the host KVCache bookkeeping of qwen3_5.cpp:973-983):
+// the launch writes the next step's descriptors itself.
 int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
-    hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st,
-                       (const pk::PArgs*)s->d_args);
+    if (advance && max_position(s, true) >= s->rope_rows) {
+        // the table must hold the next step's row: grow it (the previous
+        // launch, which wrote the descriptors being replaced, completes first)
+        ANELM_HIP(hipStreamSynchronize(st));
+        const int rc = upload(s, true);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st, (const pk::PArgs*)s->d_args,
+                       advance ? 1 : 0);
     ANELM_LAUNCHED("step_kernel");
     if (advance) {
+        // host mirror of the launch's own advance (no copy, no wait)
         for (size_t i = 0; i < s->host_layers.size(); i++) {
             if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) continue;
             s->start[i] = s->host_layers[i].ring_start;
             s->len[i] = s->host_layers[i].ring_len;
             s->pos[i]++;
         }
-        // the next launch may only see new descriptors after this one has read them
-        ANELM_HIP(hipStreamSynchronize(st));
-        return upload(s, st);
+        plan_positions(s);
     }
     return ANELM_OK;
 }

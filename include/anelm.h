@@ -455,9 +455,12 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          advance);
  *   ANELM_STEP_PERSISTENT  the whole step as ONE kernel launch (one workgroup
  *                          per compute unit, grid barriers between the
- *                          layers' phases); advances rings like EAGER, or
- *                          replays like GRAPH when combined with
- *                          ANELM_STEP_STATIC.  Supported for hidden/inter
+ *                          layers' phases); advances rings like EAGER (the
+ *                          launch writes the next step's ring descriptors
+ *                          itself: consecutive runs queue without a host
+ *                          wait, except once per 4096 positions when the
+ *                          RoPE table grows), or replays like GRAPH when
+ *                          combined with ANELM_STEP_STATIC.  Supported for hidden/inter
  *                          sizes that tile over the device's compute units
  *                          (the Qwen3.5-4B shape on 256 CUs) and layers
  *                          without projections (first_w NULL); other

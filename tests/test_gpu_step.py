@@ -223,17 +223,10 @@ def _graph_after_growth(anelm, orc, dev, dm, m, x0):
         anelm.call("anelm_hybrid_step_destroy", h)
 
 
-def test_persistent_step_matches_eager(anelm, dev):
-    """8 layers, 3 advancing decode steps: one ring mid-fill (5000 of 8192
-    keys), one full ring that wraps and overwrites its oldest slot.
-
-    LUTs ~ N(0, 0.005): with the 0.02 scale of the other tests, eight random
-    FFN blocks amplify any fp32 summation-order difference through the fp16
-    activation roundings (a 1e-7 relative nudge of x moves the oracle's own x
-    by 7e-4 after one step); at 0.005 the same nudge moves it by < 2e-5 over
-    three steps while the FFNs still change x by 4% per step, so the hidden
-    state is checked at 1e-4."""
-    m = hybrid_model(901, 8, rings=[(0, 5000), (8000, 8192)], lut_std=0.005)
+def _persistent_vs_eager(anelm, m, dev, steps, label):
+    """Runs `steps` advancing decode steps of model m through the eager path
+    and the persistent step side by side and compares every core output,
+    state, cache and the hidden state after each."""
     a = DeviceModel(anelm, m, dev)
     b = DeviceModel(anelm, m, dev)
     s = _stream()
@@ -244,8 +237,8 @@ def test_persistent_step_matches_eager(anelm, dev):
         anelm.call("anelm_hybrid_step_destroy", ha)
         pytest.skip(f"persistent step unsupported here: {anelm.last_error()}")
     try:
-        for step in range(3):
-            print(f"persistent step {step}", flush=True)
+        for step in range(steps):
+            print(f"{label}: persistent step {step}", flush=True)
             anelm.call("anelm_hybrid_step_run", ha, s)
             anelm.call("anelm_hybrid_step_run", hb, s)
             torch.cuda.synchronize()
@@ -265,3 +258,26 @@ def test_persistent_step_matches_eager(anelm, dev):
     finally:
         anelm.call("anelm_hybrid_step_destroy", ha)
         anelm.call("anelm_hybrid_step_destroy", hb)
+
+
+def test_persistent_step_matches_eager(anelm, dev):
+    """8 layers, 3 advancing decode steps: one ring mid-fill (5000 of 8192
+    keys), one full ring that wraps and overwrites its oldest slot.
+
+    LUTs ~ N(0, 0.005): with the 0.02 scale of the other tests, eight random
+    FFN blocks amplify any fp32 summation-order difference through the fp16
+    activation roundings (a 1e-7 relative nudge of x moves the oracle's own x
+    by 7e-4 after one step); at 0.005 the same nudge moves it by < 2e-5 over
+    three steps while the FFNs still change x by 4% per step, so the hidden
+    state is checked at 1e-4."""
+    m = hybrid_model(901, 8, rings=[(0, 5000), (8000, 8192)], lut_std=0.005)
+    _persistent_vs_eager(anelm, m, dev, 3, "8 layers")
+
+
+def test_persistent_step_rope_table_growth(anelm, dev):
+    """The persistent step advances its own descriptors on the device and
+    reads RoPE rows from a table sized in 4096-position blocks; starting at
+    position 4094, the second step needs row 4096, so the table grows (the
+    host waits for the launch before, rebuilds and re-uploads) between steps."""
+    m = hybrid_model(905, 4, rings=[(0, 4094)], lut_std=0.005)
+    _persistent_vs_eager(anelm, m, dev, 3, "table growth")
