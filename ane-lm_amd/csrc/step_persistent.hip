@@ -1644,11 +1644,15 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     int splits = 0, kps = 0, nkj = 0;
     if (n_attn) {
         ANELM_REQUIRE(d->head_dim == pk::kAttnD && d->n_heads == pk::kAttnG * d->n_kv_heads &&
-                          d->n_kv_heads <= pk::kMaxKvh && nwg % d->n_kv_heads == 0,
+                          d->n_kv_heads <= pk::kMaxKvh,
                       "persistent step: attention needs head_dim 256 and 4 q heads per kv head");
-        splits = nwg / d->n_kv_heads;
-        ANELM_REQUIRE(splits == pk::kAttnSplits && pk::kAttnSplits == pk::kAttnG * (pk::kAttnD / 16),
-                      "persistent step: %d splits per kv head", splits);
+        // 64 key splits per kv head (the merge puts split s in lane s); with
+        // fewer kv heads than the grid holds, the remaining workgroups have
+        // no attention work and only take part in the barriers
+        splits = pk::kAttnSplits;
+        static_assert(pk::kAttnSplits == pk::kAttnG * (pk::kAttnD / 16), "merge slices");
+        ANELM_REQUIRE(d->n_kv_heads * splits <= nwg, "persistent step: %d kv heads need %d workgroups (%d CUs)",
+                      d->n_kv_heads, d->n_kv_heads * splits, nwg);
         kps = (cap + splits - 1) / splits;
         nkj = (kps + 19) / 20;
         ANELM_REQUIRE(nkj <= 7, "persistent step: cache capacity %d beyond %d keys", cap, splits * 140);
@@ -1658,16 +1662,22 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
                       "persistent step: rope_mode %d", d->rope_mode);
     }
     if (n_attn < n_layers) {
-        ANELM_REQUIRE(d->lin_dim == pk::kDnD && d->lin_v_heads * pk::kDnSlabs == nwg && d->lin_k_heads > 0 &&
+        // 8 workgroups per value head; any others idle through the DeltaNet cores
+        ANELM_REQUIRE(d->lin_dim == pk::kDnD && d->lin_v_heads * pk::kDnSlabs <= nwg && d->lin_k_heads > 0 &&
                           d->lin_v_heads % d->lin_k_heads == 0,
-                      "persistent step: DeltaNet needs 128-dim heads and %d value heads (8 workgroups each)",
+                      "persistent step: DeltaNet needs 128-dim heads and at most %d value heads (8 workgroups each)",
                       nwg / pk::kDnSlabs);
     }
-    // Supported instantiation: the Qwen3.5-4B shape on a 256-CU device.
+    // Instantiations on a 256-CU device: the Qwen3.5-4B shape (hidden 2560,
+    // inter 9216) and the reference's default Qwen3.5-0.8B shape (hidden 1024,
+    // inter 3584, qwen3_5.h:51-69).  Seven key slots per lane cover caches up
+    // to 8960 keys; smaller caches leave slots past their split empty.
     void* kp = nullptr;
     const int jh = d->hidden / 256, ji = d->inter / 512;
-    if (nig == 18 && nid == 10 && jh == 10 && ji == 18 && (n_attn == 0 || nkj == 7))
-        kp = kernel_ptr<18, 10, 7, 10, 18>();
+    if (nkj <= 7) {
+        if (nig == 18 && nid == 10 && jh == 10 && ji == 18) kp = kernel_ptr<18, 10, 7, 10, 18>();
+        else if (nig == 14 && nid == 2 && jh == 4 && ji == 7) kp = kernel_ptr<14, 2, 7, 4, 7>();
+    }
     ANELM_REQUIRE(kp != nullptr,
                   "persistent step: no kernel for this shape (gate/up %d, down %d instructions, %d key slots)",
                   nig, nid, nkj);

@@ -462,9 +462,10 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          RoPE table grows), or replays like GRAPH when
  *                          combined with ANELM_STEP_STATIC.  Supported for hidden/inter
  *                          sizes that tile over the device's compute units
- *                          (the Qwen3.5-4B shape on 256 CUs) and layers
- *                          without projections (first_w NULL); other
- *                          shapes return ANELM_EINVAL from create. */
+ *                          (the Qwen3.5-4B and Qwen3.5-0.8B shapes on 256
+ *                          CUs) and layers without projections (first_w
+ *                          NULL); other shapes return ANELM_EINVAL from
+ *                          create. */
 #define ANELM_STEP_EAGER 0
 #define ANELM_STEP_GRAPH 1
 #define ANELM_STEP_PERSISTENT 2

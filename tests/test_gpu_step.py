@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from gpu_util import assert_close, to_dev, to_host
-from workloads import QWEN35_4B, hybrid_model, oracle_hybrid_step, widen
+from workloads import QWEN35_08B, QWEN35_4B, hybrid_model, oracle_hybrid_step, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -281,3 +281,27 @@ def test_persistent_step_rope_table_growth(anelm, dev):
     host waits for the launch before, rebuilds and re-uploads) between steps."""
     m = hybrid_model(905, 4, rings=[(0, 4094)], lut_std=0.005)
     _persistent_vs_eager(anelm, m, dev, 3, "table growth")
+
+
+def test_persistent_step_08b_shape_matches_oracle(anelm, orc, dev):
+    """The reference's default model shape (Qwen3.5-0.8B, qwen3_5.h:51-69:
+    hidden 1024, inter 3584, 8 q / 2 kv heads, 16 value heads) as one
+    persistent launch on the 256-CU grid: attention uses 128 of the
+    workgroups and the DeltaNet cores 128, the rest only join the barriers.
+    8 layers, one step against the oracle."""
+    m = hybrid_model(906, 8, dims=QWEN35_08B, rings=[(0, 3000), (8000, 8192)])
+    dm = DeviceModel(anelm, m, dev)
+    s = _stream()
+    h = _persistent_or_skip(anelm, dm, s)
+    try:
+        _check_against_oracle(anelm, orc, dm, h, m, s, 1, 1e-3, 2e-2, "0.8B shape", True)
+    finally:
+        anelm.call("anelm_hybrid_step_destroy", h)
+
+
+def test_persistent_step_08b_shape_advancing_matches_eager(anelm, dev):
+    """The 0.8B shape, 3 advancing steps (one ring mid-fill, one wrapping)
+    against the eager path."""
+    m = hybrid_model(907, 8, dims=QWEN35_08B, rings=[(0, 3000), (8000, 8192)], lut_std=0.005)
+    _persistent_vs_eager(anelm, m, dev, 3, "0.8B shape")
+
