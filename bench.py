@@ -41,6 +41,9 @@ TRAFFIC = {"step_kernel": 2223129293}
 
 CFG = dict(hidden=2560, inter=9216, layers=32, n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64,
            theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=32, lin_dim=128, ctx=8192)
+# the reference's default model (models/llm/qwen3_5.h:51-69)
+CFG_08B = dict(hidden=1024, inter=3584, layers=24, n_heads=8, n_kv_heads=2, head_dim=256, rot_dim=64,
+               theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=16, lin_dim=128, ctx=8192)
 
 
 def step_bytes(c=CFG):
@@ -91,11 +94,11 @@ def proj_bytes(c=CFG):
     return w + conv
 
 
-def build_step(anelm, torch, dev, seed=0, mode=None, proj=False):
-    """Allocates the synthetic 4B-shaped model state and returns (step, keep, x).
-    With proj, every layer also carries its projections (input norm + first
-    projection, DeltaNet conv ring, o_proj) and the step runs whole layers."""
-    c = CFG
+def build_step(anelm, torch, dev, seed=0, mode=None, proj=False, c=CFG):
+    """Allocates the synthetic model state of shape c (the 4B shape by
+    default) and returns (step, keep, x).  With proj, every layer also carries
+    its projections (input norm + first projection, DeltaNet conv ring,
+    o_proj) and the step runs whole layers."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     H, I, D = c["hidden"], c["inter"], c["head_dim"]
@@ -481,6 +484,28 @@ def measure_batch32_step(anelm, torch, dev, seed=12, reps=5):
     return r
 
 
+def measure_step_08b(anelm, torch, dev, reps=50):
+    """The same decode step at the reference's default 0.8B shape (24 layers,
+    ctx 8192) as one persistent launch; on the 256-CU grid its 2 kv heads and
+    16 value heads occupy 128 workgroups in the cores."""
+    handle, keep, x, mode = build_step(anelm, torch, dev, seed=5, mode=anelm.STEP_PERSISTENT | anelm.STEP_STATIC,
+                                       c=CFG_08B)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(5):
+        anelm.call("anelm_hybrid_step_run", handle, s)
+    us = _gpu_us(torch, lambda: anelm.call("anelm_hybrid_step_run", handle, s), reps, warm=0)
+    st = ctypes.c_int(0)
+    anelm.call("anelm_hybrid_step_status", handle, ctypes.byref(st))
+    assert st.value == 0 and torch.isfinite(x).all(), "0.8B step failed"
+    anelm.call("anelm_hybrid_step_destroy", handle)
+    del keep
+    r = _hbm(us, step_bytes(CFG_08B)["total"])
+    r["execution"] = "persistent kernel, one launch per step"
+    r["composition"] = ("24 layers: 6 full-attention cores (8q/2kv, ctx 8192), 18 Gated-DeltaNet cores "
+                        "(16k/16v heads), 24 LUT6 SwiGLU FFN 1024->3584->1024")
+    return r
+
+
 def measure_complete_step(anelm, torch, dev, reps=20):
     """The same 32-layer step with the projections around the cores inside
     (qwen3_5.cpp:1287-1354 per layer: input norm + LUT6 first projection, the
@@ -814,6 +839,7 @@ def main():
             cores["batch32_decode_step"] = measure_batch32_step(anelm, torch, dev)
             torch.cuda.empty_cache()
             cores["complete_step_graph"] = measure_complete_step(anelm, torch, dev)
+            cores["decode_step_0.8b"] = measure_step_08b(anelm, torch, dev)
 
     b = step_bytes()
     gbps = b["total"] / (us_step * 1e-6) / 1e9
