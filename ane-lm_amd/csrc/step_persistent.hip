@@ -1676,7 +1676,16 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     const int jh = d->hidden / 256, ji = d->inter / 512;
     if (nkj <= 7) {
         if (nig == 18 && nid == 10 && jh == 10 && ji == 18) kp = kernel_ptr<18, 10, 7, 10, 18>();
-        else if (nig == 14 && nid == 2 && jh == 4 && ji == 7) kp = kernel_ptr<14, 2, 7, 4, 7>();
+        else if (nig == 14 && nid == 2 && jh == 4 && ji == 7) {
+#if ANELM_STEP_TRACE
+            // The clock-stamped build of this shape took a memory access fault
+            // whose cause is not found; the diagnostic build refuses it (the
+            // production build of the same shape is unaffected).
+            return set_error(ANELM_EINVAL, "step trace: the 0.8B shape is disabled in the trace build");
+#else
+            kp = kernel_ptr<14, 2, 7, 4, 7>();
+#endif
+        }
     }
     ANELM_REQUIRE(kp != nullptr,
                   "persistent step: no kernel for this shape (gate/up %d, down %d instructions, %d key slots)",
