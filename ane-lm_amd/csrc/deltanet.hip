@@ -352,6 +352,7 @@ constexpr int kCRec = 5 * kCMat + 64;           // Ut, Wm, Op, Qh, Kh, gC
 // 66 KB, so two workgroups share a CU (one's serial phases overlap the other).
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kPmNT = 512;
 constexpr int kPmK = 0;                        // K rows [64][128]
 constexpr int kPmR = kCMat;                    // Q rows [64][128] for the Gram tiles, then:
@@ -534,15 +535,19 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
 #pragma unroll
             for (int t = 0; t < 16; t++) Am[sw64(16 * b + t, 16 * b + j)] = x[t];
         } else {
-            // ---- Kh = diag(exp(lg_L - lg)) K, gC (waves 1..7)
+            // ---- Kh = diag(exp(lg_L - lg)) K, stored transposed (Kh^T [128][64]:
+            // the scan reads it as rows of its state-row tiles), gC (waves 1..7)
             const float lgL = lg[kChunk];
             for (int e = ltid - 64; e < kCMat / 4; e += kPmNT - 64) {
-                const int t = e >> 5, ch = e & 31;
-                const float sc = expf(lgL - lg[t + 1]);
-                const float4 k4 = *reinterpret_cast<const float4*>(Ks + sw128(t, 4 * ch));
-                const float4 o4 = make_float4(k4.x * sc, k4.y * sc, k4.z * sc, k4.w * sc);
+                const int kd = e >> 4, t4 = e & 15;
+                v4f o4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int t = 4 * t4 + j;
+                    o4[j] = Ks[sw128(t, kd)] * expf(lgL - lg[t + 1]);
+                }
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o4), ro,
-                                                       (4 * kCMat + t * kDK + 4 * ch) * 4, 0, 0);
+                                                       (4 * kCMat + kd * kChunk + 4 * t4) * 4, 0, 0);
             }
             if (ltid == 64)
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, expf(lgL)), ro, 5 * kCMat * 4, 0, 0);
@@ -610,43 +615,79 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
     }
 }
 
-// Sequential part: workgroup (slab of 16 state columns, value head) keeps its
 // The state is carried through the chunks in slabs of 16 columns (8 per head).
 constexpr int kSeqCB = 16;
 constexpr int kSlabs = kDV / kSeqCB;
 
 // ------------------------------------------------ chunk scan on fp32 MFMA
 // The same three products per chunk on v_mfma_f32_16x16x4_f32 (fp32 inputs,
-// fp32 accumulation).  A workgroup (4 waves, one per SIMD) owns a 16-column
+// fp32 accumulation).  A workgroup (8 waves, two per SIMD) owns a 16-column
 // slab of one head's state, kept in LDS column-major (Sc[c][i]):
-//   wave w: X = Wm S0 and Y = Qh S0 for chunk rows t in [16w, 16w + 16)
-//           (32 MFMAs each over the 128 state rows), U = Ut - X, y = Op + Y;
-//   then    S = gC S0 + Kh^T U for state rows i in [32w, 32w + 32)
-//           (2 tiles x 16 MFMAs over the 64 chunk rows).
+//   waves 0-3: X = Wm S0 for chunk rows [16 w, 16 w + 16), U = Ut - X (LDS);
+//   waves 4-7: Y = Qh S0 for chunk rows [16 (w - 4), ...), y = Op + Y (LDS,
+//   then stored by all 8 waves);
+//   then wave w: S = gC S0 + Kh^T U for state rows [16 w, 16 w + 16).
+// Every operand but the state and U is read by one wave only (its Wm or Qh
+// rows, its Kh^T rows, its Ut or Op entries), so it goes from memory straight
+// into registers, the next chunk's loads spread over this chunk's products;
+// LDS carries only the state slab and U.
 // MFMA operand layouts (16x16x4, one block): A[m][k] in lane m + 16 k,
 // B[k][n] in lane n + 16 k, D[m][n] in lane n + 16 (m / 4), element m % 4.
 // The contraction index is permuted identically in both operands: lane (m, k)
 // of k-step (x, e) takes state row (or chunk row) 16 x + 4 k + e, so an A
-// operand is one 16-byte read per lane and four.
-// The chunk's operands (Wm, Qh, Kh whole; the slab's columns of Ut and Op)
-// stream into LDS with buffer loads (16 bytes per lane, 1 KiB per wave
-// instruction) while the previous chunk is computed; each wave then reads its
-// operands from LDS into registers.  Wm / Qh rows are stored with their
-// 16-byte chunks XOR-swizzled by the row (conflict-free operand reads).
-constexpr int kMsNT = 256;
-constexpr int kScP = kDK + 4;                      // Sc row pitch (floats)
-constexpr int kOpWm = 0, kOpQh = kCMat, kOpKh = 2 * kCMat;   // operand buffer (floats)
-constexpr int kOpUt = 3 * kCMat, kOpOp = 3 * kCMat + kChunk * 16;
-constexpr int kOpFloats = 3 * kCMat + 2 * kChunk * 16;
-constexpr int kMsLds = (kOpFloats + kSeqCB * kScP + kChunk * (kSeqCB + 1)) * 4;
+// operand is one 16-byte read per lane for four k-steps.
+constexpr int kMsNT = 512;
+constexpr int kScP = kDK + 4;        // Sc row pitch (floats): 16-byte reads of 16 lanes hit distinct banks
+constexpr int kUlP = kSeqCB + 4;     // U row pitch: rows 4 apart land 16 banks apart
+constexpr int kMsLds = (kSeqCB * kScP + 2 * kChunk * kUlP) * 4;
 
-__global__ __launch_bounds__(kMsNT) __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_chunk_mfma_kernel(
+// One wave's operands of one chunk.
+struct ScanOps {
+    v4f m[8];     // Wm (waves 0-3) or Qh (4-7) row 16 (w & 3) + lr, state rows 16 x + 4 lq + (0..3)
+    v4f kt[4];    // Kh^T row 16 w + lr, chunk rows 16 x + 4 lq + (0..3)
+    float uo[4];  // Ut (waves 0-3) or Op (4-7) at chunk row 16 (w & 3) + 4 lq + j, slab column lr
+    float gc;
+};
+
+// Where one wave's operands of chunk ch lie: one chunk record per buffer
+// resource (offsets stay small for any sequence length).
+struct ScanSrc {
+    __amdgpu_buffer_rsrc_t rr;
+    int mo, ko, uo;   // float offsets of this lane's first Wm / Qh, Kh^T and Ut / Op element
+};
+
+__device__ __forceinline__ ScanSrc scan_src(const float* rec, int ch, int Hv, int h, int w, int lr, int lq, int c0) {
+    ScanSrc s;
+    s.rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rec) + ((size_t)ch * Hv + h) * kCRec, 0, kCRec * 4,
+                                             0x00020000);
+    const int mt = w & 3;
+    s.mo = (w < 4 ? kCMat : 3 * kCMat) + (16 * mt + lr) * kDK + 4 * lq;
+    s.ko = 4 * kCMat + (16 * w + lr) * kChunk + 4 * lq;
+    s.uo = (w < 4 ? 0 : 2 * kCMat) + (16 * mt + 4 * lq) * kDK + c0 + lr;
+    return s;
+}
+
+// Part x (0..7) of a wave's loads of one chunk: m[x], then kt[x] (x < 4) or
+// uo[x - 4] (x >= 4), and gc with the last part.  The parts are issued
+// between the MFMA groups of the previous chunk's products: issued all at
+// once, the workgroup's loads fill the CU's memory queue and the waves stall
+// at their next memory instruction instead of computing.
+__device__ __forceinline__ void scan_part(ScanOps& o, const ScanSrc& s, int x) {
+    o.m[x] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(s.rr, (s.mo + 16 * x) * 4, 0, 0));
+    if (x < 4)
+        o.kt[x] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(s.rr, (s.ko + 16 * x) * 4, 0, 0));
+    else
+        o.uo[x - 4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.rr, (s.uo + (x - 4) * kDK) * 4, 0, 0));
+    if (x == 7) o.gc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.rr, 5 * kCMat * 4, 0, 0));
+}
+
+__global__ __launch_bounds__(kMsNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void dn_chunk_mfma_kernel(
     float* __restrict__ y, float* __restrict__ state, const float* __restrict__ rec, int S, int Hv, int n_chunks) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float* opb = smem;                                     // operand buffer
-    float (*Sc)[kScP] = reinterpret_cast<float (*)[kScP]>(smem + kOpFloats);        // state slab
-    float (*Ul)[kSeqCB + 1] = reinterpret_cast<float (*)[kSeqCB + 1]>(smem + kOpFloats + kSeqCB * kScP);
-    // XCD-aware: the 8 slabs of a head share its chunk matrices, so they go to
+    float (*Sc)[kScP] = reinterpret_cast<float (*)[kScP]>(smem);                   // state slab
+    float (*Ul)[kUlP] = reinterpret_cast<float (*)[kUlP]>(smem + kSeqCB * kScP);   // U of the chunk
+    float (*Yl)[kUlP] = Ul + kChunk;                                               // its y tile
+    // XCD-aware: the 8 slabs of a head share its chunk records, so they go to
     // one XCD (workgroup id mod 8 selects the XCD; Hv * 8 workgroups)
     const int nwg = gridDim.x, id = blockIdx.x;
     const int per_xcd = nwg / 8, k8 = id / 8, xcd = id % 8;
@@ -654,125 +695,92 @@ __global__ __launch_bounds__(kMsNT) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lq = lane >> 4;
-    const int c0 = slab * kSeqCB, col = c0 + lr;
+    const int mt = w & 3;
+    const int c0 = slab * kSeqCB;
     const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(y, 0, (int)((size_t)S * Hv * kDV * 4), 0x00020000);
-    // per-lane byte offsets of this wave's 26 operand loads within a chunk record
-    // (instruction k of the workgroup covers 1 KiB of the operand buffer)
-    auto issue = [&](int ch) __attribute__((always_inline)) {
-        // one chunk record per resource: offsets stay small for any sequence length
-        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(rec) + ((size_t)ch * Hv + h) * kCRec, 0, kCRec * 4, 0x00020000);
-        constexpr int base = 0;
-        char* ob = reinterpret_cast<char*>(opb);
-        // Wm, Qh: 32 instructions each (rows 2k, 2k+1); Kh: 32 (straight copy)
-#pragma unroll
-        for (int x = 0; x < 8; x++) {
-            const int k = 8 * w + x, row = 2 * k + (lane >> 5), p = lane & 31, c = p ^ (row & 15);
-            const int go = row * kDK * 4 + c * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpWm * 4 + k * 1024)), 16,
-                                                     base + kCMat * 4 + go, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpQh * 4 + k * 1024)), 16,
-                                                     base + 3 * kCMat * 4 + go, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpKh * 4 + k * 1024)), 16,
-                                                     base + 4 * kCMat * 4 + k * 1024 + lane * 16, 0, 0, 0);
-        }
-        // the slab's 16 columns of Ut and Op: row 16 w + lane / 4, 16-byte chunk lane % 4
-        const int go = (16 * w + (lane >> 2)) * kDK * 4 + c0 * 4 + (lane & 3) * 16;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpUt * 4 + w * 1024)), 16,
-                                                 base + go, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ob + (kOpOp * 4 + w * 1024)), 16,
-                                                 base + 2 * kCMat * 4 + go, 0, 0, 0);
-    };
 
+    // two operand sets, A and B: a chunk is computed from one while the next
+    // chunk's loads land in the other (no register copies between them)
+    ScanOps opA, opB;
+    {
+        const ScanSrc s0 = scan_src(rec, 0, Hv, h, w, lr, lq, c0);
+#pragma unroll
+        for (int x = 0; x < 8; x++) scan_part(opA, s0, x);
+    }
     float* Sp = state + (size_t)h * kDK * kDV;
     for (int e = tid; e < kDK * kSeqCB; e += kMsNT) {
         const int i = e / kSeqCB, c = e % kSeqCB;
         Sc[c][i] = Sp[(size_t)i * kDV + c0 + c];
     }
-    issue(0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's part of chunk 0 landed
-    lds_barrier();
+    __syncthreads();
 
-    for (int ch = 0; ch < n_chunks; ch++) {
-        const int t0 = ch * kChunk;
-        // ---- operands of this chunk from LDS
-        float4 wa[8], qa[8], sb[8];
-        {
-            const int row = 16 * w + lr;
+    auto chunk = [&](const ScanOps& cur, ScanOps& nxt, int ch) __attribute__((always_inline)) {
+        // the next chunk's operands (the last chunk reloads its own: no branch)
+        const ScanSrc src = scan_src(rec, ch + 1 < n_chunks ? ch + 1 : ch, Hv, h, w, lr, lq, c0);
+        // ---- X = Wm S0 (waves 0-3) or Y = Qh S0 (waves 4-7): 32 MFMAs in 4
+        // chains, one part of the next chunk's loads ahead of each group of 4
+        v4f sb[8];
 #pragma unroll
-            for (int x = 0; x < 8; x++) {
-                const int c = (4 * x + lq) ^ (row & 15);
-                wa[x] = *reinterpret_cast<const float4*>(opb + kOpWm + row * kDK + 4 * c);
-                qa[x] = *reinterpret_cast<const float4*>(opb + kOpQh + row * kDK + 4 * c);
-                sb[x] = *reinterpret_cast<const float4*>(&Sc[lr][16 * x + 4 * lq]);
-            }
-        }
-        float kh[2][16];
+        for (int x = 0; x < 8; x++) sb[x] = *reinterpret_cast<const v4f*>(&Sc[lr][16 * x + 4 * lq]);
+        v4f Z[4];
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-            for (int s = 0; s < 16; s++)
-                kh[tb][s] = opb[kOpKh + (16 * (s >> 2) + 4 * lq + (s & 3)) * kDK + 32 * w + 16 * tb + lr];
-        float utv[4], opv[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            utv[j] = opb[kOpUt + (16 * w + 4 * lq + j) * 16 + lr];
-            opv[j] = opb[kOpOp + (16 * w + 4 * lq + j) * 16 + lr];
-        }
-        const float gc = rec[((size_t)ch * Hv + h) * kCRec + 5 * kCMat];
-        lds_barrier();   // every wave holds its operands: the buffer takes the next chunk
-        if (ch + 1 < n_chunks) issue(ch + 1);
-        // ---- X = Wm S0, Y = Qh S0 (four independent accumulation chains)
-        v4f X0 = {0.f, 0.f, 0.f, 0.f}, X1 = X0, Y0 = X0, Y1 = X0;
+        for (int e = 0; e < 4; e++) Z[e] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int x = 0; x < 8; x++) {
-            X0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].x, sb[x].x, X0, 0, 0, 0);
-            Y0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].x, sb[x].x, Y0, 0, 0, 0);
-            X1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].y, sb[x].y, X1, 0, 0, 0);
-            Y1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].y, sb[x].y, Y1, 0, 0, 0);
-            X0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].z, sb[x].z, X0, 0, 0, 0);
-            Y0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].z, sb[x].z, Y0, 0, 0, 0);
-            X1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[x].w, sb[x].w, X1, 0, 0, 0);
-            Y1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[x].w, sb[x].w, Y1, 0, 0, 0);
+            scan_part(nxt, src, x);
+            __builtin_amdgcn_sched_barrier(0);   // the part is issued here, not hoisted or sunk
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                Z[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.m[x][e], sb[x][e], Z[e], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const v4f X = X0 + X1, Y = Y0 + Y1;
-        // ---- U = Ut - X (to LDS), y = Op + Y; element j is chunk row 16w + 4 lq + j
-        // (y rows past S fall out of the buffer range and are dropped)
+        const v4f Zs = (Z[0] + Z[1]) + (Z[2] + Z[3]);
+        // element j is chunk row 16 mt + 4 lq + j, slab column lr:
+        // U = Ut - X (waves 0-3) and y = Op + Y (waves 4-7) go to LDS
+        {
+            float (*dst)[kUlP] = w < 4 ? Ul : Yl;
+            const float sg = w < 4 ? -1.f : 1.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int t = 16 * w + 4 * lq + j;
-            Ul[t][lr] = utv[j] - X[j];
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, opv[j] + Y[j]), ry,
-                                                  (((t0 + t) * Hv + h) * kDV + col) * 4, 0, 0);
+            for (int j = 0; j < 4; j++) dst[16 * mt + 4 * lq + j][lr] = cur.uo[j] + sg * Zs[j];
         }
-        lds_barrier();   // U complete; every wave's reads of S0 are done
-        // ---- S = gC S0 + Kh^T U for state rows 32w + 16 tb + (0..15)
-        float ubv[16];
+        lds_barrier();   // U and y complete; every wave's reads of S0 are done
+        {
+            // the y tile to memory, one 8-byte store per lane of every wave:
+            // all waves then have the same memory operations in flight, so the
+            // waits for this chunk's operands count the same everywhere
+            // (y rows past S fall out of the buffer range and are dropped)
+            const int t = tid >> 3, cp = tid & 7;
+            const float2 yv = *reinterpret_cast<const float2*>(&Yl[t][2 * cp]);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, yv), ry,
+                                                  (((ch * kChunk + t) * Hv + h) * kDV + c0 + 2 * cp) * 4, 0, 0);
+        }
+        // ---- S = gC S0 + Kh^T U for state rows 16 w + (0..15): 16 MFMAs in 4 chains
+        float ub[16];
 #pragma unroll
-        for (int s = 0; s < 16; s++) ubv[s] = Ul[16 * (s >> 2) + 4 * lq + (s & 3)][lr];
-        v4f Sn[2][2];
+        for (int s = 0; s < 16; s++) ub[s] = Ul[16 * (s >> 2) + 4 * lq + (s & 3)][lr];
+        v4f* srow = reinterpret_cast<v4f*>(&Sc[lr][16 * w + 4 * lq]);
+        v4f Sn[4];
+        Sn[0] = cur.gc * *srow;
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++)
+        for (int e = 1; e < 4; e++) Sn[e] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                Sn[tb][0][j] = gc * Sc[lr][32 * w + 16 * tb + 4 * lq + j];
-                Sn[tb][1][j] = 0.f;
-            }
+        for (int x = 0; x < 4; x++)
 #pragma unroll
-        for (int s = 0; s < 16; s++)
-#pragma unroll
-            for (int tb = 0; tb < 2; tb++)
-                Sn[tb][s & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kh[tb][s], ubv[s], Sn[tb][s & 1], 0, 0, 0);
+            for (int e = 0; e < 4; e++)
+                Sn[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.kt[x][e], ub[4 * x + e], Sn[e], 0, 0, 0);
         // rows written here are read (as C) only by this wave
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++) {
-            const v4f sn = Sn[tb][0] + Sn[tb][1];
-#pragma unroll
-            for (int j = 0; j < 4; j++) Sc[lr][32 * w + 16 * tb + 4 * lq + j] = sn[j];
-        }
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's part of the next chunk landed (and its y stores)
-        lds_barrier();   // new state complete, U consumed, next chunk's operands in LDS
+        *srow = (Sn[0] + Sn[1]) + (Sn[2] + Sn[3]);
+        lds_barrier();   // new state complete, U and y consumed
+    };
+    // pairs of chunks, then an odd last one: inside the loop both halves run
+    // unconditionally, so the loads a half issues for the other are not sunk
+    // into a conditional block next to their use
+    int ch = 0;
+    for (; ch + 1 < n_chunks; ch += 2) {
+        chunk(opA, opB, ch);
+        chunk(opB, opA, ch + 1);
     }
+    if (ch < n_chunks) chunk(opA, opB, ch);
     for (int e = tid; e < kDK * kSeqCB; e += kMsNT) {
         const int i = e / kSeqCB, c = e % kSeqCB;
         Sp[(size_t)i * kDV + c0 + c] = Sc[c][i];
