@@ -107,7 +107,7 @@ int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, co
 // `n` counters of the current device's pool, in the range reserved for one
 // user (ranges never overlap, so no user sees another's values); nullptr if n
 // exceeds the range.  Every range starts zeroed.
-enum CounterUser : int { kCtrPrefill = 0, kCtrDeltaNetConv = 1, kCtrUsers = 2 };
+enum CounterUser : int { kCtrPrefill = 0, kCtrDeltaNetConv = 1, kCtrDecode = 2, kCtrUsers = 3 };
 uint32_t* counters(size_t n, CounterUser user);
 
 constexpr size_t kCounterPool = 1 << 16;

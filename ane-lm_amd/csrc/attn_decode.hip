@@ -6,9 +6,9 @@
 // and re-reads K/V per q head; here one workgroup owns (kv head, key split) and
 // scores all G = Hq/Hkv query heads of that kv head against each K/V row read
 // once.  Splits are merged with the standard (max, sum, unnormalised output)
-// log-sum-exp combine in a second small kernel (a kernel boundary publishes
-// the partials; an in-kernel last-block combine would need agent-scope fences,
-// each of which writes back the L2 of the issuing XCD).
+// log-sum-exp combine: for up to 16 splits of a ring by the last workgroup of
+// each kv head to finish (records handed over with device-coherent stores and
+// loads, an arrival counter per kv head), else in a second small kernel.
 #include "anelm_internal.hpp"
 
 #include <algorithm>
@@ -37,6 +37,7 @@ struct DecodeParams {
     float scale;
     int kps, max_splits;
     float* part;       // partials [seq][Hkv][max_splits][G][D+2]: m, l, o[D]
+    uint32_t* arrivals;   // ring mode, in-kernel merge: per-kv-head arrival counters (zero); else null
     // paged mode: pages [page][Hkv][page_size][D]; key t of sequence s is
     // row t % page_size of page page_table[s*max_pages + t/page_size]
     int paged;
@@ -64,14 +65,6 @@ struct DecodeParams {
     const float* rope_tab;
     int rope_rows;
     float theta;
-};
-
-// Per-workgroup view of its sequence.
-struct SeqView {
-    const float* q;
-    float* out;
-    int len, n_splits;
-    float* part;
 };
 
 template <typename KV> struct Raw8;
@@ -186,6 +179,32 @@ __device__ void norm_rope_rows(float (*rows)[D], const float* w, const DecodePar
     __syncthreads();
 }
 
+// In-kernel merge of the split records (ring mode, 2..kInlineMaxSplits
+// splits): each workgroup publishes its record with device-coherent stores,
+// waits for them to complete, and counts its arrival on the (sequence, kv
+// head) counter; the last to arrive reads every record of its kv head back
+// with device-coherent loads, merges them, writes the output and resets the
+// counter to zero (every counter is zero between calls).  Longer caches keep
+// the merge kernel: there one workgroup would read too many records.
+constexpr int kInlineMaxSplits = 16;
+constexpr int kArrivalWords = 256;                       // counters: n_seqs * n_kv_heads <= 256
+constexpr size_t kArrivalBytes = kArrivalWords * sizeof(uint32_t);
+
+// Records go through a buffer resource with the device-coherent cache policy
+// (sc1): plain loads and stores that pipeline, unlike atomic ones, each of
+// which waits for the previous.
+constexpr int kCoherent = 16;
+__device__ __forceinline__ void st_coherent(__amdgpu_buffer_rsrc_t r, int idx, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, idx * 4, 0, kCoherent);
+}
+__device__ __forceinline__ float ld_coherent(__amdgpu_buffer_rsrc_t r, int idx) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4, 0, kCoherent));
+}
+
+// Ring-mode decode: one workgroup per (key split, kv head).  Every memory
+// operand of the prologue (q rows, norm weights, the RoPE row, gate logits,
+// the new key / value, this split's K and V rows) is requested up front, so
+// the workgroup waits for one memory round trip before computing.
 template <typename KV, int D, int G>
 __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) {
     constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
@@ -193,73 +212,79 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     constexpr int KPB = kNW * KPI;    // key rows per workgroup instruction
     constexpr int KB = LPK / G;       // instructions batched per reduction
     constexpr int REC = D + 2;
+    constexpr int KPS = KPB * KB;     // keys per split (= 256 / G)
+    constexpr int NO = (G * D + kNT - 1) / kNT;   // output elements per thread
     static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
+    static_assert(D <= kNT, "one thread per head dimension");
 
-    __shared__ float q_s[G][D];
-    __shared__ float kn_s[D];
-    __shared__ float sc[G][256 / G];
+    __shared__ float q_s[G + 1][D];   // the G query rows, then (owner) the new key row
+    __shared__ float sc[G][KPS];
     __shared__ float red_o[kNW][G][D];
-    __shared__ float red[kNW];
-    __shared__ float red_g[kNW][G];
+    __shared__ float red_g[kNW][G + 1];
+    __shared__ float cs_s[kMaxRotPairs], sn_s[kMaxRotPairs];
+    __shared__ float ml_s[kInlineMaxSplits][G][2];
+    __shared__ int last_s;
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
-    const int seq = blockIdx.z;
-    const int Hkv = p.n_kv_heads;
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int sub = lane / LPK, dl = lane % LPK;
-
-    SeqView sv;
-    sv.len = p.paged ? min(p.seq_lens[seq], p.len) : p.len;
-    if (sv.len <= 0) {  // empty sequence: zeros, as cpu_ops.cpp:152-155
+    const int len = p.len;
+    float* const out = p.out + (size_t)kvh * G * D;
+    if (len <= 0) {  // empty cache: zeros, as cpu_ops.cpp:152-155
         if (split == 0)
-            for (int e = tid; e < G * D; e += kNT)
-                p.out[(size_t)seq * Hkv * G * D + (size_t)kvh * G * D + e] = 0.f;
+            for (int e = tid; e < G * D; e += kNT) out[e] = 0.f;
         return;
     }
-    sv.n_splits = (sv.len + p.kps - 1) / p.kps;
-    if (split >= sv.n_splits) return;
-    sv.q = p.q + (size_t)seq * Hkv * G * p.q_stride;
-    sv.out = p.out + (size_t)seq * Hkv * G * D;
-    sv.part = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * G * REC;
+    const int n_splits = (len + p.kps - 1) / p.kps;
+    if (split >= n_splits) return;
+    const bool inline_merge = p.arrivals != nullptr;
+    const bool finisher = n_splits == 1 || inline_merge;   // may write the output
+    float* const part = p.part + (size_t)kvh * p.max_splits * G * REC;
 
-    constexpr int KPS = KPB * KB;     // keys per split (= 256 / G)
     const int t0 = split * KPS;
-    const int nk = min(KPS, sv.len - t0);
+    const int nk = min(KPS, len - t0);
     const size_t tok_stride = (size_t)p.tok_stride, head_off = (size_t)kvh * p.head_stride;
     const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
     const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
-    const bool owner = p.fused && split == sv.n_splits - 1;   // holds the newest key
+    const bool owner = p.fused && split == n_splits - 1;   // holds the newest key
+    const float* qh = p.q + (size_t)kvh * G * p.q_stride;
 
-    // ---- the q rows are requested first (registers; D <= kNT), then every K
-    // and V row of this lane, so the q prologue below waits for q only (memory
-    // loads retire in issue order) and the K / V latency overlaps it
+    // ---- every operand requested at once
     float qv[G];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-        qv[g] = tid < D ? sv.q[(size_t)(kvh * G + g) * p.q_stride + tid] : 0.f;
-    // the newest key and value (split holding them) are requested now too, so
-    // the owner's prologue waits for one memory round trip, not two
+    for (int g = 0; g < G; g++) qv[g] = tid < D ? qh[(size_t)g * p.q_stride + tid] : 0.f;
+    float wq = 1.f, wk = 1.f;
+    if (p.fused && p.q_norm_w != nullptr && tid < D) wq = p.q_norm_w[tid];
     float kn_reg = 0.f, vn_reg = 0.f;
     float vn8[8];
     if (owner) {
         if (tid < D) {
             kn_reg = p.k_new[(size_t)kvh * D + tid];
             vn_reg = p.v_new[(size_t)kvh * D + tid];
+            if (p.k_norm_w != nullptr) wk = p.k_norm_w[tid];
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) vn8[i] = p.v_new[(size_t)kvh * D + dl * 8 + i];   // any alignment
     }
-    const int32_t* ptab = p.paged ? p.page_table + (size_t)seq * p.max_pages : nullptr;
+    // gate logits of this kv head's outputs (a workgroup that may write them)
+    float gl[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        const int e = tid + i * kNT, g = e / D, d = e % D;
+        gl[i] = (p.gate && finisher && e < G * D) ? qh[(size_t)g * p.q_stride + D + d] : 0.f;
+    }
+    if (p.fused && tid < p.rot_pairs) {
+        // cos / sin through pointers into the argument segment: indexing the
+        // by-value arrays directly expands into a select over every entry
+        const float* csp = p.cs;
+        const float* snp = p.sn;
+        cs_s[tid] = csp[tid];
+        sn_s[tid] = snp[tid];
+    }
     auto row_ptr = [&](const KV* base, int t) -> const KV* {
-        const int lt = t0 + t;
-        if (p.paged) {
-            const int page = min(max(ptab[lt / p.page_size], 0), p.n_pages - 1);
-            const int row = lt % p.page_size;
-            return base + (((size_t)page * Hkv + kvh) * p.page_size + row) * D + dl * 8;
-        }
-        int phys = p.start + lt;
+        int phys = p.start + t0 + t;
         if (phys >= p.cap) phys -= p.cap;
         return base + (size_t)phys * tok_stride + head_off + dl * 8;
     };
@@ -273,34 +298,63 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         }
     }
 
-    // ---- q rows (and, for the split holding the newest key, the append)
+    // ---- q rows (and the owner's key row): RMSNorm + RoPE in one reduction round
     if (tid < D) {
 #pragma unroll
         for (int g = 0; g < G; g++) q_s[g][tid] = qv[g];
+        q_s[G][tid] = kn_reg;
+    }
+    const int nrows = owner ? G + 1 : G;
+    if (p.fused) {
+        if (p.q_norm_w != nullptr) {
+            // partial sums in the order of block_sum: per wave, then over the waves
+            float ss[G + 1];
+#pragma unroll
+            for (int r = 0; r <= G; r++) {
+                const float v = tid < D ? (r < G ? qv[r] : kn_reg) : 0.f;
+                ss[r] = wave_sum(v * v);
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r <= G; r++) red_g[w][r] = ss[r];
+            }
+            __syncthreads();
+            if (tid < D) {
+#pragma unroll
+                for (int r = 0; r <= G; r++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int i = 0; i < kNW; i++) t += red_g[i][r];
+                    const float inv = 1.0f / sqrtf(t / (float)D + p.eps);
+                    q_s[r][tid] = (q_s[r][tid] * inv) * (r < G ? wq : wk);
+                }
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < nrows * p.rot_pairs; e += kNT) {
+            const int r = e / p.rot_pairs, j = e - r * p.rot_pairs;
+            const int i0 = p.rope_mode == 0 ? 2 * j : j;
+            const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
+            const float c = cs_s[j], sv = sn_s[j];
+            const float v0 = q_s[r][i0], v1 = q_s[r][i1];
+            rotate_pair(q_s[r][i0], q_s[r][i1], v0, v1, c, sv);
+        }
     }
     __syncthreads();
-    if (p.fused) {
-        // cos / sin read through pointers into the argument segment: indexing
-        // the by-value arrays directly expands into a select over every entry
-        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, p.cs, p.sn);
-        if (owner) {
-            if (tid < D) kn_s[tid] = kn_reg;
-            __syncthreads();
-            norm_rope_row<D>(kn_s, p.k_norm_w, p, red, p.cs, p.sn);
-            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
-            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
-            if (tid < D) {
-                store_kv(kw + tid, kn_s[tid]);
-                store_kv(vw + tid, vn_reg);
-            }
-            // The row loads above ran before the append: the newest key and
-            // value come from the prologue instead, rounded as stored.
+    if (owner) {
+        KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
+        KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
+        if (tid < D) {
+            store_kv(kw + tid, q_s[G][tid]);
+            store_kv(vw + tid, vn_reg);
+        }
+        // The row loads above ran before the append: the newest key and
+        // value come from the prologue instead, rounded as stored.
 #pragma unroll
-            for (int b = 0; b < KB; b++) {
-                if (b * KPB + w * KPI + sub == nk - 1) {
-                    rk[b] = make_raw<KV>(kn_s + dl * 8);
-                    rv[b] = make_raw<KV>(vn8);
-                }
+        for (int b = 0; b < KB; b++) {
+            if (b * KPB + w * KPI + sub == nk - 1) {
+                rk[b] = make_raw<KV>(&q_s[G][dl * 8]);
+                rv[b] = make_raw<KV>(vn8);
             }
         }
     }
@@ -313,7 +367,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
 
     // ---- scores: one transpose reduction over the KB rows of each lane
     {
-        float part[KB * G];
+        float part_s[KB * G];
 #pragma unroll
         for (int b = 0; b < KB; b++) {
             const int t = b * KPB + w * KPI + sub;
@@ -324,21 +378,34 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
                 float s = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; i++) s = fmaf(qr[g][i], kf[i], s);
-                part[b * G + g] = (t < nk) ? s : 0.f;
+                part_s[b * G + g] = (t < nk) ? s : 0.f;
             }
         }
-        transpose_reduce<LPK, KB * G>(part, dl);
+        transpose_reduce<LPK, KB * G>(part_s, dl);
         const int b = dl / G, g = dl % G;
         const int t = b * KPB + w * KPI + sub;
-        if (t < nk) sc[g][t] = part[0] * p.scale;
+        if (t < nk) sc[g][t] = part_s[0] * p.scale;
     }
     __syncthreads();
 
     // ---- softmax statistics per head over this split
-    // (one reduction round for all G heads each: the same per-wave partials
-    // and the same order over the waves as block_max / block_sum)
     float mloc[G], lloc[G];
-    {
+    if constexpr (KPS <= 64) {
+        // a head's KPS scores lie in one group of KPS lanes: thread tid holds
+        // key tid % KPS of head tid / KPS, reduced within its group
+        const int gg = tid / KPS, t = tid % KPS;
+        const float sv = t < nk ? sc[gg][t] : -INFINITY;
+        const float m = wave_max_from<KPS / 2>(sv);
+        const float e = t < nk ? __expf(sv - m) : 0.f;
+        const float l = wave_sum_from<KPS / 2>(e);
+        if (t < nk) sc[gg][t] = e;
+        if (t == 0) { ml_s[0][gg][0] = m; ml_s[0][gg][1] = l; }
+        __syncthreads();   // (also publishes the probabilities in sc)
+#pragma unroll
+        for (int g = 0; g < G; g++) { mloc[g] = ml_s[0][g][0]; lloc[g] = ml_s[0][g][1]; }
+        __syncthreads();   // ml_s is rewritten by the merge
+    } else {
+        // one reduction round for all G heads each over the waves
         float mw[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -359,8 +426,6 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
             mloc[g] = t;
         }
         __syncthreads();   // red_g is rewritten below
-    }
-    {
         float lw[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -420,28 +485,87 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     }
     __syncthreads();
 
-    // ---- output: direct when there is one split, else partial + combine
-    if (sv.n_splits == 1) {
-        for (int e = tid; e < G * D; e += kNT) {
+    // ---- output: direct when there is one split, else a record (+ merge)
+    if (n_splits == 1) {
+#pragma unroll
+        for (int i = 0; i < NO; i++) {
+            const int e = tid + i * kNT;
+            if (e >= G * D) break;
             const int g = e / D, d = e % D;
             float o = 0.f;
 #pragma unroll
             for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
-            const int h = kvh * G + g;
             float y = o / lloc[g];
-            if (p.gate) y = y / (1.0f + expf(-sv.q[(size_t)h * p.q_stride + D + d]));
-            sv.out[(size_t)h * D + d] = y;
+            if (p.gate) y = y / (1.0f + expf(-gl[i]));
+            out[e] = y;
         }
         return;
     }
-    float* rec = sv.part + (size_t)split * G * REC;
+    float* rec = part + (size_t)split * G * REC;
+    // this kv head's records (n_splits of them), device-coherent
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(part, 0, n_splits * G * REC * 4, 0x00020000);
     for (int e = tid; e < G * D; e += kNT) {
         const int g = e / D, d = e % D;
         float o = 0.f;
 #pragma unroll
         for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
-        rec[(size_t)g * REC + 2 + d] = o;
-        if (d == 0) { rec[(size_t)g * REC] = mloc[g]; rec[(size_t)g * REC + 1] = lloc[g]; }
+        if (inline_merge) {
+            const int ri = (split * G + g) * REC;
+            st_coherent(rr, ri + 2 + d, o);
+            if (d == 0) {
+                st_coherent(rr, ri, mloc[g]);
+                st_coherent(rr, ri + 1, lloc[g]);
+            }
+        } else {
+            rec[(size_t)g * REC + 2 + d] = o;
+            if (d == 0) { rec[(size_t)g * REC] = mloc[g]; rec[(size_t)g * REC + 1] = lloc[g]; }
+        }
+    }
+    if (!inline_merge) return;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // this thread's record stores completed
+    __syncthreads();
+    uint32_t* const ctr = p.arrivals + kvh;
+    if (tid == 0) last_s = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                           (uint32_t)(n_splits - 1);
+    __syncthreads();
+    if (!last_s) return;
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- merge: M = max m_s, L = sum l_s e^(m_s-M), O = sum o_s e^(m_s-M),
+    // out = O / L, then the sigmoid gate; every record load is issued before
+    // the first is used (one memory round trip)
+    float ov[NO][kInlineMaxSplits];
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        const int e = tid + i * kNT, g = (e / D) % G, d = e % D;
+#pragma unroll
+        for (int sp = 0; sp < kInlineMaxSplits; sp++)
+            ov[i][sp] = (sp < n_splits && e < G * D) ? ld_coherent(rr, (sp * G + g) * REC + 2 + d) : 0.f;
+    }
+    if (tid < n_splits * G) {
+        const int sp = tid / G, g = tid % G;
+        ml_s[sp][g][0] = ld_coherent(rr, (sp * G + g) * REC);
+        ml_s[sp][g][1] = ld_coherent(rr, (sp * G + g) * REC + 1);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        const int e = tid + i * kNT;
+        if (e >= G * D) break;
+        const int g = e / D;
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_splits; sp++) M = fmaxf(M, ml_s[sp][g][0]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < kInlineMaxSplits; sp++) {
+            if (sp < n_splits) {
+                const float wt = __expf(ml_s[sp][g][0] - M);
+                L += ml_s[sp][g][1] * wt;
+                O += ov[i][sp] * wt;
+            }
+        }
+        float y = O / L;
+        if (p.gate) y = y / (1.0f + expf(-gl[i]));
+        out[e] = y;
     }
 }
 
@@ -779,7 +903,7 @@ int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
         ANELM_LAUNCHED("attn_decode_kernel");
     }
-    if (p.max_splits > 1) {
+    if (p.max_splits > 1 && p.arrivals == nullptr) {
         dim3 cgrid(D / 64, grid.y * G, grid.z);
         hipLaunchKernelGGL((attn_combine_kernel<D, G>), cgrid, dim3(256), 0, st, p);
         ANELM_LAUNCHED("attn_combine_kernel");
@@ -837,15 +961,28 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
         p.head_stride = D;
     }
     const size_t need = part_bytes(n_heads, Hkv, D, n_seqs, max_len, p.paged != 0);
+    // ring mode with few splits: merged in the split kernel (arrival counters)
+    const bool merge_inline = !p.paged && max_splits >= 2 && max_splits <= kInlineMaxSplits &&
+                              Hkv * n_seqs <= kArrivalWords;
+    p.arrivals = nullptr;
     if (need > 0 && part != nullptr) {
-        if (need > part_cap)
+        // a caller's buffer holds the records from its start and, in its last
+        // kArrivalBytes (zero when the caller hands it over), the counters
+        if (need + (merge_inline ? kArrivalBytes : 0) > part_cap)
             return set_error(ANELM_ERANGE, "decode attention: %zu bytes of split partials, buffer holds %zu",
-                             need, part_cap);
+                             need + (merge_inline ? kArrivalBytes : 0), part_cap);
         p.part = part;
+        if (merge_inline)
+            p.arrivals = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(part) +
+                                                     ((part_cap - kArrivalBytes) & ~(size_t)255));
     } else if (need > 0) {
         float* ws = static_cast<float*>(workspace(need, st));
         if (!ws) return ANELM_ENOMEM;
         p.part = ws;
+        if (merge_inline) {
+            p.arrivals = counters((size_t)Hkv * n_seqs, kCtrDecode);
+            if (p.arrivals == nullptr) return ANELM_ENOMEM;
+        }
     } else {
         p.part = nullptr;
     }
@@ -1013,7 +1150,9 @@ int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, co
 }
 
 size_t full_attn_part_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len) {
-    return part_bytes(n_heads, n_kv_heads, head_dim, 1, max_len, false);
+    // records, plus the arrival counters at the end of a caller's buffer
+    const size_t b = part_bytes(n_heads, n_kv_heads, head_dim, 1, max_len, false);
+    return b > 0 ? ((b + 255) & ~(size_t)255) + kArrivalBytes : 0;
 }
 
 }  // namespace anelm

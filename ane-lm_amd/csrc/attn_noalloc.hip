@@ -10,7 +10,9 @@ namespace anelm {
 
 // ------------------------------------------------------ allocation-free entry
 // Split partials of anelm_full_attn_decode_noalloc live in this file-scope
-// device array (each device holds its own copy for the life of the process).
+// device array (each device holds its own copy for the life of the process);
+// its last 1 KiB holds the arrival counters of the in-kernel split merge,
+// zero at load and left zero by every call.
 // Host code never uses the symbol itself as an address: the array's device
 // address is looked up once per device with hipGetSymbolAddress and kept in
 // g_scratch_ptr.  Calls that overlap on one device share the array and race.

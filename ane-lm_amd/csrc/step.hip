@@ -156,6 +156,13 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
         if (rc == ANELM_OK && s->part_bytes > 0) {
             hipError_t e = hipMalloc(&s->part, s->part_bytes);
             if (e != hipSuccess) rc = hip_fail(e, "hipMalloc(step partials)");
+            // the arrival counters at its end start at zero (the launches
+            // leave them zero)
+            if (rc == ANELM_OK) {
+                e = hipMemset(s->part, 0, s->part_bytes);
+                if (e == hipSuccess) e = hipDeviceSynchronize();
+                if (e != hipSuccess) rc = hip_fail(e, "hipMemset(step partials)");
+            }
         }
         if (rc == ANELM_OK) {
             hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);

@@ -151,9 +151,10 @@ int anelm_full_attn_decode_kv(float* out, const float* q_gate, const float* k, c
  * arguments and results as anelm_full_attn_decode; the split partials live in
  * a static per-device array of 8 MiB (held by every device the library runs
  * on until the process ends), which bounds n_kv_heads * ceil(len / (256 / G))
- * * G * (head_dim + 2) * 4 bytes (len = keys attended after the append,
- * G = n_heads / n_kv_heads): 16 q / 4 kv heads at head_dim 256 attend up to
- * 32512 keys.  Larger calls return ANELM_ERANGE.  Calls that overlap on one
+ * * G * (head_dim + 2) * 4 bytes plus 1 KiB of split-merge counters (len =
+ * keys attended after the append, G = n_heads / n_kv_heads): 16 q / 4 kv
+ * heads at head_dim 256 attend up to
+ * 32448 keys.  Larger calls return ANELM_ERANGE.  Calls that overlap on one
  * device share that array and race; the library's first call on a device
  * that allocates (e.g. anelm_device_cus) is not needed before this one. */
 int anelm_full_attn_decode_noalloc(float* out, const float* q_gate, const float* k, const float* v,
