@@ -361,7 +361,10 @@ constexpr int kPmP = kPmA + kChunk * kChunk;   //   P [64][64]
 constexpr int kPmLg = kPmR + kCMat;            // lg[65] (+3 pad)
 constexpr int kPmBt = kPmLg + 68;              // beta[64]
 constexpr int kPmQs = kPmBt + kChunk;          // q row scale[64] (l2 norm and 1/sqrt(dk))
-constexpr int kPmLds = (kPmQs + kChunk) * 4;
+constexpr int kPmEb = kPmQs + kChunk;          // exp(lg[t + 1]) (decay-first) or exp(lg[t]): scales K in B
+constexpr int kPmEq = kPmEb + kChunk;          // exp(lg[t + 1]): scales q in Qh
+constexpr int kPmEk = kPmEq + kChunk;          // exp(lg_L - lg[t + 1]): scales K in Kh
+constexpr int kPmLds = (kPmEk + kChunk) * 4;
 
 __device__ __forceinline__ int sw128(int t, int d) { return t * kDK + 4 * ((d >> 2) ^ (t & 15)) + (d & 3); }
 __device__ __forceinline__ int sw64(int r, int c) { return r * kChunk + 4 * ((c >> 2) ^ (r & 15)) + (c & 3); }
@@ -379,6 +382,9 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
     float* lg = sm + kPmLg;
     float* bt = sm + kPmBt;
     float* qs = sm + kPmQs;
+    float* eb = sm + kPmEb;
+    float* eq = sm + kPmEq;
+    float* ek = sm + kPmEk;
     const int c = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lm = lane & 15, lk = lane >> 4;
@@ -491,6 +497,15 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
             lg[lane + 1] = x;
             if (lane == 0) lg[0] = 0.f;
             bt[lane] = bv;
+            // the per-row decay factors every lane of the value head uses
+            // (the same expressions as per element, evaluated once per row)
+            const float xs = __shfl_up(x, 1, 64);   // (every lane takes part in the shuffles)
+            const float xl = __shfl(x, 63, 64);     // lg_L
+            const float xp = lane == 0 ? 0.f : xs;  // lg[t]
+            const float e1 = expf(x);
+            eq[lane] = e1;
+            eb[lane] = TF ? e1 : expf(xp);
+            ek[lane] = expf(xl - x);
         }
         lds_barrier();
         // ---- Am = -A and P from the Gram tiles
@@ -544,7 +559,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int t = 4 * t4 + j;
-                    o4[j] = Ks[sw128(t, kd)] * expf(lgL - lg[t + 1]);
+                    o4[j] = Ks[sw128(t, kd)] * ek[t];
                 }
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o4), ro,
                                                        (4 * kCMat + kd * kChunk + 4 * t4) * 4, 0, 0);
@@ -565,8 +580,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int t = 16 * r + 4 * lk + e;
-                    acc[e] = bt[t] * (wpart ? Ks[sw128(t, 16 * (jt - 8) + lm)] * expf(TF ? lg[t + 1] : lg[t])
-                                            : pre[u][r][e]);
+                    acc[e] = bt[t] * (wpart ? Ks[sw128(t, 16 * (jt - 8) + lm)] * eb[t] : pre[u][r][e]);
                 }
 #pragma unroll
                 for (int s2 = 0; s2 < r; s2++) {
@@ -604,7 +618,7 @@ __global__ __launch_bounds__(kPmNT, 2) void dn_chunk_prep_mfma_kernel(
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ro, (ox + t * kDK + col) * 4,
                                                           0, 0);
                     float yv = y[e];
-                    if (wpart) yv = expf(lg[t + 1]) * (qs[t] * pre[u][r][e]) - yv;
+                    if (wpart) yv = eq[t] * (qs[t] * pre[u][r][e]) - yv;
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv), ro, (oy + t * kDK + col) * 4,
                                                           0, 0);
                 }
