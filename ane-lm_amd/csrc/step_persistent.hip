@@ -672,8 +672,10 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
     const float* qs = reinterpret_cast<const float*>(lds + kAqOff);
     const int Lg = tid, hw = Lg >> 5, dl = Lg & 31;
     // -- K rows (LDS) and V chunks (registers) of this wave have landed
+    const bool tw0 = wave == 0 && lane == 0;
     vm_drain();
     wg_sync();
+    trace_stamp(a, 3 * layer, kTrX0, tw0);
     // -- scores
     if (active && wave < kCW) {
         const int t_new = flags[0];
@@ -729,6 +731,7 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
         }
     }
     wg_sync();
+    trace_stamp(a, 3 * layer, kTrX1, tw0);
     // -- softmax statistics per q head (waves 0..3)
     if (active && wave < kAttnG) {
         const int g = wave;
@@ -748,6 +751,7 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
         }
     }
     wg_sync();
+    trace_stamp(a, 3 * layer, kTrX2, tw0);
     // -- P V, reduced over the 20 half-waves
     if (active && wave < kCW) {
         float acc[kAttnG][8];
@@ -786,6 +790,7 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
         }
     }
     wg_sync();
+    trace_stamp(a, 3 * layer, kTrX3, tw0);
     // -- split record: o[256], m, l per q head (device-coherent stores)
     if (active) {
         const int rec = kAttnRec;
@@ -802,7 +807,6 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
             stf_sc(pr + tid * rec + kAttnD + 1, nk > 0 ? ml[kAttnG + tid] : 0.f);
         }
     }
-    (void)layer;
 }
 
 // ================================================================= DeltaNet
