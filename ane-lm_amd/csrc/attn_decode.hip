@@ -223,6 +223,8 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     __shared__ float red_g[kNW][G + 1];
     __shared__ float cs_s[kMaxRotPairs], sn_s[kMaxRotPairs];
     __shared__ float ml_s[kInlineMaxSplits][G][2];
+    __shared__ float wl_s[kInlineMaxSplits][G];   // merge weights e^(m_s - M), zero past the last split
+    __shared__ float L_s[G];
     __shared__ int last_s;
 
     const int split = blockIdx.x;
@@ -539,7 +541,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         const int e = tid + i * kNT, g = (e / D) % G, d = e % D;
 #pragma unroll
         for (int sp = 0; sp < kInlineMaxSplits; sp++)
-            ov[i][sp] = (sp < n_splits && e < G * D) ? ld_coherent(rr, (sp * G + g) * REC + 2 + d) : 0.f;
+            ov[i][sp] = ld_coherent(rr, (sp * G + g) * REC + 2 + d);   // past the last split: 0 (buffer range)
     }
     if (tid < n_splits * G) {
         const int sp = tid / G, g = tid % G;
@@ -547,22 +549,33 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         ml_s[sp][g][1] = ld_coherent(rr, (sp * G + g) * REC + 1);
     }
     __syncthreads();
+    // one weight per (split, head), zero past the last split
+    if (tid < kInlineMaxSplits * G) {
+        const int sp = tid / G, g = tid % G;
+        float wt = 0.f;
+        if (sp < n_splits) {
+            float M = -INFINITY;
+            for (int s2 = 0; s2 < n_splits; s2++) M = fmaxf(M, ml_s[s2][g][0]);
+            wt = __expf(ml_s[sp][g][0] - M);
+        }
+        wl_s[sp][g] = wt;
+    }
+    __syncthreads();
+    if (tid < G) {
+        float L = 0.f;
+        for (int sp = 0; sp < n_splits; sp++) L += ml_s[sp][tid][1] * wl_s[sp][tid];
+        L_s[tid] = L;
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < NO; i++) {
         const int e = tid + i * kNT;
         if (e >= G * D) break;
         const int g = e / D;
-        float M = -INFINITY;
-        for (int sp = 0; sp < n_splits; sp++) M = fmaxf(M, ml_s[sp][g][0]);
-        float L = 0.f, O = 0.f;
+        float O = 0.f;
 #pragma unroll
-        for (int sp = 0; sp < kInlineMaxSplits; sp++) {
-            if (sp < n_splits) {
-                const float wt = __expf(ml_s[sp][g][0] - M);
-                L += ml_s[sp][g][1] * wt;
-                O += ov[i][sp] * wt;
-            }
-        }
+        for (int sp = 0; sp < kInlineMaxSplits; sp++) O = fmaf(wl_s[sp][g], ov[i][sp], O);
+        const float L = L_s[g];
         float y = O / L;
         if (p.gate) y = y / (1.0f + expf(-gl[i]));
         out[e] = y;
