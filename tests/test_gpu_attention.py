@@ -89,6 +89,24 @@ def test_full_attn_decode_variants(anelm, orc, dev, rope_mode, gate):
     _check_decode(_run_decode(anelm, c, dev, rope_mode, gate), _oracle_decode(orc, c, rope_mode, gate))
 
 
+@pytest.mark.parametrize("n_heads,n_kv_heads,head_dim,cached", [
+    (8, 2, 256, 127),    # G 4, 64-key splits: 2 splits, the smallest in-kernel merge
+    (8, 2, 256, 1023),   # 16 splits, the largest merged in the split kernel
+    (8, 2, 256, 1024),   # 17 splits: the merge kernel
+    (16, 2, 128, 300),   # G 8, 32-key splits: 10 splits
+    (4, 2, 128, 700),    # G 2, 128-key splits (workgroup-wide softmax): 6 splits
+    (4, 4, 64, 1000),    # G 1, 256-key splits: 4 splits
+])
+def test_full_attn_decode_split_merge(anelm, orc, dev, n_heads, n_kv_heads, head_dim, cached):
+    """Split counts around the in-kernel merge of the split records (up to 16
+    splits of 256/G keys merged by the last workgroup of each kv head, more by
+    a second kernel) and the other head groupings, over a wrapped ring,
+    against the oracle."""
+    c = attn_decode_case(330 + cached % 97, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+                         cached=cached, capacity=cached + 5, start=7)
+    _check_decode(_run_decode(anelm, c, dev), _oracle_decode(orc, c))
+
+
 def test_full_attn_decode_table_row(anelm, orc, dev):
     """cos/sin passed as the reference's table row give the same step."""
     c = attn_decode_case(305)
