@@ -205,22 +205,31 @@ __device__ __forceinline__ float ld_coherent(__amdgpu_buffer_rsrc_t r, int idx) 
 // operand of the prologue (q rows, norm weights, the RoPE row, gate logits,
 // the new key / value, this split's K and V rows) is requested up front, so
 // the workgroup waits for one memory round trip before computing.
+// Threads of a ring-decode workgroup: 8 waves for G <= 4 (each lane holds half
+// the key rows of the 4-wave layout: the per-wave score and P V work halves),
+// 4 waves for G = 8.
+template <int G>
+constexpr int ring_threads() { return G <= 4 ? 512 : 256; }
+
 template <typename KV, int D, int G>
-__global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(ring_threads<G>()) void attn_decode_kernel(const DecodeParams p) {
+    constexpr int NT = ring_threads<G>();
+    constexpr int NW = NT / 64;
     constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
     constexpr int KPI = 64 / LPK;     // key rows per wave instruction
-    constexpr int KPB = kNW * KPI;    // key rows per workgroup instruction
-    constexpr int KB = LPK / G;       // instructions batched per reduction
+    constexpr int KPB = NW * KPI;     // key rows per workgroup instruction
+    constexpr int KPS = 256 / G;      // keys per split
+    constexpr int KB = KPS / KPB;     // key rows per lane
+    constexpr int R = KB * G;         // partial dots per lane (LPK, or LPK / 2 with 8 waves)
     constexpr int REC = D + 2;
-    constexpr int KPS = KPB * KB;     // keys per split (= 256 / G)
-    constexpr int NO = (G * D + kNT - 1) / kNT;   // output elements per thread
-    static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
-    static_assert(D <= kNT, "one thread per head dimension");
+    constexpr int NO = (G * D + NT - 1) / NT;   // output elements per thread
+    static_assert(KB >= 1 && KB * KPB == KPS && (R == LPK || 2 * R == LPK), "split layout");
+    static_assert(D <= NT, "one thread per head dimension");
 
     __shared__ float q_s[G + 1][D];   // the G query rows, then (owner) the new key row
     __shared__ float sc[G][KPS];
-    __shared__ float red_o[kNW][G][D];
-    __shared__ float red_g[kNW][G + 1];
+    __shared__ float red_o[NW][G][D];
+    __shared__ float red_g[NW][G + 1];
     __shared__ float cs_s[kMaxRotPairs], sn_s[kMaxRotPairs];
     __shared__ float ml_s[kInlineMaxSplits][G][2];
     __shared__ float wl_s[kInlineMaxSplits][G];   // merge weights e^(m_s - M), zero past the last split
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     float* const out = p.out + (size_t)kvh * G * D;
     if (len <= 0) {  // empty cache: zeros, as cpu_ops.cpp:152-155
         if (split == 0)
-            for (int e = tid; e < G * D; e += kNT) out[e] = 0.f;
+            for (int e = tid; e < G * D; e += NT) out[e] = 0.f;
         return;
     }
     const int n_splits = (len + p.kps - 1) / p.kps;
@@ -274,7 +283,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     float gl[NO];
 #pragma unroll
     for (int i = 0; i < NO; i++) {
-        const int e = tid + i * kNT, g = e / D, d = e % D;
+        const int e = tid + i * NT, g = e / D, d = e % D;
         gl[i] = (p.gate && finisher && e < G * D) ? qh[(size_t)g * p.q_stride + D + d] : 0.f;
     }
     if (p.fused && tid < p.rot_pairs) {
@@ -326,14 +335,14 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
                 for (int r = 0; r <= G; r++) {
                     float t = 0.f;
 #pragma unroll
-                    for (int i = 0; i < kNW; i++) t += red_g[i][r];
+                    for (int i = 0; i < NW; i++) t += red_g[i][r];
                     const float inv = 1.0f / sqrtf(t / (float)D + p.eps);
                     q_s[r][tid] = (q_s[r][tid] * inv) * (r < G ? wq : wk);
                 }
             }
         }
         __syncthreads();
-        for (int e = tid; e < nrows * p.rot_pairs; e += kNT) {
+        for (int e = tid; e < nrows * p.rot_pairs; e += NT) {
             const int r = e / p.rot_pairs, j = e - r * p.rot_pairs;
             const int i0 = p.rope_mode == 0 ? 2 * j : j;
             const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
@@ -383,10 +392,16 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
                 part_s[b * G + g] = (t < nk) ? s : 0.f;
             }
         }
-        transpose_reduce<LPK, KB * G>(part_s, dl);
-        const int b = dl / G, g = dl % G;
+        if constexpr (R == LPK) {
+            transpose_reduce<LPK, R>(part_s, dl);
+        } else {
+            // R values over 2R lanes: within each R-lane half, then across the halves
+            transpose_reduce<R, R>(part_s, dl % R);
+            part_s[0] += shfl_xor(part_s[0], R);
+        }
+        const int b = (dl % R) / G, g = dl % G;
         const int t = b * KPB + w * KPI + sub;
-        if (t < nk) sc[g][t] = part_s[0] * p.scale;
+        if (t < nk && dl < R) sc[g][t] = part_s[0] * p.scale;
     }
     __syncthreads();
 
@@ -395,13 +410,16 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     if constexpr (KPS <= 64) {
         // a head's KPS scores lie in one group of KPS lanes: thread tid holds
         // key tid % KPS of head tid / KPS, reduced within its group
-        const int gg = tid / KPS, t = tid % KPS;
-        const float sv = t < nk ? sc[gg][t] : -INFINITY;
+        // (threads past G * KPS hold no score)
+        const bool own = tid < G * KPS;
+        const int gg = own ? tid / KPS : 0, t = tid % KPS;
+        const bool hit = own && t < nk;
+        const float sv = hit ? sc[gg][t] : -INFINITY;
         const float m = wave_max_from<KPS / 2>(sv);
-        const float e = t < nk ? __expf(sv - m) : 0.f;
+        const float e = hit ? __expf(sv - m) : 0.f;
         const float l = wave_sum_from<KPS / 2>(e);
-        if (t < nk) sc[gg][t] = e;
-        if (t == 0) { ml_s[0][gg][0] = m; ml_s[0][gg][1] = l; }
+        if (hit) sc[gg][t] = e;
+        if (own && t == 0) { ml_s[0][gg][0] = m; ml_s[0][gg][1] = l; }
         __syncthreads();   // (also publishes the probabilities in sc)
 #pragma unroll
         for (int g = 0; g < G; g++) { mloc[g] = ml_s[0][g][0]; lloc[g] = ml_s[0][g][1]; }
@@ -412,7 +430,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float m = -INFINITY;
-            for (int t = tid; t < nk; t += kNT) m = fmaxf(m, sc[g][t]);
+            for (int t = tid; t < nk; t += NT) m = fmaxf(m, sc[g][t]);
             mw[g] = wave_max(m);
         }
         if (lane == 0) {
@@ -424,7 +442,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         for (int g = 0; g < G; g++) {
             float t = red_g[0][g];
 #pragma unroll
-            for (int i = 1; i < kNW; i++) t = fmaxf(t, red_g[i][g]);
+            for (int i = 1; i < NW; i++) t = fmaxf(t, red_g[i][g]);
             mloc[g] = t;
         }
         __syncthreads();   // red_g is rewritten below
@@ -432,7 +450,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float l = 0.f;
-            for (int t = tid; t < nk; t += kNT) {
+            for (int t = tid; t < nk; t += NT) {
                 const float e = __expf(sc[g][t] - mloc[g]);
                 sc[g][t] = e;
                 l += e;
@@ -448,7 +466,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
         for (int g = 0; g < G; g++) {
             float t = 0.f;
 #pragma unroll
-            for (int i = 0; i < kNW; i++) t += red_g[i][g];
+            for (int i = 0; i < NW; i++) t += red_g[i][g];
             lloc[g] = t;
         }
     }
@@ -491,12 +509,12 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     if (n_splits == 1) {
 #pragma unroll
         for (int i = 0; i < NO; i++) {
-            const int e = tid + i * kNT;
+            const int e = tid + i * NT;
             if (e >= G * D) break;
             const int g = e / D, d = e % D;
             float o = 0.f;
 #pragma unroll
-            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+            for (int ww = 0; ww < NW; ww++) o += red_o[ww][g][d];
             float y = o / lloc[g];
             if (p.gate) y = y / (1.0f + expf(-gl[i]));
             out[e] = y;
@@ -506,11 +524,11 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     float* rec = part + (size_t)split * G * REC;
     // this kv head's records (n_splits of them), device-coherent
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(part, 0, n_splits * G * REC * 4, 0x00020000);
-    for (int e = tid; e < G * D; e += kNT) {
+    for (int e = tid; e < G * D; e += NT) {
         const int g = e / D, d = e % D;
         float o = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+        for (int ww = 0; ww < NW; ww++) o += red_o[ww][g][d];
         if (inline_merge) {
             const int ri = (split * G + g) * REC;
             st_coherent(rr, ri + 2 + d, o);
@@ -538,7 +556,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     float ov[NO][kInlineMaxSplits];
 #pragma unroll
     for (int i = 0; i < NO; i++) {
-        const int e = tid + i * kNT, g = (e / D) % G, d = e % D;
+        const int e = tid + i * NT, g = (e / D) % G, d = e % D;
 #pragma unroll
         for (int sp = 0; sp < kInlineMaxSplits; sp++)
             ov[i][sp] = ld_coherent(rr, (sp * G + g) * REC + 2 + d);   // past the last split: 0 (buffer range)
@@ -569,7 +587,7 @@ __global__ __launch_bounds__(kNT) void attn_decode_kernel(const DecodeParams p) 
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NO; i++) {
-        const int e = tid + i * kNT;
+        const int e = tid + i * NT;
         if (e >= G * D) break;
         const int g = e / D;
         float O = 0.f;
@@ -913,7 +931,7 @@ int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_paged_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
         ANELM_LAUNCHED("attn_paged_kernel");
     } else {
-        hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
+        hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(ring_threads<G>()), 0, st, p);
         ANELM_LAUNCHED("attn_decode_kernel");
     }
     if (p.max_splits > 1 && p.arrivals == nullptr) {
