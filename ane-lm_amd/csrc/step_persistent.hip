@@ -831,7 +831,8 @@ __device__ __forceinline__ void dn_prefetch(Buf<kDnBuf>& b, const PArgs& a, cons
 }
 
 constexpr int kDqOff = kLdsMisc;            // q[128] k[128] v[16] ... beta decay at 384
-constexpr int kDredOff = kLdsMisc + 4096;   // [8][16] partials
+constexpr int kDredOff = kLdsMisc + 4096;   // [8][16] partials of k.S
+constexpr int kDyOff = kDredOff + 512;      // [8][16] partials of the outputs
 
 // Control wave, two parts.  dn_stage_load reads this step's inputs of the
 // slab (q and k of its key head, its 16 v columns, the gate inputs) into
@@ -902,6 +903,7 @@ __device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int
     const bool active = hd < a.Hv;
     const float* s = reinterpret_cast<const float*>(lds + kDqOff);
     float* red = reinterpret_cast<float*>(lds + kDredOff);
+    float* ry = reinterpret_cast<float*>(lds + kDyOff);
     const bool tf = (L.dn_flags & ANELM_DN_ORDER_TRANSFORMERS) != 0;
     const int Lg = wave * 64 + lane, r = Lg >> 2, cq = Lg & 3;
     const bool holder = active && wave < 8;
@@ -943,23 +945,24 @@ __device__ float dn_compute(Buf<kDnBuf>& b, const PArgs& a, const PLayer& L, int
             st[j] = n;
             yp[j] = sum_rows16(n * qr);
         }
+        // the output partials go to LDS before the state store is issued: a
+        // store waiting for room in the CU's memory queue stalls its wave
+        if (lane < 4) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) ry[wave * kDnCols + 4 * cq + j] = yp[j];
+        }
         f32x4 o;
         o.x = st[0]; o.y = st[1]; o.z = st[2]; o.w = st[3];
         *reinterpret_cast<f32x4*>(L.state + (size_t)hd * kDnD * kDnD + (size_t)r * kDnD + kDnCols * c + 4 * cq) = o;
     }
-    wg_sync();   // Sk partials consumed
+    wg_sync();   // Sk partials consumed, output partials complete
     trace_stamp(a, p, kTrX2, tw0);
-    if (holder && lane < 4) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) red[wave * kDnCols + 4 * cq + j] = yp[j];
-    }
-    wg_sync();
     trace_stamp(a, p, kTrX3, tw0);
     float y = 0.f;
     if (active && wave == kCtl) {
         if (lane < kDnCols) {
 #pragma unroll
-            for (int w = 0; w < 8; w++) y += red[w * kDnCols + lane];
+            for (int w = 0; w < 8; w++) y += ry[w * kDnCols + lane];
         }
         if (L.dn_flags & ANELM_DN_GATED_NORM) {
             const float ss = wave_sum(lane < kDnCols ? y * y : 0.f);
