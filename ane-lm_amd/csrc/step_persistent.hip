@@ -836,7 +836,8 @@ constexpr int kDyOff = kDredOff + 512;      // [8][16] partials of the outputs
 
 // Control wave, two parts.  dn_stage_load reads this step's inputs of the
 // slab (q and k of its key head, its 16 v columns, the gate inputs) into
-// registers before the barrier the core waits on; dn_stage_fin, after it:
+// registers before the barrier the core waits on; dn_stage_fin, while that
+// barrier resolves (the inputs are step constants):
 // l2 norm of q, k (cpu_ops.cpp:82-87), q scale (qwen3_5.cpp:879-887), beta and
 // decay (qwen3_5.cpp:896-898) into LDS.
 struct DnStage {
@@ -1357,7 +1358,13 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         AttnStage as;
         DnStage ds;
         if constexpr (NEXT == kATT) attn_stage_load(a, Ln, ln, as);
-        else if constexpr (NEXT == kDN) dn_stage_load(a, Ln, ln, ds);
+        else if constexpr (NEXT == kDN) {
+            dn_stage_load(a, Ln, ln, ds);
+            // q/k norms, beta and decay into LDS while the barrier resolves:
+            // they depend on step constants only, and the region (the down
+            // phase's row sums, read before the arrival) is free
+            dn_stage_fin(a, Ln, ln, lds, ds);
+        }
         const int okw = more ? (int)ctl_wait(a, p0 + 2, ln) : 1;
         trace_stamp(a, p0 + 2, kTrRelease, twc);
         if (ln == 0) ctl[0] = okw;
@@ -1366,7 +1373,6 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
             stage_x_load<JH>(a, ln, lds);
             stage_w<JH>(a, Ln.ffn_norm_w, ln, lds);
             if constexpr (NEXT == kATT) attn_stage_fin(a, Ln, ln, lds, as);
-            else if constexpr (NEXT == kDN) dn_stage_fin(a, Ln, ln, lds, ds);
         }
     } else if constexpr (NEXT == kATT) {
         attn_prefetch<NKJ>(next_buf, a, Ln, wave, ln, lds);
