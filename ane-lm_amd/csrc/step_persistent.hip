@@ -1409,6 +1409,15 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     LutRegs glr;
     Buf<8 * kNDG> gd;
     trace_stamp(a, kMaxPhases, 0, tid == 0);
+#if ANELM_STEP_TRACE
+    if (tid == 0) {
+        // placement of this workgroup (trace build only): HW_ID and XCC_ID
+        a.trace[((size_t)blockIdx.x * (kMaxPhases + 1) + kMaxPhases) * kTrEv + 2] =
+            (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+        a.trace[((size_t)blockIdx.x * (kMaxPhases + 1) + kMaxPhases) * kTrEv + 3] =
+            (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 20);
+    }
+#endif
     // phase 0: core of layer 0 (inputs are ready at launch)
     dn_prefetch(cdn, a, L0, wave, lane);
     if (wave == kCtl) {
