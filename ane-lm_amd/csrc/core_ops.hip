@@ -158,27 +158,38 @@ __global__ void conv1d_kernel(float* y, float* st, const float* x, const float* 
 }
 
 // core/cpu_ops.cpp:131-146 for one head; one thread per value column j keeps
-// its column of the state in registers between the two passes.
+// its column of the state in registers between the two passes when it fits
+// (key_dim <= 128); a 256-long column would spill to scratch, so it is read
+// again (from cache) in the second pass instead.
 template <int DK>
 __global__ __launch_bounds__(kNT) void ssm_step_kernel(float* y, float* S, const float* q,
                                                        const float* k, const float* v, float decay,
                                                        float beta, int dv, int order) {
+    constexpr bool kHold = DK <= 128;
+    constexpr int kUnroll = kHold ? DK : 16;   // a fully unrolled re-read would reuse the first loads
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= dv) return;
-    float col[DK];
+    float col[kHold ? DK : 1];
     float sk = 0.f;
-#pragma unroll
+#pragma unroll kUnroll
     for (int i = 0; i < DK; i++) {
         float s = S[(size_t)i * dv + j];
         if (order) s = decay * s;
-        col[i] = s;
+        if constexpr (kHold) col[i] = s;
         sk = fmaf(s, k[i], sk);
     }
     const float delta = order ? (v[j] - sk) * beta : v[j] - sk;
     float yo = 0.f;
-#pragma unroll
+#pragma unroll kUnroll
     for (int i = 0; i < DK; i++) {
-        float s = order ? fmaf(k[i], delta, col[i]) : fmaf(beta * k[i], delta, decay * col[i]);
+        float c;
+        if constexpr (kHold) {
+            c = col[i];
+        } else {
+            c = S[(size_t)i * dv + j];
+            if (order) c = decay * c;
+        }
+        float s = order ? fmaf(k[i], delta, c) : fmaf(beta * k[i], delta, decay * c);
         S[(size_t)i * dv + j] = s;
         yo = fmaf(s, q[i], yo);
     }

@@ -1298,7 +1298,12 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     }
     wg_sync();   // the bulk loads below queue behind the arrival
     constexpr int NAD = NID / 2;     // weights issued before the barrier
-    constexpr int NDD = NAD;         // of them decoded before the input (all that were issued)
+    // of them decoded before the input: all that were issued, except after an
+    // attention layer's merge, where holding more decoded instructions across
+    // the barrier pushes live registers past the 3-waves-per-SIMD budget and
+    // the compiler spills them to scratch (reloaded one at a time, each queued
+    // behind the bulk weight loads)
+    constexpr int NDD = KIND == kATT ? (NAD < 2 ? NAD : 2) : NAD;
     Buf<8 * NDD> dd;
     ln = opaque(lane);
     if (wave == kCtl) {
@@ -1402,6 +1407,9 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the control wave's staging, merges and barrier work are on the critical
+    // path; the compute waves sharing its SIMD yield issue slots to it
+    if (wave == kCtl) __builtin_amdgcn_s_setprio(3);
     int* ctl = ctl_ints(lds);
     Buf<kDnBuf> cdn;
     Buf<4 * NKJ> cat;

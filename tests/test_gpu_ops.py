@@ -78,10 +78,13 @@ def test_conv1d_update_steps(anelm, orc, dev):
 
 
 @pytest.mark.parametrize("order", [0, 1])
-def test_ssm_step_single_head(anelm, orc, dev, order):
-    rng = np.random.default_rng(104 + order)
-    S = (0.1 * rng.standard_normal((128, 128))).astype(np.float32)
-    q, k, v = (rng.standard_normal(128).astype(np.float32) for _ in range(3))
+@pytest.mark.parametrize("dk,dv", [(128, 128), (256, 300), (64, 70)])
+def test_ssm_step_single_head(anelm, orc, dev, order, dk, dv):
+    """key_dim 256 re-reads its state column in the second pass; 64 and 128 hold it."""
+    rng = np.random.default_rng(104 + order + dk)
+    S = (0.1 * rng.standard_normal((dk, dv))).astype(np.float32)
+    q, k = (rng.standard_normal(dk).astype(np.float32) for _ in range(2))
+    v = rng.standard_normal(dv).astype(np.float32)
     tS = to_dev(S, dev)
     y = anelm.ops.ssm_step(tS, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 0.9, 0.4,
                            2 if order else 0)
