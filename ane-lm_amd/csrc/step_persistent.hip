@@ -81,7 +81,7 @@ constexpr long kFinOff = kRelOff + (long)kMaxPhases * kNG * kPad;
 constexpr long kAbortOff = kFinOff + kPad;
 constexpr long kStatusOff = kAbortOff + kPad;
 constexpr long kSyncWords = kStatusOff + kPad;
-constexpr int kSpinLimit = 1 << 22;   // ~0.1-0.5 s of polling before abort
+constexpr int kSpinLimit = 1 << 19;   // ~0.7 s of polling (a poll ~1.4 us apart) before abort
 
 // ------------------------------------------------------------------ LDS map
 constexpr int kLdsTab = 0;            // 6 pair tables x 16 KiB (GEMV); attention scratch
@@ -309,7 +309,9 @@ __device__ bool bar_wait(unsigned* sync, int p) {
     for (int it = 0; it < kSpinLimit; it++) {
         if (scalar_word(f)) return true;
         if ((it & 255) == 255 && scalar_word(sync + kAbortOff)) return false;
-        __builtin_amdgcn_s_sleep(2);
+        // ~0.85 us between polls: 256 pollers at a shorter period slow the
+        // arrivals' atomics on the same L2 more than the later sighting costs
+        __builtin_amdgcn_s_sleep(32);
     }
     st_sc(sync + kAbortOff, 1u);
     st_sc(sync + kStatusOff, 1u);
