@@ -40,6 +40,7 @@ _FP = ctypes.POINTER(ctypes.c_float)
 SIGNATURES = {
     "anelm_version": [],
     "anelm_device_cus": [],
+    "anelm_stream_release": [_P],
     "anelm_rmsnorm": [_P, _P, _P, _I, _I, _I, _I, _F, _P],
     "anelm_rmsnorm_gated": [_P, _P, _P, _P, _I, _I, _P],
     "anelm_l2_normalize": [_P, _I, _I, _P],
@@ -84,6 +85,7 @@ SIGNATURES = {
     "anelm_hybrid_step_trace": [_P, _P, ctypes.c_size_t, _IP, _IP],
     "anelm_batch_step_create": [ctypes.POINTER(_P), _P, _P, _I, _P, _P],
     "anelm_batch_step_run": [_P, _I, _P],
+    "anelm_batch_step_status": [_P, _IP],
     "anelm_batch_step_destroy": [_P],
     # compat tier (host pointers, synchronous)
     "anelm_cpu_silu_vec_inplace": [_P, _I, _P],

@@ -7,6 +7,9 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <mutex>
+#include <vector>
+
 #include "../../include/anelm.h"
 
 namespace anelm {
@@ -40,28 +43,41 @@ int hip_fail(hipError_t e, const char* what);
         if (e_ != hipSuccess) return ::anelm::hip_fail(e_, name); \
     } while (0)
 
-// Per-device state.  `ws` is a growable scratch buffer (contents undefined
-// between calls); `counters` is a zeroed uint32 array that kernels use for
-// last-block-done reductions and always leave zeroed again.
-struct Device {
-    int id = -1;
-    int num_cus = 0;
+// State of one (device, stream) pair: growable scratch buffers (contents
+// undefined between calls) and a uint32 counter pool that kernels use for
+// last-block-done reductions and always leave zeroed again.  Calls on
+// different streams never share any of it, so they may run concurrently;
+// calls on one stream are ordered by the stream.
+struct StreamState {
+    hipStream_t stream = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
     void* ws2 = nullptr;      // second slot: split-K partials of the batched GEMM
     size_t ws2_bytes = 0;
     uint32_t* counters = nullptr;
-    size_t n_counters = 0;
+    std::mutex mu;            // guards growth of ws / ws2
+};
+
+struct Device {
+    int id = -1;
+    int num_cus = 0;
+    std::mutex mu;                         // guards `streams`
+    std::vector<StreamState*> streams;
 };
 
 // Current device's state (lazily initialised).  nullptr on failure with the
 // error recorded.
 Device* device();
 
-// Workspace of at least `bytes` on the current device (grows with a stream
-// sync + free + malloc).  Returns nullptr on failure with the error recorded.
+// State of `stream` on the current device (created on first use).
+StreamState* stream_state(hipStream_t stream);
+// Frees the state of `stream` on the current device (after syncing it).
+int stream_release(hipStream_t stream);
+
+// Workspace of `stream` of at least `bytes` (grows with a sync of that stream
+// + free + malloc).  Returns nullptr on failure with the error recorded.
 void* workspace(size_t bytes, hipStream_t stream);
-// Same, from a second per-device buffer (for callees of a workspace user).
+// Same, from a second buffer of the stream (for callees of a workspace user).
 void* workspace2(size_t bytes, hipStream_t stream);
 
 // Workgroup barrier for LDS exchange only: this wave's LDS operations
@@ -104,11 +120,11 @@ int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, co
                              int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
                              int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
 
-// `n` counters of the current device's pool, in the range reserved for one
-// user (ranges never overlap, so no user sees another's values); nullptr if n
-// exceeds the range.  Every range starts zeroed.
+// `n` counters of the pool of `stream` on the current device, in the range
+// reserved for one user (ranges never overlap, so no user sees another's
+// values); nullptr if n exceeds the range.  Every range starts zeroed.
 enum CounterUser : int { kCtrPrefill = 0, kCtrDeltaNetConv = 1, kCtrDecode = 2, kCtrUsers = 3 };
-uint32_t* counters(size_t n, CounterUser user);
+uint32_t* counters(size_t n, CounterUser user, hipStream_t stream);
 
 constexpr size_t kCounterPool = 1 << 16;
 constexpr size_t kCounterRange = kCounterPool / 4;   // counters per user

@@ -1011,7 +1011,7 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
         if (!ws) return ANELM_ENOMEM;
         p.part = ws;
         if (merge_inline) {
-            p.arrivals = counters((size_t)Hkv * n_seqs, kCtrDecode);
+            p.arrivals = counters((size_t)Hkv * n_seqs, kCtrDecode, st);
             if (p.arrivals == nullptr) return ANELM_ENOMEM;
         }
     } else {

@@ -450,7 +450,7 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     const size_t part_bytes = (size_t)2 * units * kGSlotFloats * sizeof(float);
     char* ws = static_cast<char*>(workspace(vt_bytes + part_bytes, st));
     if (!ws) return ANELM_ENOMEM;
-    uint32_t* ctr = counters(units, kCtrPrefill);   // zeroed; each call leaves them zeroed
+    uint32_t* ctr = counters(units, kCtrPrefill, st);   // zeroed; each call leaves them zeroed
     if (!ctr) return ANELM_ERANGE;
     _Float16* vt = reinterpret_cast<_Float16*>(ws);
     float* part = reinterpret_cast<float*>(ws + vt_bytes);

@@ -24,14 +24,22 @@ struct anelm_batch_step {
     float* xn = nullptr;       // [B][H]
     float* gu = nullptr;       // [B][2I]
     float* h = nullptr;        // [B][I]
+    int32_t* status = nullptr; // device word: a sequence reached max_seq_len
 };
 
 namespace anelm {
 namespace {
 
-__global__ void advance_kernel(int32_t* seq_lens, int32_t* positions, int n) {
+// A sequence whose cache held max_seq_len keys before the step appended
+// nothing (anelm_attn_decode_paged_step): it does not advance, and the step's
+// status word records that it hit the limit.
+__global__ void advance_kernel(int32_t* seq_lens, int32_t* positions, int n, int max_seq_len, int32_t* status) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
+        if (seq_lens[i] >= max_seq_len) {
+            *status = 1;
+            return;
+        }
         seq_lens[i] += 1;
         if (positions) positions[i] += 1;
     }
@@ -81,6 +89,8 @@ extern "C" int anelm_batch_step_create(anelm_batch_step** out, const anelm_hybri
     hipError_t e = hipMalloc(&s->xn, B * H * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&s->gu, B * 2 * I * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&s->h, B * I * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&s->status, sizeof(int32_t));
+    if (e == hipSuccess) e = hipMemset(s->status, 0, sizeof(int32_t));
     if (e != hipSuccess) {
         anelm_batch_step_destroy(s);
         return hip_fail(e, "hipMalloc(batch step scratch)");
@@ -129,14 +139,25 @@ extern "C" int anelm_batch_step_run(anelm_batch_step* s, int advance, void* stre
     }
     if (advance) {
         hipLaunchKernelGGL(advance_kernel, dim3((B + 255) / 256), dim3(256), 0, as_stream(stream), q.seq_lens,
-                           q.positions, B);
+                           q.positions, B, q.max_seq_len, s->status);
         ANELM_LAUNCHED("advance_kernel");
     }
     return ANELM_OK;
 }
 
+extern "C" int anelm_batch_step_status(anelm_batch_step* s, int* status) {
+    ANELM_NONNULL(s);
+    ANELM_NONNULL(status);
+    int32_t v = 0;
+    ANELM_HIP(hipMemcpy(&v, s->status, sizeof(v), hipMemcpyDeviceToHost));
+    *status = v;
+    if (v) ANELM_HIP(hipMemset(s->status, 0, sizeof(int32_t)));
+    return ANELM_OK;
+}
+
 extern "C" int anelm_batch_step_destroy(anelm_batch_step* s) {
     if (!s) return ANELM_OK;
+    if (s->status) (void)hipFree(s->status);
     if (s->xn) (void)hipFree(s->xn);
     if (s->gu) (void)hipFree(s->gu);
     if (s->h) (void)hipFree(s->h);

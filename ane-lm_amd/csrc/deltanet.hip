@@ -908,8 +908,9 @@ extern "C" int anelm_deltanet_decode_from_proj(float* y, float* state, float* co
     ANELM_REQUIRE((flags & ~7) == 0, "deltanet_decode_from_proj: unknown flags 0x%x", flags);
     const bool gated = (flags & ANELM_DN_GATED_NORM) != 0;
     ANELM_REQUIRE(!gated || norm_w != nullptr, "deltanet_decode_from_proj: GATED_NORM needs norm_w");
-    uint32_t* ctr = counters((size_t)Hk, kCtrDeltaNetConv);
-    if (!ctr) return set_error(ANELM_ERANGE, "deltanet_decode_from_proj: %d key heads exceed the counter pool", Hk);
+    hipStream_t st = as_stream(stream);
+    uint32_t* ctr = counters((size_t)Hk, kCtrDeltaNetConv, st);
+    if (!ctr) return ANELM_ERANGE;
     const long qkv = 2L * Hk * kDK + (long)Hv * kDV;
     DnParams p{};
     p.y = y;
@@ -930,7 +931,6 @@ extern "C" int anelm_deltanet_decode_from_proj(float* y, float* state, float* co
     p.conv_pos = *conv_pos;
     p.conv_k = conv_kernel;
     p.readers_done = ctr;
-    hipStream_t st = as_stream(stream);
     if (gated) {
         p.readers = Hv / Hk;
         hipLaunchKernelGGL((deltanet_decode_kernel<128, 512, true, true>), dim3(1, Hv), dim3(512), 0, st, p);

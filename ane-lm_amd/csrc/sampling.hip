@@ -58,8 +58,9 @@ __global__ __launch_bounds__(kSNT) void sample_penalty_kernel(float* adj, const 
     }
 }
 
-// Block maximum with the first index attaining it (NaN never wins: the
-// reference's strict > skips it).  With scale, the values are multiplied by
+// Block maximum with the first index attaining it (a NaN element never wins
+// here: the reference's strict > never moves to one; the one exception, a NaN
+// at index 0, is resolved by sample_argmax_kernel).  With scale, the values are multiplied by
 // inv_t and written back first.
 __global__ __launch_bounds__(kSNT) void sample_max_kernel(float* adj, float* pmax, int* pidx, int vocab,
                                                           float inv_t, int scale) {
@@ -108,8 +109,11 @@ __global__ __launch_bounds__(kSNT) void sample_max_kernel(float* adj, float* pma
 }
 
 // Greedy: the first maximum over the block results (sampling.cpp:47-53).
-__global__ __launch_bounds__(64) void sample_argmax_kernel(int32_t* token, const float* pmax, const int* pidx,
-                                                           int nb) {
+// The reference starts from max_i = 0 and moves only on adjusted[i] >
+// adjusted[max_i]: with a NaN at index 0 no comparison succeeds and it
+// returns 0, whatever follows.
+__global__ __launch_bounds__(64) void sample_argmax_kernel(int32_t* token, const float* adj, const float* pmax,
+                                                           const int* pidx, int nb) {
     float best = -INFINITY;
     int bi = 0x7fffffff;
     for (int b = threadIdx.x; b < nb; b += 64) {
@@ -126,8 +130,8 @@ __global__ __launch_bounds__(64) void sample_argmax_kernel(int32_t* token, const
             bi = oi;
         }
     }
-    // every value NaN or -inf: the reference keeps index 0
-    if (threadIdx.x == 0) *token = bi == 0x7fffffff ? 0 : bi;
+    // every value NaN or -inf, or a NaN at index 0: the reference keeps index 0
+    if (threadIdx.x == 0) *token = (bi == 0x7fffffff || __builtin_isnan(adj[0])) ? 0 : bi;
 }
 
 // Softmax numerators exp(x - max) in place and their block sums.
@@ -227,7 +231,7 @@ extern "C" int anelm_sample_token(int32_t* token, const float* logits, int vocab
                        greedy ? 1.0f : 1.0f / temperature, greedy ? 0 : 1);
     ANELM_LAUNCHED("sample_max_kernel");
     if (greedy) {
-        hipLaunchKernelGGL(sample_argmax_kernel, dim3(1), dim3(64), 0, st, token, pmax, pidx, nb);
+        hipLaunchKernelGGL(sample_argmax_kernel, dim3(1), dim3(64), 0, st, token, adj, pmax, pidx, nb);
         ANELM_LAUNCHED("sample_argmax_kernel");
         return ANELM_OK;
     }

@@ -146,7 +146,9 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
         // The captured launches allocate nothing: the attention layers' split
         // partials go to a buffer of the step, sized for full rings; the FFN
         // blocks use h_scratch.  No step runs before the capture.
-        int rc = device() ? ANELM_OK : ANELM_EHIP;
+        // the capture stream's counters and workspace exist before the
+        // capture (their creation launches a fill kernel and allocates)
+        int rc = stream_state(st) ? ANELM_OK : ANELM_EHIP;
         for (int i = 0; i < n_layers && rc == ANELM_OK; i++)
             if (layers[i].kind == ANELM_LAYER_ATTENTION) {
                 const size_t need = full_attn_part_bytes(dims->n_heads, dims->n_kv_heads, dims->head_dim,

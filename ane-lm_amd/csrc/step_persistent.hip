@@ -1469,6 +1469,9 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     wg_sync();
     if (ctl[3]) {
         // last workgroup out: every other one has finished all sync accesses
+        // (a timed-out wait stored the abort flag before its workgroup's
+        // drain and arrival here)
+        const bool aborted = ld_sc(a.sync + kAbortOff) != 0u;
         const int np = 3 * a.n_layers + a.n_layers / 4;
         for (int i = tid; i < np * (2 * kNG + 1); i += kNT) {
             const int p = i / (2 * kNG + 1), k = i - p * (2 * kNG + 1);
@@ -1480,11 +1483,12 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
             st_sc(a.sync + kFinOff, 0u);
             st_sc(a.sync + kAbortOff, 0u);
         }
-        if (advance) {
+        if (advance && !aborted) {
             // the next step's descriptors: every attention ring and position
             // moves one token forward (the KVCache bookkeeping of
             // qwen3_5.cpp:973-983), so consecutive launches need no host
-            // update; the host mirrors the same arithmetic
+            // update; the host mirrors the same arithmetic.  An aborted step
+            // does not advance: the next launch redoes its token.
             PLayer* lw = const_cast<PLayer*>(a.layers);
             for (int i = tid; i < a.n_layers; i += kNT) {
                 if (lw[i].kind != ANELM_LAYER_ATTENTION) continue;
@@ -1529,6 +1533,7 @@ struct PersistentStep {
     int rope_rows = 0;
     void (*kernel)(const pk::PArgs*, int) = nullptr;
     int grid = 0;
+    bool launched = false;             // the device descriptors are the launches' own
 };
 
 namespace {
@@ -1587,7 +1592,9 @@ int max_position(const PersistentStep* s, bool advance) {
 // RoPE table for positions [0, rows), the reference formula per row
 // (cpu_ops.cpp:51-55, the same host computation as every other RoPE path).
 int build_rope_table(PersistentStep* s, int rows) {
-    std::vector<float> host((size_t)rows * s->rot);
+    // at least two floats: the kernel reads a row's first cos/sin pair
+    // unconditionally (a row has rot floats)
+    std::vector<float> host(std::max((size_t)rows * s->rot, (size_t)2), 0.f);
     for (int p = 0; p < rows; p++)
         rope_row(&host[(size_t)p * s->rot], &host[(size_t)p * s->rot + s->rot / 2], s->rot, p, s->theta);
     float* d = nullptr;
@@ -1605,12 +1612,34 @@ int build_rope_table(PersistentStep* s, int rows) {
     return ANELM_OK;
 }
 
+// Host mirror from the device descriptors, which the launches advance
+// themselves (an aborted launch does not): the ring state before each
+// attention layer's next append and its position.  A post-append ring of
+// full length is reached from (start, cap - 1) without an overwrite as from
+// (start - 1, cap) with one; both plan the same descriptors.  The stream
+// must be idle.
+int resync(PersistentStep* s) {
+    if (!s->launched) return ANELM_OK;
+    std::vector<pk::PLayer> dl(s->host_layers.size());
+    ANELM_HIP(hipMemcpy(dl.data(), s->d_layers, dl.size() * sizeof(pk::PLayer), hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < dl.size(); i++) {
+        if (dl[i].kind != ANELM_LAYER_ATTENTION) continue;
+        s->start[i] = dl[i].ring_start;
+        s->len[i] = dl[i].ring_len - 1;
+        s->pos[i] = dl[i].pos;
+    }
+    plan_positions(s);
+    return ANELM_OK;
+}
+
 // Descriptors and arguments to the device (synchronous copies: at creation,
-// and when the RoPE table has to grow).
+// and when the RoPE table has to grow; the stream is idle then).
 int upload(PersistentStep* s, bool advance) {
+    int rc = resync(s);
+    if (rc) return rc;
     const int need = max_position(s, advance) + 1;
     if (need > s->rope_rows) {
-        const int rc = build_rope_table(s, (need + 4095) / 4096 * 4096);   // 4096-position blocks
+        rc = build_rope_table(s, (need + 4095) / 4096 * 4096);   // 4096-position blocks
         if (rc) return rc;
     }
     plan_positions(s);
@@ -1637,12 +1666,35 @@ void persistent_destroy(PersistentStep* s) {
 int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const anelm_hybrid_layer* layers,
                       int n_layers, float* x, float* h, hipStream_t st) {
     *out = nullptr;
+    // argument checks that need no device come first
+    ANELM_REQUIRE(n_layers >= 1 && n_layers <= pk::kMaxLayers, "persistent step: %d layers (max %d)",
+                  n_layers, pk::kMaxLayers);
+    bool any_attn = false;
+    for (int i = 0; i < n_layers; i++) {
+        const anelm_hybrid_layer& L = layers[i];
+        // every pointer the kernel reads or writes unconditionally
+        const bool ffn = L.ffn_norm_w && L.gate_w && L.gate_lut && L.up_w && L.up_lut && L.down_w && L.down_lut;
+        bool core;
+        if (L.kind == ANELM_LAYER_ATTENTION) {
+            any_attn = true;
+            core = L.q_gate && L.k && L.v && L.k_cache && L.v_cache && L.q_norm_w && L.k_norm_w && L.core_out;
+        } else {
+            core = L.state && L.dn_q && L.dn_k && L.dn_v && L.dn_a && L.dn_b && L.dn_A && L.dn_dt_bias &&
+                   L.core_out && (!(L.dn_flags & ANELM_DN_GATED_NORM) || (L.dn_z && L.dn_norm_w));
+        }
+        if (!ffn || !core)
+            return set_error(ANELM_ENULL, "persistent step: layer %d lacks a %s pointer (q/k norm weights are "
+                             "required here)", i, ffn ? "core" : "FFN");
+    }
+    // a rotary width of 0 would leave the kernel's RoPE row reads without a
+    // table row to read
+    ANELM_REQUIRE(!any_attn || (d->rot_dim >= 2 && d->rot_dim % 2 == 0 && d->rot_dim <= pk::kAttnD &&
+                                d->rot_dim / 2 <= 64),
+                  "persistent step: rot_dim %d (even, 2..128)", d->rot_dim);
     Device* dev = device();
     if (!dev) return ANELM_EHIP;
     const int nwg = dev->num_cus;
     int gC, gP, gRP, dC, dP, dRP;
-    ANELM_REQUIRE(n_layers >= 1 && n_layers <= pk::kMaxLayers, "persistent step: %d layers (max %d)",
-                  n_layers, pk::kMaxLayers);
     ANELM_REQUIRE(geo(d->hidden, gC, gP, gRP) && geo(d->inter, dC, dP, dRP),
                   "persistent step: hidden %d / inter %d must be multiples of 512", d->hidden, d->inter);
     ANELM_REQUIRE(2 * gP <= pk::kCW && dP <= pk::kCW && dC <= 768,
@@ -1688,8 +1740,6 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
         kps = (cap + splits - 1) / splits;
         nkj = (kps + 19) / 20;
         ANELM_REQUIRE(nkj <= 7, "persistent step: cache capacity %d beyond %d keys", cap, splits * 140);
-        ANELM_REQUIRE(d->rot_dim % 2 == 0 && d->rot_dim <= pk::kAttnD && d->rot_dim / 2 <= 64,
-                      "persistent step: rot_dim %d", d->rot_dim);
         ANELM_REQUIRE(d->rope_mode == ANELM_ROPE_INTERLEAVED || d->rope_mode == ANELM_ROPE_HALF_SPLIT,
                       "persistent step: rope_mode %d", d->rope_mode);
     }
@@ -1841,8 +1891,10 @@ int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
     hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st, (const pk::PArgs*)s->d_args,
                        advance ? 1 : 0);
     ANELM_LAUNCHED("step_kernel");
+    s->launched = true;
     if (advance) {
-        // host mirror of the launch's own advance (no copy, no wait)
+        // host mirror of the launch's own advance (no copy, no wait); after
+        // an abort it runs ahead of the device until the next resync
         for (size_t i = 0; i < s->host_layers.size(); i++) {
             if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) continue;
             s->start[i] = s->host_layers[i].ring_start;
@@ -1874,6 +1926,9 @@ int persistent_status(PersistentStep* s, int* status) {
     if (v) {
         const unsigned z = 0;
         ANELM_HIP(hipMemcpy(s->args.sync + pk::kStatusOff, &z, sizeof(z), hipMemcpyHostToDevice));
+        // the aborted launch left the descriptors where they were
+        ANELM_HIP(hipDeviceSynchronize());
+        return resync(s);
     }
     return ANELM_OK;
 }

@@ -6,10 +6,14 @@
  * "host"; `stream` is a hipStream_t passed as void* (NULL = null stream).
  * Calls are asynchronous on `stream` and return an int status:
  *   0 = ANELM_OK, < 0 = error (see anelm_last_error(), thread-local text).
- * Nothing throws across the ABI.  The library keeps one device workspace and
- * one zeroed counter array per device; calls that use them must be issued
- * from one host thread / one stream at a time per device (the reference's
- * callers are serial: main.cpp:276-371, scripts/serve_hybrid.py:699).
+ * Nothing throws across the ABI.  Device scratch (workspaces and the zeroed
+ * counters of in-kernel reductions) is owned per (device, stream): calls on
+ * different streams share no mutable state and may run concurrently, from
+ * one host thread or several, as the reference's cpu_ops functions keep no
+ * mutable globals (core/cpu_ops.cpp:1-206).  Calls on one stream are ordered
+ * by that stream; one host thread at a time may issue on a given stream.
+ * anelm_stream_release frees a stream's scratch before the stream is
+ * destroyed.
  *
  * Each declaration names the reference interface it replaces.
  */
@@ -56,6 +60,12 @@ const char* anelm_last_error(void);
 int anelm_version(void);
 /* Number of compute units of the current device (0 on error). */
 int anelm_device_cus(void);
+/* Frees the library's scratch for `stream` on the current device (created
+ * by the first call on that stream), after waiting for the stream.  Call it
+ * before destroying a stream that library calls were issued on.  No
+ * counterpart in the reference (its functions use alloca / malloc per call,
+ * core/cpu_ops.cpp:35, 165, 203). */
+int anelm_stream_release(void* stream);
 
 /* ---------------------------------------------------------------- norms */
 
@@ -365,7 +375,9 @@ int anelm_lut6_topk(int32_t* out_idx, float* out_val, const uint8_t* w, const ui
  * uniform draw in [0, 1) the reference takes from drand48() (:57): the caller
  * owns the random stream.  *token (device int32) receives the result; logits
  * are not modified (the adjusted copy lives in the library workspace).
- * At most 4096 tokens in the penalty window.  NaN logits never win. */
+ * At most 4096 tokens in the penalty window.  Greedy: a NaN logit never
+ * becomes the maximum, but a NaN at index 0 returns 0, as the reference's
+ * scan from max_i = 0 with a strict > does (sampling.cpp:47-53). */
 int anelm_sample_token(int32_t* token, const float* logits, int vocab, const int32_t* recent,
                        int n_recent, float temperature, float repetition_penalty,
                        int repetition_context_size, float frequency_penalty, float r, void* stream);
@@ -560,8 +572,15 @@ int anelm_batch_step_create(anelm_batch_step** out, const anelm_hybrid_dims* dim
                             const anelm_batch_layer* layers, int n_layers,
                             const anelm_batch_seqs* seqs, float* x);
 /* One step for every sequence; with `advance`, seq_lens (and positions) are
- * incremented on the device afterwards, as the KV caches grew by one key. */
+ * incremented on the device afterwards, as the KV caches grew by one key.  A
+ * sequence whose cache already held max_seq_len keys appended nothing: it is
+ * not advanced, and the step's status records it. */
 int anelm_batch_step_run(anelm_batch_step* step, int advance, void* stream);
+/* Synchronous: *status = 1 if, since the last call, an advancing run found a
+ * sequence at max_seq_len keys (its new key was not cached), else 0; clears
+ * the flag.  No counterpart in the reference (its ring caches slide,
+ * qwen3_5.cpp:973-983; a paged cache of fixed size cannot). */
+int anelm_batch_step_status(anelm_batch_step* step, int* status);
 int anelm_batch_step_destroy(anelm_batch_step* step);
 
 #ifdef __cplusplus

@@ -95,3 +95,54 @@ def test_argument_validation_without_device(anelm):
               None) == -1   # max_seq_len > max_pages * page_size
     assert st("anelm_apply_rope", P, P, 1, 1, 64, 64, 64, 66, 0, 1e7, None, None, 0, None) == -1
     assert st("anelm_cpu_rmsnorm", None, P, P, 4, 1e-6) == -2
+
+
+def _persistent_layers(anelm, n=4):
+    """Four layers (3 DeltaNet, 1 attention) whose every pointer is a
+    non-NULL dummy (never dereferenced: creation fails before any device work)."""
+    P = 16
+    layers = (anelm.HybridLayer * n)()
+    for i in range(n):
+        L = layers[i]
+        L.kind = anelm.LAYER_ATTENTION if (i + 1) % 4 == 0 else anelm.LAYER_DELTANET
+        for name, typ in anelm.HybridLayer._fields_:
+            if typ is ctypes.c_void_p and name not in ("in_norm_w", "first_w", "first_lut", "o_w", "o_lut",
+                                                        "proj", "conv_state", "conv_w"):
+                setattr(L, name, P)
+        L.cache_capacity, L.cache_len, L.pos = 8192, 8191, 8191
+        L.dn_flags = 5
+    return layers
+
+
+def test_persistent_step_rejects_before_device_work(anelm):
+    """The persistent step refuses, at creation and before touching a device,
+    a rotary width of 0 (the kernel reads a RoPE row unconditionally) and a
+    layer without a pointer its kernel reads (e.g. no q/k norm weights)."""
+    st = anelm.status
+    dims = anelm.HybridDims(2560, 9216, 16, 4, 256, 64, 0, 1e7, 1e-6, 16, 32, 128, 4)
+    h = ctypes.c_void_p()
+    P = ctypes.c_void_p(16)
+    for rot in (0, 3, 260):
+        dims.rot_dim = rot
+        layers = _persistent_layers(anelm)
+        assert st("anelm_hybrid_step_create", ctypes.byref(h), ctypes.byref(dims), layers, 4, P, P,
+                  anelm.STEP_PERSISTENT, None) == -1, rot
+        assert "rot_dim" in anelm.last_error()
+        assert not h.value
+    dims.rot_dim = 64
+    for name, layer in (("q_norm_w", 3), ("k_norm_w", 3), ("state", 0), ("down_lut", 1), ("dn_z", 2)):
+        layers = _persistent_layers(anelm)
+        setattr(layers[layer], name, None)
+        assert st("anelm_hybrid_step_create", ctypes.byref(h), ctypes.byref(dims), layers, 4, P, P,
+                  anelm.STEP_PERSISTENT, None) == -2, name
+        assert f"layer {layer}" in anelm.last_error()
+    # without the gated norm a DeltaNet layer needs no z / norm weight: the
+    # pointer checks pass and only the device lookup can fail here
+    layers = _persistent_layers(anelm)
+    layers[2].dn_flags = 1
+    layers[2].dn_z = None
+    rc = st("anelm_hybrid_step_create", ctypes.byref(h), ctypes.byref(dims), layers, 4, P, P,
+            anelm.STEP_PERSISTENT, None)
+    assert rc not in (-1, -2), anelm.last_error()
+    if rc == 0:   # a device was present: the step was built (nothing launched)
+        anelm.call("anelm_hybrid_step_destroy", h)

@@ -120,3 +120,40 @@ def test_batch_step_32_sequences_matches_oracle(anelm, orc, dev):
         assert exact_rows >= 60, f"only {exact_rows} of 64 rows were separated enough to compare indices"
     finally:
         anelm.call("anelm_batch_step_destroy", h)
+
+
+def test_batch_step_stops_at_max_seq_len(anelm, dev):
+    """A sequence whose paged cache is full (max_seq_len keys) appends nothing
+    (anelm_attn_decode_paged_step): an advancing step leaves its length and
+    position where they are and raises the step status; the others advance."""
+    m = batch_model(1310, 4, 4, lo=256, hi=300)
+    db = DeviceBatch(anelm, m, dev)
+    top = int(m.lens.max())
+    db.seqs.max_seq_len = top + 1            # the longest sequence fills its cache at step 1
+    pos = torch.tensor(m.lens + 1000, dtype=torch.int32, device=dev)
+    db.seqs.positions = pos.data_ptr()
+    h = _P()
+    rc = anelm.status("anelm_batch_step_create", ctypes.byref(h), ctypes.byref(db.dims), db.layers,
+                      len(m.layers), ctypes.byref(db.seqs), _P(db.x.data_ptr()))
+    assert rc == 0, anelm.last_error()
+    st = ctypes.c_int(-1)
+    s = _P(torch.cuda.current_stream().cuda_stream)
+    try:
+        print("batch step at max_seq_len: step 1", flush=True)
+        anelm.call("anelm_batch_step_run", h, 1, s)
+        anelm.call("anelm_batch_step_status", h, ctypes.byref(st))
+        assert st.value == 0
+        assert np.array_equal(to_host(db.lens), m.lens + 1)
+        print("batch step at max_seq_len: step 2", flush=True)
+        anelm.call("anelm_batch_step_run", h, 1, s)
+        anelm.call("anelm_batch_step_status", h, ctypes.byref(st))
+        assert st.value == 1
+        full = m.lens == top
+        assert full.any() and not full.all()
+        want = np.where(full, m.lens + 1, m.lens + 2)
+        assert np.array_equal(to_host(db.lens), want)
+        assert np.array_equal(to_host(pos), want + 1000)
+        anelm.call("anelm_batch_step_status", h, ctypes.byref(st))
+        assert st.value == 0   # cleared by the read
+    finally:
+        anelm.call("anelm_batch_step_destroy", h)

@@ -37,6 +37,25 @@ def test_sample_greedy_with_penalties(anelm, orc, dev):
     assert int(to_host(anelm.ops.sample_token(to_dev(flat, dev), None, 0.0))[0]) == 77
 
 
+def test_sample_greedy_nan_layouts(anelm, orc, dev):
+    """sampling.cpp:47-53 starts at max_i = 0 and moves on a strict >: a NaN
+    at index 0 is never replaced (token 0), a NaN elsewhere never wins."""
+    rng = np.random.default_rng(901)
+    base = rng.standard_normal(VOCAB).astype(np.float32)
+    top = int(np.argmax(base))
+    cases = []
+    a = base.copy(); a[0] = np.nan; cases.append(("nan at 0", a))
+    a = base.copy(); a[top - 1] = np.nan; a[VOCAB - 1] = np.nan; cases.append(("nan elsewhere", a))
+    a = np.full(VOCAB, -np.inf, np.float32); cases.append(("all -inf", a))
+    a = np.full(VOCAB, np.nan, np.float32); cases.append(("all nan", a))
+    a = base.copy(); a[0] = -np.inf; a[1:1000] = np.nan; cases.append(("-inf at 0, nan run", a))
+    for name, lg in cases:
+        want, _ = orc.sample_token(lg, np.zeros(0, np.int32), 0.0, 1.0, 0, 0.0, 0.5)
+        got = int(to_host(anelm.ops.sample_token(to_dev(lg, dev), None, 0.0))[0])
+        assert got == want, (name, got, want)
+    assert orc.sample_token(cases[0][1], np.zeros(0, np.int32), 0.0, 1.0, 0, 0.0, 0.5)[0] == 0
+
+
 def _exact_cdf(orc, logits, recent, T):
     """Float64 running sum of the exact softmax of the penalised logits times
     1/T (the fp32 values both implementations exponentiate)."""

@@ -473,6 +473,11 @@ def test_topk_and_argmax(orc):
     assert list(idx[:5]) == [17, 4000, 9999, 3, 5]
     assert orc.argmax(logits) == 17
     assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
+    # sampling.cpp:47-53 from max_i = 0 with a strict >: a NaN at index 0 is
+    # never replaced, -inf everywhere keeps 0, a NaN later never wins
+    assert orc.argmax(np.array([np.nan, 5, 7, 2], np.float32)) == 0
+    assert orc.argmax(np.full(6, -np.inf, np.float32)) == 0
+    assert orc.argmax(np.array([1, np.nan, 7, np.nan], np.float32)) == 2
 
 
 def test_topk_nan_ranks_as_minus_inf(orc):
