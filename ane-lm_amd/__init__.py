@@ -62,6 +62,10 @@ SIGNATURES = {
                                      _I, _I, _I, _I, _I, _F, _F, _I, _I, _P],
     "anelm_rope_table": [_P, _I, _I, _F],
     "anelm_attn_prefill": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P],
+    "anelm_full_attn_prefill": [_P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _I, _I,
+                                _P, _I, _IP, _IP, _I, _P],
+    "anelm_deltanet_prefill_from_proj": [_P, _P, _P, _IP, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                         _P],
     "anelm_ssm_step": [_P, _P, _P, _P, _P, _F, _F, _I, _I, _I, _P],
     "anelm_deltanet_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "anelm_deltanet_decode_batched": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],

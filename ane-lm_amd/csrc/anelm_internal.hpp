@@ -120,6 +120,14 @@ int full_attn_decode_kv_impl(float* out, const float* q_gate, const float* k, co
                              int rope_mode, int gate, const float* cos_row, const float* sin_row, int* cache_start,
                              int* cache_len, int cache_capacity, hipStream_t stream, float* part, size_t part_cap);
 
+// Causal prefill attention core (attn_prefill.hip): S query rows q
+// [S][Hq][D] over L keys k / v [L][Hkv][D] (fp16), row r being key qoff + r
+// and attending keys (qoff + r - win, qoff + r] (win 0: from key 0); out
+// [S][Hq][D] fp32 or fp16; with gate, each output element is multiplied by
+// sigmoid(gate[r * gtok + h * ghead + d]).  Uses the stream's workspace.
+int prefill_core(void* out, bool out16, const uint16_t* q, const uint16_t* k, const uint16_t* v, int S, int L,
+                 int qoff, int win, int Hq, int Hkv, int D, const float* gate, int gtok, int ghead, hipStream_t st);
+
 // `n` counters of the pool of `stream` on the current device, in the range
 // reserved for one user (ranges never overlap, so no user sees another's
 // values); nullptr if n exceeds the range.  Every range starts zeroed.

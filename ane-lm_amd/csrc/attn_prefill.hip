@@ -27,10 +27,15 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBN = 32;  // keys per tile
 
+// Query row r is key qoff + r of the L keys in k / v (the keys before qoff
+// are a cached prefix) and attends keys (qoff + r - win, qoff + r] (win 0: no
+// lower bound).  With gate, the output row is multiplied by sigmoid of
+// gate[r * gtok + h * ghead + d] (the reference's output gate).
 template <int D, int HB, int RB, bool OUT16>
 __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const _Float16* q,
                                                                const _Float16* k, const _Float16* v,
-                                                               int S, int Hq, int Hkv) {
+                                                               int S, int L, int qoff, int win, int Hq, int Hkv,
+                                                               const float* gate, int gtok, int ghead) {
     constexpr int NW = HB * RB;
     constexpr int NT = NW * 64;
     constexpr int KS = D / 16;   // QK k-steps
@@ -64,15 +69,17 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
     float m = -INFINITY, l = 0.f;
     const float sl2 = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
 
-    const int nkt = (row_end + kBN - 1) / kBN;
-    for (int kt = 0; kt < nkt; kt++) {
+    const int nkt = (qoff + row_end + kBN - 1) / kBN;
+    // first tile any row of the workgroup sees
+    const int kt0 = win > 0 ? max(0, qoff + qt * RB * 32 + 1 - win) / kBN : 0;
+    for (int kt = kt0; kt < nkt; kt++) {
         const int j0 = kt * kBN;
         __syncthreads();
         for (int c = tid; c < kBN * D / 8; c += NT) {
             const int kr = c / (D / 8), kc = (c % (D / 8)) * 8;
             const int key = j0 + kr;
             uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
-            if (key < S) {
+            if (key < L) {
                 kv4 = *reinterpret_cast<const uint4*>(k + ((size_t)key * Hkv + kvh) * D + kc);
                 vv4 = *reinterpret_cast<const uint4*>(v + ((size_t)key * Hkv + kvh) * D + kc);
             }
@@ -82,7 +89,9 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
             for (int i = 0; i < 8; i++) Vt[kc + i][kr] = vh[i];
         }
         __syncthreads();
-        if (q0 >= S || j0 > q0 + 31) continue;  // wave-uniform: tile fully masked
+        // wave-uniform: every key of the tile after the wave's rows, or (with
+        // a window) before the window of its first row
+        if (q0 >= S || j0 > qoff + q0 + 31 || (win > 0 && j0 + kBN <= qoff + q0 + 1 - win)) continue;
 
         float16_t s = float16_t{};
 #pragma unroll
@@ -92,21 +101,25 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
         }
         // s[e] = score of key j0 + 8*(e/4) + 4*hh + e%4 for query row qrow
         float mx = -INFINITY;
+        const int kmax = qoff + qrow, kmin = win > 0 ? qoff + qrow - win : -1;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int key = j0 + 8 * (e / 4) + 4 * hh + (e % 4);
-            const float val = (key <= qrow) ? s[e] * sl2 : -INFINITY;
+            const float val = (key <= kmax && key > kmin) ? s[e] * sl2 : -INFINITY;
             s[e] = val;
             mx = fmaxf(mx, val);
         }
         mx = fmaxf(mx, shfl_xor(mx, 32));
+        // a row that has seen no key yet (below its window) keeps m = -inf:
+        // its terms are exp2(-inf) = 0 against a finite reference
         const float m_new = fmaxf(m, mx);
-        const float alpha = exp2f(m - m_new);
+        const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2f(m - m_ref);
         float ps = 0.f;
         half8 pf[2];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            const float pe = exp2f(s[e] - m_new);
+            const float pe = exp2f(s[e] - m_ref);
             ps += pe;
             pf[e / 8][e % 8] = (_Float16)pe;
         }
@@ -136,8 +149,15 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
         for (int g4 = 0; g4 < 4; g4++) {
             const int d = 32 * db + 8 * g4 + 4 * hh;
             const size_t off = ((size_t)qrow * Hq + h) * D + d;
-            const float a0 = o[db][4 * g4] * inv, a1 = o[db][4 * g4 + 1] * inv;
-            const float a2 = o[db][4 * g4 + 2] * inv, a3 = o[db][4 * g4 + 3] * inv;
+            float a0 = o[db][4 * g4] * inv, a1 = o[db][4 * g4 + 1] * inv;
+            float a2 = o[db][4 * g4 + 2] * inv, a3 = o[db][4 * g4 + 3] * inv;
+            if (gate) {
+                const float* gr = gate + (size_t)qrow * gtok + (size_t)h * ghead + d;
+                a0 = a0 / (1.0f + expf(-gr[0]));
+                a1 = a1 / (1.0f + expf(-gr[1]));
+                a2 = a2 / (1.0f + expf(-gr[2]));
+                a3 = a3 / (1.0f + expf(-gr[3]));
+            }
             if (OUT16) {
                 half4 hv = {(_Float16)a0, (_Float16)a1, (_Float16)a2, (_Float16)a3};
                 *reinterpret_cast<half4*>(static_cast<_Float16*>(out) + off) = hv;
@@ -211,26 +231,32 @@ __global__ __launch_bounds__(256) void vt_kernel(_Float16* vt, const _Float16* v
 
 __device__ __forceinline__ int key_perm(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-// Key tiles needed by 64-row block blk: keys 0 .. min(64 blk + 63, S - 1).
-__device__ __forceinline__ int block_tiles(int blk, int S) { return (min(64 * blk + 64, S) + 31) / 32; }
+// Key tiles needed by 64-row block blk: keys 0 .. qoff + min(64 blk + 63, S - 1).
+__device__ __forceinline__ int block_tiles(int blk, int S, int qoff) {
+    return (qoff + min(64 * blk + 64, S) + 31) / 32;
+}
 
+// Query row r is key qoff + r of the L keys (the keys before qoff are a
+// cached prefix) and attends keys 0 .. qoff + r.  With gate, output row
+// (r, h) is multiplied by sigmoid(gate[r * gtok + h * ghead + d]).
 template <bool OUT16>
 __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Float16* q, const _Float16* k,
                                                            const _Float16* vt, float* part, uint32_t* ctr, int S,
-                                                           int S_pad, int Hq, int Hkv) {
+                                                           int L, int L_pad, int qoff, int Hq, int Hkv,
+                                                           const float* gate, int gtok, int ghead) {
     constexpr int D = 256, KS = D / 16, DB = D / 32;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hl = w & 3, rh = w >> 2;
     const int nb = (S + 63) / 64, npair = nb / 2, upk = npair + (nb & 1);
     // consecutive units on one XCD (workgroup id mod 8 selects the XCD): one KV head per L2
-    int L = blockIdx.x;
-    if (gridDim.x % 8 == 0) L = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
-    const int unit = L >> 1, half_id = L & 1;
+    int lw = blockIdx.x;
+    if (gridDim.x % 8 == 0) lw = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+    const int unit = lw >> 1, half_id = lw & 1;
     const int kvh = unit / upk, pu = unit % upk;
     const int h = kvh * 4 + hl;
     const int blk_a = pu < npair ? pu : -1, blk_b = pu < npair ? nb - 1 - pu : npair;
-    const int nta = blk_a >= 0 ? block_tiles(blk_a, S) : 0, ntb = block_tiles(blk_b, S);
+    const int nta = blk_a >= 0 ? block_tiles(blk_a, S, qoff) : 0, ntb = block_tiles(blk_b, S, qoff);
     const int half = (nta + ntb) / 2, nb0 = half - nta;   // tiles of b taken by the first workgroup
     const bool split = nb0 > 0;
     // this workgroup's segments (block, first key tile, tile count)
@@ -250,9 +276,9 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
     const int nseg = n1 > 0 ? 2 : 1;
     const int ntot = n0 + n1;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(k), 0, (int)min((size_t)S * Hkv * D * 2, (size_t)0x7fffffff), 0x00020000);
+        const_cast<_Float16*>(k), 0, (int)min((size_t)L * Hkv * D * 2, (size_t)0x7fffffff), 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(vt), 0, (int)min((size_t)Hkv * D * S_pad * 2, (size_t)0x7fffffff), 0x00020000);
+        const_cast<_Float16*>(vt), 0, (int)min((size_t)Hkv * D * L_pad * 2, (size_t)0x7fffffff), 0x00020000);
     const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;   // 1/sqrt(256) * log2(e)
     auto key_tile = [&](int i) { return i < n0 ? t00 + i : t01 + (i - n0); };
     // stream tile i -> buffer i % 4; wave w loads K chunks 2w, 2w+1 and V^T pieces 2w, 2w+1
@@ -264,14 +290,14 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
 #pragma unroll
         for (int x = 0; x < 2; x++) {
             const int c = 2 * w + x, row = c + 16 * (ln >> 5), key = j0 + row;
-            const int off = key < S ? ((key * Hkv + kvh) * D + 8 * (ln & 31)) * 2 : 0x7fffffff;
+            const int off = key < L ? ((key * Hkv + kvh) * D + 8 * (ln & 31)) * 2 : 0x7fffffff;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(base + c * 1040), 16,
                                                      off, 0, 0, 0);
         }
 #pragma unroll
         for (int x = 0; x < 2; x++) {
             const int p = (2 * w + x) * 64 + ln, d = p >> 2, gs = p & 3, g = gs ^ ((d >> 2) & 3);
-            const int off = (((kvh * D + d) * S_pad) + j0 + 8 * g) * 2;
+            const int off = (((kvh * D + d) * L_pad) + j0 + 8 * g) * 2;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rv, (__attribute__((address_space(3))) void*)(base + kGKBytes + (2 * w + x) * 1024), 16, off, 0, 0, 0);
         }
@@ -308,7 +334,7 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
             __syncthreads();   // every wave's part of tile i landed; buffer (i+3)%4 (tile i-1) is free
             if (i + 3 < ntot) issue(i + 3);
             const int kt = key_tile(i), j0 = kt * kGKeys;
-            if (j0 > row0 + 31) continue;   // every key of this tile lies after this wave's rows
+            if (j0 > qoff + row0 + 31) continue;   // every key of this tile lies after this wave's rows
             const char* base = lds + (i % kGBuf) * kGTile;
             int ln = threadIdx.x & 63;
             asm volatile("" : "+v"(ln));
@@ -323,8 +349,8 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                                                                 0, 0, 0);
             }
             // ---- online softmax; element e holds key j0 + (e < 8 ? 8 h + e : 16 + 8 h + e - 8)
-            if (j0 + 31 > row0) {
-                const int h2 = ln >> 5, qr = row0 + (ln & 31);
+            if (j0 + 31 > qoff + row0) {
+                const int h2 = ln >> 5, qr = qoff + row0 + (ln & 31);
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int key = j0 + (e < 8 ? 8 * h2 + e : 16 + 8 * h2 + (e - 8));
@@ -422,10 +448,17 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                     if (have_other)
                         ov = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                                             rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
-                    const float v0 = (o[db][4 * g4] * a0 + ov.x * a1) * inv;
-                    const float v1 = (o[db][4 * g4 + 1] * a0 + ov.y * a1) * inv;
-                    const float v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
-                    const float v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
+                    float v0 = (o[db][4 * g4] * a0 + ov.x * a1) * inv;
+                    float v1 = (o[db][4 * g4 + 1] * a0 + ov.y * a1) * inv;
+                    float v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
+                    float v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
+                    if (gate) {
+                        const float* gr = gate + (size_t)erow * gtok + (size_t)h * ghead + dd;
+                        v0 = v0 / (1.0f + expf(-gr[0]));
+                        v1 = v1 / (1.0f + expf(-gr[1]));
+                        v2 = v2 / (1.0f + expf(-gr[2]));
+                        v3 = v3 / (1.0f + expf(-gr[3]));
+                    }
                     if (OUT16) {
                         half4 hv = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
                         *reinterpret_cast<half4*>(static_cast<_Float16*>(out) + off) = hv;
@@ -439,14 +472,14 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
     }
 }
 
-int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const void* v, int S, int Hq, int Hkv,
-                      hipStream_t st) {
+int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const void* v, int S, int L, int qoff,
+                      int Hq, int Hkv, const float* gate, int gtok, int ghead, hipStream_t st) {
     constexpr int D = 256;
-    const int S_pad = (S + kGKeys - 1) / kGKeys * kGKeys;
-    ANELM_REQUIRE((size_t)S * Hkv * D * 2 < 0x7fffffffu && (size_t)Hkv * D * S_pad * 2 < 0x7fffffffu,
-                  "prefill: %d tokens exceed the 2 GiB buffer range", S);
+    const int L_pad = (L + kGKeys - 1) / kGKeys * kGKeys;
+    ANELM_REQUIRE((size_t)L * Hkv * D * 2 < 0x7fffffffu && (size_t)Hkv * D * L_pad * 2 < 0x7fffffffu,
+                  "prefill: %d keys exceed the 2 GiB buffer range", L);
     const int nb = (S + 63) / 64, upk = nb / 2 + (nb & 1), units = Hkv * upk;
-    const size_t vt_bytes = ((size_t)Hkv * D * S_pad * 2 + 255) & ~(size_t)255;
+    const size_t vt_bytes = ((size_t)Hkv * D * L_pad * 2 + 255) & ~(size_t)255;
     const size_t part_bytes = (size_t)2 * units * kGSlotFloats * sizeof(float);
     char* ws = static_cast<char*>(workspace(vt_bytes + part_bytes, st));
     if (!ws) return ANELM_ENOMEM;
@@ -454,8 +487,8 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     if (!ctr) return ANELM_ERANGE;
     _Float16* vt = reinterpret_cast<_Float16*>(ws);
     float* part = reinterpret_cast<float*>(ws + vt_bytes);
-    hipLaunchKernelGGL(vt_kernel, dim3(S_pad / kGKeys, Hkv), dim3(256), 0, st, vt, static_cast<const _Float16*>(v), S,
-                       S_pad, Hkv);
+    hipLaunchKernelGGL(vt_kernel, dim3(L_pad / kGKeys, Hkv), dim3(256), 0, st, vt, static_cast<const _Float16*>(v), L,
+                       L_pad, Hkv);
     ANELM_LAUNCHED("vt_kernel");
     static bool attr_set = false;
     if (!attr_set) {
@@ -469,44 +502,60 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     const _Float16* kh = static_cast<const _Float16*>(k);
     const dim3 grid(2 * units);
     if (out16)
-        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, S_pad,
-                           Hq, Hkv);
+        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, L,
+                           L_pad, qoff, Hq, Hkv, gate, gtok, ghead);
     else
-        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, S_pad,
-                           Hq, Hkv);
+        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, L,
+                           L_pad, qoff, Hq, Hkv, gate, gtok, ghead);
     ANELM_LAUNCHED("prefill_g4_kernel");
     return ANELM_OK;
 }
 
 template <int D, int HB, int RB>
-int launch_prefill(void* out, bool out16, const void* q, const void* k, const void* v, int S, int Hq,
-                   int Hkv, hipStream_t st) {
+int launch_prefill(void* out, bool out16, const void* q, const void* k, const void* v, int S, int L, int qoff,
+                   int win, int Hq, int Hkv, const float* gate, int gtok, int ghead, hipStream_t st) {
     const int rows = 32 * RB;
     dim3 grid((S + rows - 1) / rows, Hq / HB), block(HB * RB * 64);
     const _Float16* qh = static_cast<const _Float16*>(q);
     const _Float16* kh = static_cast<const _Float16*>(k);
     const _Float16* vh = static_cast<const _Float16*>(v);
-    if (out16) hipLaunchKernelGGL((prefill_kernel<D, HB, RB, true>), grid, block, 0, st, out, qh, kh, vh, S, Hq, Hkv);
-    else hipLaunchKernelGGL((prefill_kernel<D, HB, RB, false>), grid, block, 0, st, out, qh, kh, vh, S, Hq, Hkv);
+    if (out16)
+        hipLaunchKernelGGL((prefill_kernel<D, HB, RB, true>), grid, block, 0, st, out, qh, kh, vh, S, L, qoff, win,
+                           Hq, Hkv, gate, gtok, ghead);
+    else
+        hipLaunchKernelGGL((prefill_kernel<D, HB, RB, false>), grid, block, 0, st, out, qh, kh, vh, S, L, qoff, win,
+                           Hq, Hkv, gate, gtok, ghead);
     ANELM_LAUNCHED("prefill_kernel");
     return ANELM_OK;
 }
 
 template <int D>
-int dispatch_g(void* out, bool out16, const void* q, const void* k, const void* v, int S, int Hq,
-               int Hkv, hipStream_t st) {
+int dispatch_g(void* out, bool out16, const void* q, const void* k, const void* v, int S, int L, int qoff, int win,
+               int Hq, int Hkv, const float* gate, int gtok, int ghead, hipStream_t st) {
     switch (Hq / Hkv) {
-        case 1: return launch_prefill<D, 1, 8>(out, out16, q, k, v, S, Hq, Hkv, st);
-        case 2: return launch_prefill<D, 2, 4>(out, out16, q, k, v, S, Hq, Hkv, st);
+        case 1: return launch_prefill<D, 1, 8>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
+        case 2: return launch_prefill<D, 2, 4>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
         case 4:
-            if (D == 256) return launch_prefill_g4(out, out16, q, k, v, S, Hq, Hkv, st);
-            return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, Hq, Hkv, st);
-        case 8: return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, Hq, Hkv, st);
+            // the pipelined kernel walks every key from 0: no window
+            if (D == 256 && win == 0)
+                return launch_prefill_g4(out, out16, q, k, v, S, L, qoff, Hq, Hkv, gate, gtok, ghead, st);
+            return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
+        case 8: return launch_prefill<D, 4, 2>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
         default: return set_error(ANELM_EINVAL, "prefill: n_heads/n_kv_heads = %d unsupported", Hq / Hkv);
     }
 }
 
 }  // namespace
+
+int prefill_core(void* out, bool out16, const uint16_t* q, const uint16_t* k, const uint16_t* v, int S, int L,
+                 int qoff, int win, int Hq, int Hkv, int D, const float* gate, int gtok, int ghead, hipStream_t st) {
+    switch (D) {
+        case 128: return dispatch_g<128>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
+        case 256: return dispatch_g<256>(out, out16, q, k, v, S, L, qoff, win, Hq, Hkv, gate, gtok, ghead, st);
+        default: return set_error(ANELM_EINVAL, "prefill: head_dim %d unsupported (128, 256)", D);
+    }
+}
+
 }  // namespace anelm
 
 using namespace anelm;
@@ -522,11 +571,6 @@ extern "C" int anelm_attn_prefill(void* out, int out_dtype, const uint16_t* q, c
     ANELM_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "prefill: heads %d/%d", n_heads,
                   n_kv_heads);
     ANELM_REQUIRE(out_dtype == ANELM_F32 || out_dtype == ANELM_F16, "prefill: out_dtype %d", out_dtype);
-    const bool out16 = out_dtype == ANELM_F16;
-    hipStream_t st = as_stream(stream);
-    switch (head_dim) {
-        case 128: return dispatch_g<128>(out, out16, q, k, v, S, n_heads, n_kv_heads, st);
-        case 256: return dispatch_g<256>(out, out16, q, k, v, S, n_heads, n_kv_heads, st);
-        default: return set_error(ANELM_EINVAL, "prefill: head_dim %d unsupported (128, 256)", head_dim);
-    }
+    return prefill_core(out, out_dtype == ANELM_F16, q, k, v, S, S, 0, 0, n_heads, n_kv_heads, head_dim, nullptr, 0,
+                        0, as_stream(stream));
 }

@@ -3,7 +3,12 @@
 // whose whole forward runs on the GPU.
 //
 //   prefill: one forward per prompt token (the single-token path,
-//            generate.cpp:76-84), the LM head only after the last;
+//            generate.cpp:76-84), the LM head only after the last; or
+//            (PREFILL_MODE 1) the whole prompt through each layer at once,
+//            as Qwen35Model::forward_batch (models/llm/qwen3_5.cpp:1164-1217)
+//            batches the projections -- here the cores take the prompt in
+//            one call too (anelm_full_attn_prefill,
+//            anelm_deltanet_prefill_from_proj);
 //   decode:  sample_token over the logits with the generated tokens as the
 //            penalty window (generate.cpp:96-104, core/sampling.cpp:11-66),
 //            then forward(next token) until max_tokens.
@@ -14,7 +19,7 @@
 // o_proj, FFN), the final norm and the LUT6 LM head.
 //
 // Usage: stream_generate MODEL PROMPT MAX_TOKENS TEMPERATURE REP_PENALTY
-//                        REP_CONTEXT FREQ_PENALTY SEED
+//                        REP_CONTEXT FREQ_PENALTY SEED [PREFILL_MODE]
 //   MODEL   weights as written by tests/test_gpu_host_loop.py: a sequence
 //           of records (int64 byte count, bytes) in a fixed order;
 //   PROMPT  comma-separated token ids.
@@ -23,6 +28,7 @@
 // drand48(), core/sampling.cpp:57).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
@@ -89,7 +95,7 @@ void* zeros(size_t bytes) {
 
 struct Model {
     int hidden, inter, n_layers, n_heads, n_kv_heads, head_dim, rot_dim, lin_k, lin_v, lin_dim, conv_k,
-        vocab, cap;
+        vocab, cap, max_first;
     float theta, eps;
     std::vector<anelm_hybrid_layer> layers;
     float* embed;
@@ -125,6 +131,7 @@ Model load(const char* path) {
         L.in_norm_w = static_cast<float*>(upload(r.next()));
         std::vector<char> fw = r.next();
         const int first_out = (int)(fw.size() * 4 / 3 / m.hidden);
+        if (first_out > m.max_first) m.max_first = first_out;
         L.first_w = static_cast<uint8_t*>(upload(fw));
         L.first_lut = static_cast<uint16_t*>(upload(r.next()));
         L.o_w = static_cast<uint8_t*>(upload(r.next()));
@@ -176,11 +183,14 @@ struct Lcg {
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc != 9) {
-        fprintf(stderr, "usage: %s MODEL PROMPT MAX_TOKENS TEMPERATURE REP_PENALTY REP_CONTEXT FREQ_PENALTY SEED\n",
+    if (argc != 9 && argc != 10) {
+        fprintf(stderr,
+                "usage: %s MODEL PROMPT MAX_TOKENS TEMPERATURE REP_PENALTY REP_CONTEXT FREQ_PENALTY SEED "
+                "[PREFILL_MODE]\n",
                 argv[0]);
         return 2;
     }
+    const int prefill_mode = argc == 10 ? atoi(argv[9]) : 0;
     Model m = load(argv[1]);
     std::vector<int> prompt;
     for (const char* p = argv[2]; *p;) {
@@ -207,7 +217,6 @@ int main(int argc, char** argv) {
     anelm_hybrid_dims dims{m.hidden, m.inter, m.n_heads, m.n_kv_heads, m.head_dim, m.rot_dim,
                            ANELM_ROPE_INTERLEAVED, m.theta, m.eps, m.lin_k, m.lin_v, m.lin_dim, m.conv_k};
     anelm_hybrid_step* step = nullptr;
-    CHECK(anelm_hybrid_step_create(&step, &dims, m.layers.data(), m.n_layers, x, h, ANELM_STEP_EAGER, st));
 
     // Qwen35Model::forward(token, pos, compute_logits)
     auto forward = [&](int token, bool compute_logits) {
@@ -219,7 +228,64 @@ int main(int argc, char** argv) {
         CHECK(anelm_lut6_gemv(logits, m.lm_w, m.lm_lut, xf, m.vocab, m.hidden, st));
     };
 
-    for (size_t i = 0; i < prompt.size(); i++) forward(prompt[i], i + 1 == prompt.size());
+    // Qwen35Model::forward_batch(tokens, S, 0) over the whole prompt, then the
+    // LM head on its last row.  Per layer: input norm and the first projection
+    // for all tokens, the core over the prompt, o_proj + residual, the FFN
+    // block; the rings and conv state end as after S single-token forwards.
+    auto prefill_batch = [&](const std::vector<int>& toks) {
+        const int S = (int)toks.size(), H = m.hidden, I = m.inter;
+        const int core_max = std::max(m.n_heads * m.head_dim, m.lin_v * m.lin_dim);
+        float* X = static_cast<float*>(zeros((size_t)S * H * 4));
+        float* XN = static_cast<float*>(zeros((size_t)S * H * 4));
+        float* P = static_cast<float*>(zeros((size_t)S * m.max_first * 4));
+        float* C = static_cast<float*>(zeros((size_t)S * core_max * 4));
+        float* G = static_cast<float*>(zeros((size_t)S * I * 4));
+        float* U = static_cast<float*>(zeros((size_t)S * I * 4));
+        float* rope = static_cast<float*>(zeros((size_t)m.cap * m.rot_dim * 4));
+        CHECK(anelm_rope_table(rope, m.rot_dim, m.cap, m.theta));   // qwen3_5.cpp:308-324
+        for (int t = 0; t < S; t++)
+            HIPCHECK(hipMemcpyAsync(X + (size_t)t * H, m.embed + (size_t)toks[t] * H, (size_t)H * 4,
+                                    hipMemcpyDeviceToDevice, st));
+        for (anelm_hybrid_layer& L : m.layers) {
+            const bool attn = L.kind == ANELM_LAYER_ATTENTION;
+            const int core_dim = attn ? m.n_heads * m.head_dim : m.lin_v * m.lin_dim;
+            const int first_out = attn ? m.n_heads * 2 * m.head_dim + 2 * m.n_kv_heads * m.head_dim
+                                       : 2 * m.lin_k * m.lin_dim + 2 * m.lin_v * m.lin_dim + 2 * m.lin_v;
+            CHECK(anelm_rmsnorm(XN, X, L.in_norm_w, H, S, H, H, m.eps, st));
+            CHECK(anelm_lut6_gemm(P, L.first_w, L.first_lut, XN, S, first_out, H, 0, st));
+            if (attn) {
+                const float* kp = P + (size_t)m.n_heads * 2 * m.head_dim;
+                CHECK(anelm_full_attn_prefill(C, P, kp, kp + (size_t)m.n_kv_heads * m.head_dim, first_out,
+                                              L.k_cache, L.v_cache, L.q_norm_w, L.k_norm_w, S, m.n_heads,
+                                              m.n_kv_heads, m.head_dim, m.rot_dim, L.pos, m.theta, m.eps,
+                                              ANELM_ROPE_INTERLEAVED, 1, rope, m.cap, &L.cache_start, &L.cache_len,
+                                              L.cache_capacity, st));
+                L.pos += S;
+            } else {
+                CHECK(anelm_deltanet_prefill_from_proj(C, L.state, L.conv_state, &L.conv_pos, P, L.conv_w, L.dn_A,
+                                                       L.dn_dt_bias, L.dn_norm_w, S, m.lin_k, m.lin_v, m.lin_dim,
+                                                       m.lin_dim, m.conv_k, L.dn_flags, st));
+            }
+            CHECK(anelm_lut6_gemm(X, L.o_w, L.o_lut, C, S, H, core_dim, 1, st));
+            CHECK(anelm_rmsnorm(XN, X, L.ffn_norm_w, H, S, H, H, m.eps, st));
+            CHECK(anelm_lut6_gemm(G, L.gate_w, L.gate_lut, XN, S, I, H, 0, st));
+            CHECK(anelm_lut6_gemm(U, L.up_w, L.up_lut, XN, S, I, H, 0, st));
+            CHECK(anelm_swiglu(G, G, U, (int64_t)S * I, st));
+            CHECK(anelm_lut6_gemm(X, L.down_w, L.down_lut, G, S, H, I, 1, st));
+        }
+        CHECK(anelm_rmsnorm(xf, X + (size_t)(S - 1) * H, m.final_norm, H, 1, H, H, m.eps, st));
+        CHECK(anelm_lut6_gemv(logits, m.lm_w, m.lm_lut, xf, m.vocab, H, st));
+    };
+
+    if (prefill_mode == 1) {
+        prefill_batch(prompt);
+        // the decode step starts from the rings, positions and conv state the
+        // prefill left (the step copies the descriptors)
+        CHECK(anelm_hybrid_step_create(&step, &dims, m.layers.data(), m.n_layers, x, h, ANELM_STEP_EAGER, st));
+    } else {
+        CHECK(anelm_hybrid_step_create(&step, &dims, m.layers.data(), m.n_layers, x, h, ANELM_STEP_EAGER, st));
+        for (size_t i = 0; i < prompt.size(); i++) forward(prompt[i], i + 1 == prompt.size());
+    }
     std::vector<int32_t> generated;
     generated.reserve((size_t)max_tokens + 1);   // stable addresses for the async copies
     auto sample = [&]() {

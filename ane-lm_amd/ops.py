@@ -208,6 +208,32 @@ def attn_prefill(q, k, v, out_dtype=_F32):
     return out
 
 
+def full_attn_prefill(q_gate, k, v, k_cache, v_cache, q_norm_w, k_norm_w, ring: KVRing, n_heads,
+                      n_kv_heads, head_dim, rot_dim, pos0, theta=1e7, eps=1e-6, rope_mode=ROPE_INTERLEAVED,
+                      gate=True, rope_table=None, rope_rows=0, proj=None):
+    """S tokens of qwen3_5.cpp:944-1002 over the fp16 ring in one call;
+    q_gate [S][Hq][2D], k/v [S][Hkv][D] -- or proj [S][q_gate | k | v] (the
+    first projection's rows; q_gate, k, v ignored); returns out [S][Hq][D]."""
+    _need(k_cache, _F16, "k_cache")
+    stride = 0
+    if proj is not None:
+        S, stride = proj.shape
+        base = proj.data_ptr()
+        q_gate, k = proj, None
+        qp = ctypes.c_void_p(base)
+        kp = ctypes.c_void_p(base + 4 * n_heads * 2 * head_dim)
+        vp = ctypes.c_void_p(base + 4 * (n_heads * 2 * head_dim + n_kv_heads * head_dim))
+    else:
+        S = q_gate.shape[0]
+        qp, kp, vp = _p(q_gate), _p(k), _p(v)
+    out = torch.empty(S, n_heads, head_dim, device=q_gate.device, dtype=_F32)
+    call("anelm_full_attn_prefill", _p(out), qp, kp, vp, stride, _p(k_cache), _p(v_cache),
+         _p(q_norm_w), _p(k_norm_w), S, n_heads, n_kv_heads, head_dim, rot_dim, pos0, theta, eps, rope_mode,
+         1 if gate else 0, _p(rope_table), rope_rows, ctypes.byref(ring.start), ctypes.byref(ring.len),
+         ring.capacity, _s())
+    return out
+
+
 # --------------------------------------------------------------- DeltaNet
 def ssm_step(state, q, k, v, decay, beta, flags=0):
     """cpu_ops.cpp:131-146 on one head; state [dk][dv] updated in place."""
@@ -250,6 +276,17 @@ def deltanet_decode_from_proj(state, conv_state, conv_pos, proj, conv_w, A, dt_b
     call("anelm_deltanet_decode_from_proj", _p(out), _p(state), _p(conv_state), ctypes.byref(conv_pos),
          _p(proj), _p(conv_w), _p(A), _p(dt_bias), _p(norm_w), Hk, Hv, dk, dv, conv_kernel, flags, _s())
     return out
+
+
+def deltanet_prefill_from_proj(state, conv_state, conv_pos: ctypes.c_int, proj, conv_w, A, dt_bias, norm_w,
+                               Hk, flags, conv_kernel=4):
+    """S tokens of qwen3_5.cpp:849-908 from the projections; proj [S][proj_dim]."""
+    Hv, dk, dv = state.shape
+    S = proj.shape[0]
+    y = torch.empty(S, Hv, dv, device=state.device, dtype=_F32)
+    call("anelm_deltanet_prefill_from_proj", _p(y), _p(state), _p(conv_state), ctypes.byref(conv_pos),
+         _p(proj), _p(conv_w), _p(A), _p(dt_bias), _p(norm_w), S, Hk, Hv, dk, dv, conv_kernel, flags, _s())
+    return y
 
 
 def deltanet_prefill(state, q, k, v, a, b, A, dt_bias, flags, chunk=64):

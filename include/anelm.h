@@ -232,6 +232,38 @@ int anelm_attn_prefill(void* out, int out_dtype, const uint16_t* q, const uint16
                        const uint16_t* v, int S, int n_heads, int n_kv_heads, int head_dim,
                        void* stream);
 
+/* Prompt prefill through one full-attention layer core: the S decode steps
+ * generate.cpp:55-85 runs for a prompt (forward_full_attn_from_proj,
+ * models/llm/qwen3_5.cpp:944-1002, per token; forward_batch, :1164-1217,
+ * batches only the projections around it) as one call.  Token t of the
+ * prompt, at position pos0 + t:
+ *   q rows (q_gate [S][n_heads][2*head_dim]) and k (k, v
+ *   [S][n_kv_heads][head_dim]) RMS-normalised with q_norm_w / k_norm_w (both
+ *   NULL: no norm, :952-959); RoPE at pos0 + t (:961-971); k, v appended to
+ *   the fp16 ring as the t-th new key (:973-986); gqa_attention over the ring
+ *   as it stands after that append -- the last min(capacity, len0 + t + 1)
+ *   keys, len0 = *cache_len on entry (:989-991); the sigmoid output gate when
+ *   `gate` (:993-1000).
+ * proj_stride: floats from one token's rows to the next in q_gate, k and v
+ * -- with the first projection's output [S][q_gate | k | v] (forward_batch's
+ * proj_batch_, :1181-1189) pass q_gate = proj, k = proj + n_heads*2*head_dim,
+ * v = k + n_kv_heads*head_dim and its row length; 0 = each array packed.
+ * out [S][n_heads][head_dim] fp32.  *cache_start / *cache_len (HOST ints)
+ * end as after S appends; prompt keys that a later prompt key overwrote are
+ * not written.  RoPE rows: rope_table (device, [rope_rows][rot_dim]: cos of
+ * the rot_dim/2 pairs, then sin -- anelm_rope_table, the reference's table of
+ * qwen3_5.cpp:308-324) for positions below rope_rows, else the same formula
+ * on the device (the reference switches to cpu_ops.cpp:51-55 past its
+ * table); rope_table may be NULL.  q enters the fp16 MFMA products as fp16
+ * (after norm and RoPE in fp32); keys and values are the cache's fp16.
+ * head_dim 128 or 256; n_heads / n_kv_heads in {1, 2, 4, 8}. */
+int anelm_full_attn_prefill(float* out, const float* q_gate, const float* k, const float* v,
+                            int proj_stride, uint16_t* k_cache, uint16_t* v_cache, const float* q_norm_w,
+                            const float* k_norm_w, int S, int n_heads, int n_kv_heads, int head_dim,
+                            int rot_dim, int pos0, float theta, float eps, int rope_mode, int gate,
+                            const float* rope_table, int rope_rows, int* cache_start, int* cache_len,
+                            int cache_capacity, void* stream);
+
 /* ------------------------------------------------------------- DeltaNet */
 
 /* ssm_step, cpu_ops.h:50-51 / cpu_ops.cpp:131-146, for one head:
@@ -289,6 +321,23 @@ int anelm_deltanet_decode_from_proj(float* y, float* state, float* conv_state, i
 int anelm_deltanet_prefill(float* y, float* state, const float* q, const float* k, const float* v,
                            const float* a, const float* b, const float* A, const float* dt_bias,
                            int S, int Hk, int Hv, int dk, int dv, int chunk, int flags, void* stream);
+
+/* Prompt prefill through one Gated-DeltaNet layer core from its projections:
+ * the S steps of anelm_deltanet_decode_from_proj (forward_deltanet_from_proj,
+ * models/llm/qwen3_5.cpp:849-908, per token, as generate.cpp:55-85 and
+ * forward_batch :1164-1217 run it over a prompt) as one call.
+ *   proj [S][2*Hk*dk + Hv*dv + Hv*dv + 2*Hv]: per token [mixed qkv | z | a | b];
+ *   the causal conv1d over the conv ring followed by the prompt's mixed
+ *   channels + SiLU (cpu_ops.cpp:89-129, :6-13), split into q | k | v; the
+ *   chunked recurrence (anelm_deltanet_prefill); with ANELM_DN_GATED_NORM,
+ *   rmsnorm_gated(y, z, norm_w) per token and value head (:902-908).
+ * y [S][Hv][dv]; state [Hv][dk][dv] ends after the last token; conv_state
+ * [2*Hk*dk + Hv*dv][conv_kernel-1] and *conv_pos (HOST int) end as after S
+ * conv1d_update calls.  dk, dv = 128; conv_kernel 2..16. */
+int anelm_deltanet_prefill_from_proj(float* y, float* state, float* conv_state, int* conv_pos,
+                                     const float* proj, const float* conv_w, const float* A,
+                                     const float* dt_bias, const float* norm_w, int S, int Hk, int Hv,
+                                     int dk, int dv, int conv_kernel, int flags, void* stream);
 
 /* ----------------------------------------------------------------- LUT6 */
 /* LUT6 weight format: W[r][c] = lut[r/32][idx(r,c)], lut fp16 [out/32][64],

@@ -1,7 +1,8 @@
 """The C ABI from a compiled C++ caller: ane-lm_amd/stream_generate (built by
 __graft_entry__.build() from ane-lm_amd/host/stream_generate.cpp) runs the
 stream_generate decode loop of generate.cpp:30-140 -- single-token prefill of
-the prompt, then sample_token with the generated tokens as the penalty window
+the prompt (or the whole prompt through each layer at once), then
+sample_token with the generated tokens as the penalty window
 -- with every forward on the GPU through anelm_hybrid_step, the LM head and
 anelm_sample_token.  Its tokens are compared with the oracle's loop over the
 same random-init weights."""
@@ -80,10 +81,10 @@ def _oracle_loop(orc, m, prompt, n, T, seed):
     return toks, margins
 
 
-def _run(model, prompt, n, T, seed):
+def _run(model, prompt, n, T, seed, prefill_mode=0):
     assert os.path.exists(BIN), "stream_generate not built (run __graft_entry__.build())"
-    r = subprocess.run([BIN, model, ",".join(map(str, prompt)), str(n), str(T), "1.2", "256", "0.1", str(seed)],
-                       capture_output=True, text=True, timeout=120)
+    r = subprocess.run([BIN, model, ",".join(map(str, prompt)), str(n), str(T), "1.2", "256", "0.1", str(seed),
+                        str(prefill_mode)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     lines = r.stdout.split("\n")
     toks = [int(s.split()[1]) for s in lines if s.startswith("token ")]
@@ -100,6 +101,22 @@ def test_host_loop_greedy_with_penalties(orc, tmp_path):
     want, margins = _oracle_loop(orc, m, prompt, 40, 0.0, 7)
     assert min(margins) > 1e-3, "seeded model has a near-tie: pick another seed"
     assert _run(model, prompt, 40, 0.0, 7) == want
+
+
+def test_host_loop_batched_prefill_greedy(orc, tmp_path):
+    """The prompt through every layer at once (forward_batch,
+    models/llm/qwen3_5.cpp:1164-1217: batched projections; here the cores
+    take the whole prompt too -- anelm_full_attn_prefill over the fp16 ring,
+    anelm_deltanet_prefill_from_proj over the conv ring and state), then the
+    decode loop from the state it left: the same tokens as the oracle's
+    single-token prefill and decode."""
+    m = tiny_lm(2030)
+    model = str(tmp_path / "tiny.bin")
+    _write_model(m, model)
+    prompt = [1, 17, 333, 5, 4000, 12, 77, 4095, 600, 31, 2, 999]
+    want, margins = _oracle_loop(orc, m, prompt, 40, 0.0, 7)
+    assert min(margins) > 1e-3, "seeded model has a near-tie: pick another seed"
+    assert _run(model, prompt, 40, 0.0, 7, prefill_mode=1) == want
 
 
 def test_host_loop_sampled(orc, tmp_path):
