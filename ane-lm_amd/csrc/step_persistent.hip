@@ -386,6 +386,9 @@ __device__ __forceinline__ void gemv_issue(Buf<3 * NI>& b, LutRegs& lr, const Ge
         lr.v[0] = __builtin_amdgcn_raw_buffer_load_b16(rl, lane * 2, 0, 0);
         lr.v[1] = __builtin_amdgcn_raw_buffer_load_b16(rl, (64 + lane) * 2, 0, 0);   // 0 past ng groups
         lr.v[2] = __builtin_amdgcn_raw_buffer_load_b16(rl, (128 + lane) * 2, 0, 0);
+        // the LUT loads stay ahead of the weights: vector-memory waits
+        // complete in issue order, so the table build waits for these alone
+        __builtin_amdgcn_sched_barrier(0);
     }
     const uint8_t* Wt = (mt ? W[1] : W[0]) + (size_t)q.R0 * q.C * 12;
     const __amdgpu_buffer_rsrc_t r = rsrc(Wt, (uint32_t)(q.nrows * q.C * 12));
@@ -1136,18 +1139,27 @@ enum : int { kDN = 0, kATT = 1, kNONE = 2 };
 
 constexpr int kNDG = 4;              // gate/up instructions decoded before the input (registers)
 
-// Compute waves: first half of layer l's gate/up weights with its LUTs, the
-// pair tables, and the lookups of the first kNDG instructions -- none of it
-// needs the input, so it runs while a barrier is pending.
+// Compute waves: first half of layer l's gate/up weights with its LUTs,
+// issued while the barrier before a DeltaNet core is pending.
 template <int NIG>
-__device__ __forceinline__ void gu_first(Buf<3 * NIG>& gb, LutRegs& glr, Buf<8 * kNDG>& gd, const GemvGeo& gu,
-                                         const PArgs& a, const PLayer& L, int l, int wave, int ln, char* lds) {
+__device__ __forceinline__ void gu_first(Buf<3 * NIG>& gb, LutRegs& glr, const GemvGeo& gu, const PArgs& a,
+                                         const PLayer& L, int l, int wave, int ln) {
     const uint8_t* const GW[2] = {L.w[0], L.w[1]};
     const uint16_t* const GLU[2] = {L.lut[0], L.lut[1]};
-    const int p = 3 * l + 1;
     const bool tw0 = wave == 0 && ln == 0;
     gemv_issue<NIG, 0, NIG / 2, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
-    trace_stamp(a, p, kTrX0, tw0);
+    trace_stamp(a, 3 * l + 1, kTrX0, tw0);
+}
+// Compute waves: layer l's gate/up pair tables and the lookups of its first
+// kNDG instructions (from the first half issued by gu_first); they need
+// neither the input nor the core, so they run after a DeltaNet core while
+// the barrier that follows it resolves (the core does not use the table
+// region of LDS), not before the core, where a late LUT load would delay it.
+template <int NIG>
+__device__ __forceinline__ void gu_tables(const Buf<3 * NIG>& gb, const LutRegs& glr, Buf<8 * kNDG>& gd,
+                                          const GemvGeo& gu, const PArgs& a, int l, int wave, int ln, char* lds) {
+    const int p = 3 * l + 1;
+    const bool tw0 = wave == 0 && ln == 0;
     gemv_tables(glr, gu, 2, wave, ln, lds, ctl_ints(lds) + 8, gu.P * (l + 1));
     trace_stamp(a, p, kTrX1, tw0);
     static_assert(kNDG <= NIG / 2, "decode-ahead covers the issued first half only");
@@ -1201,6 +1213,13 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
         // completed with the arrival's drain): the normalised input is ready
         // before the barrier resolves
         stage_x_fin<JH>(a, ln, lds);
+    }
+    if constexpr (KIND == kDN) {
+        // the pair tables and early lookups of this layer's gate/up (first
+        // half, issued before the core) meanwhile: they issue no memory
+        // request, so they need not wait for the arrival (the control wave
+        // only defines its copies)
+        gu_tables<NIG>(gb, glr, gd, gu, a, l, wave, opaque(lane), lds);
     }
     wg_sync();   // the bulk loads below queue behind the arrival
     ln = opaque(lane);
@@ -1262,8 +1281,9 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
             trace_stamp(a, p0, kTrRelease, twc);
             if (ln == 0) ctl[0] = okw;
         }
-        // the first half landed during the core: the second half goes out now
-        // (the control wave takes no share: it only defines its copies)
+        // the first half landed during the core: the second half goes out
+        // now, while the barrier resolves (the control wave takes no share
+        // and only defines its copies)
         gemv_issue<NIG, NAG, NIG, false>(gb, glr, gu, GW, GLU, 2, wave, ln);
         trace_stamp(a, p0 + 1, kTrX3, tw0);
         wg_sync();
@@ -1386,9 +1406,9 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     }
     if constexpr (NEXT == kDN) {
         // the next layer's gate/up weights stream in during this barrier and
-        // the next core (the down tables in LDS are dead now); the control
-        // wave takes no share and only defines its copies
-        gu_first<NIG>(gb, glr, gd, gu, a, Ln, l + 1, wave, ln, lds);
+        // the next core; the control wave takes no share and only defines
+        // its copies
+        gu_first<NIG>(gb, glr, gu, a, Ln, l + 1, wave, ln);
     }
     if constexpr (more) {
         wg_sync();
@@ -1444,7 +1464,7 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     }
     wg_sync();
     // layer 0's gate/up weights start streaming with its core
-    gu_first<NIG>(gb, glr, gd, gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I), a, L0, 0, wave, lane, lds);
+    gu_first<NIG>(gb, glr, gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I), a, L0, 0, wave, lane);
     const int groups = a.n_layers / 4;
     for (int gr = 0; gr < groups; gr++) {
         const int l0 = 4 * gr;
