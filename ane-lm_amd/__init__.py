@@ -202,5 +202,6 @@ STEP_EAGER = 0
 STEP_GRAPH = 1
 STEP_PERSISTENT = 2
 STEP_STATIC = 4
+STEP_COOPERATIVE = 8
 
 from . import ops  # noqa: E402,F401

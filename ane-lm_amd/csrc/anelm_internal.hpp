@@ -150,7 +150,7 @@ struct PersistentStep;
 int persistent_create(PersistentStep** out, const anelm_hybrid_dims* dims,
                       const anelm_hybrid_layer* layers, int n_layers, float* x, float* h,
                       hipStream_t stream);
-int persistent_run(PersistentStep* s, bool advance, hipStream_t stream);
+int persistent_run(PersistentStep* s, bool advance, bool cooperative, hipStream_t stream);
 int persistent_status(PersistentStep* s, int* status);
 int persistent_trace(PersistentStep* s, unsigned long long* host, size_t n_words, int* grid, int* row);
 void persistent_destroy(PersistentStep* s);

@@ -103,8 +103,9 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
     ANELM_NONNULL(x);
     ANELM_NONNULL(h_scratch);
     ANELM_REQUIRE(n_layers > 0, "hybrid_step: n_layers %d", n_layers);
-    ANELM_REQUIRE(mode == ANELM_STEP_EAGER || mode == ANELM_STEP_GRAPH || mode == ANELM_STEP_PERSISTENT ||
-                      mode == (ANELM_STEP_PERSISTENT | ANELM_STEP_STATIC),
+    ANELM_REQUIRE(mode == ANELM_STEP_EAGER || mode == ANELM_STEP_GRAPH ||
+                      ((mode & ANELM_STEP_PERSISTENT) &&
+                       (mode & ~(ANELM_STEP_PERSISTENT | ANELM_STEP_STATIC | ANELM_STEP_COOPERATIVE)) == 0),
                   "hybrid_step: mode %d unknown", mode);
     const bool use_graph = mode == ANELM_STEP_GRAPH;
     ANELM_REQUIRE(!use_graph || stream != nullptr, "hybrid_step: graph capture needs a non-null stream");
@@ -193,7 +194,9 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
 extern "C" int anelm_hybrid_step_run(anelm_hybrid_step* step, void* stream) {
     ANELM_NONNULL(step);
     hipStream_t st = as_stream(stream);
-    if (step->ps) return persistent_run(step->ps, (step->mode & ANELM_STEP_STATIC) == 0, st);
+    if (step->ps)
+        return persistent_run(step->ps, (step->mode & ANELM_STEP_STATIC) == 0,
+                              (step->mode & ANELM_STEP_COOPERATIVE) != 0, st);
     if (step->use_graph) {
         ANELM_HIP(hipGraphLaunch(step->exec, st));
         return ANELM_OK;

@@ -1900,7 +1900,7 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
 // One step.  With `advance`, every attention ring and position moves one
 // token forward afterwards (the host KVCache bookkeeping of qwen3_5.cpp:973-983):
 // the launch writes the next step's descriptors itself.
-int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
+int persistent_run(PersistentStep* s, bool advance, bool cooperative, hipStream_t st) {
     if (advance && max_position(s, true) >= s->rope_rows) {
         // the table must hold the next step's row: grow it (the previous
         // launch, which wrote the descriptors being replaced, completes first)
@@ -1908,8 +1908,18 @@ int persistent_run(PersistentStep* s, bool advance, hipStream_t st) {
         const int rc = upload(s, true);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st, (const pk::PArgs*)s->d_args,
-                       advance ? 1 : 0);
+    if (cooperative) {
+        // the runtime admits the grid only once every workgroup can be
+        // resident, so kernels on other streams cannot starve a barrier
+        const pk::PArgs* ap = s->d_args;
+        int adv = advance ? 1 : 0;
+        void* kargs[] = {(void*)&ap, (void*)&adv};
+        ANELM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(s->kernel), dim3(s->grid),
+                                             dim3(pk::kNT), kargs, pk::kLdsBytes, st));
+    } else {
+        hipLaunchKernelGGL(s->kernel, dim3(s->grid), dim3(pk::kNT), pk::kLdsBytes, st,
+                           (const pk::PArgs*)s->d_args, advance ? 1 : 0);
+    }
     ANELM_LAUNCHED("step_kernel");
     s->launched = true;
     if (advance) {

@@ -527,11 +527,20 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          (the Qwen3.5-4B and Qwen3.5-0.8B shapes on 256
  *                          CUs) and layers without projections (first_w
  *                          NULL); other shapes return ANELM_EINVAL from
- *                          create. */
+ *                          create.
+ *   ANELM_STEP_COOPERATIVE (with PERSISTENT) launches through
+ *                          hipLaunchCooperativeKernel: the runtime starts the
+ *                          grid only when every workgroup can be resident, so
+ *                          kernels running concurrently on other streams delay
+ *                          the step instead of starving its grid barriers
+ *                          (without it, such a step gives up after ~0.7 s and
+ *                          reports status 1).  Costs ~17 us per step on
+ *                          MI355X. */
 #define ANELM_STEP_EAGER 0
 #define ANELM_STEP_GRAPH 1
 #define ANELM_STEP_PERSISTENT 2
 #define ANELM_STEP_STATIC 4
+#define ANELM_STEP_COOPERATIVE 8
 
 /* Builds a step over n_layers descriptors (copied), x [hidden] and
  * h_scratch [2*inter] device buffers (the step's FFN scratch). */

@@ -140,6 +140,36 @@ def test_generate_greedy_with_penalties_64(anelm, orc, dev):
     assert forced <= 2 and len(set(toks)) > 4, (forced, toks)
 
 
+def test_generate_greedy_exact_64(anelm, orc, dev):
+    """The 64-token greedy gate through the product step: two independent
+    loops (each feeds its OWN tokens back), greedy with the reference's
+    default penalties, must emit identical tokens.  The seed is checked
+    first: the oracle's smallest top-2 gap of the penalised logits over the
+    64 decisions is ~8e-3, far above the ~1e-6 relative GPU/oracle logit
+    difference, so every token is decided."""
+    m = tiny_lm(2042)
+    ref = OracleLM(orc, m)
+    want, gaps, tok = [], [], 1
+    for pos in range(64):
+        _, logits = ref.step(tok, pos)
+        tok, adj = orc.sample_token(logits, np.array(want, np.int32), 0.0, 1.2, 256, 0.1, 0.5)
+        top2 = np.sort(adj)[-2:]
+        gaps.append(float(top2[1] - top2[0]))
+        want.append(tok)
+    assert min(gaps) > 1e-3, "seeded model has a near-tie: pick another seed"
+    gpu = StepLM(anelm, m, dev, mode=anelm.STEP_EAGER)
+    got, tok = [], 1
+    try:
+        for pos in range(64):
+            logits = gpu.forward(tok)
+            rec = to_dev(np.array(got, np.int32), dev) if got else None
+            tok = int(to_host(anelm.ops.sample_token(logits, rec, 0.0, 1.2, 256, 0.1, 0.5))[0])
+            got.append(tok)
+    finally:
+        gpu.close()
+    assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+
+
 def test_generate_sampled_t06(anelm, orc, dev):
     """Temperature 0.6 with seeded uniform draws (the reference's drand48)."""
     m = tiny_lm(2026)

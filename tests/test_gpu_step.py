@@ -223,7 +223,7 @@ def _graph_after_growth(anelm, orc, dev, dm, m, x0):
         anelm.call("anelm_hybrid_step_destroy", h)
 
 
-def _persistent_vs_eager(anelm, m, dev, steps, label):
+def _persistent_vs_eager(anelm, m, dev, steps, label, extra_mode=0):
     """Runs `steps` advancing decode steps of model m through the eager path
     and the persistent step side by side and compares every core output,
     state, cache and the hidden state after each."""
@@ -232,7 +232,7 @@ def _persistent_vs_eager(anelm, m, dev, steps, label):
     s = _stream()
     rc, ha = _create(anelm, a, anelm.STEP_EAGER, s)
     assert rc == 0, anelm.last_error()
-    rc, hb = _create(anelm, b, anelm.STEP_PERSISTENT, s)
+    rc, hb = _create(anelm, b, anelm.STEP_PERSISTENT | extra_mode, s)
     if rc != 0:
         anelm.call("anelm_hybrid_step_destroy", ha)
         pytest.skip(f"persistent step unsupported here: {anelm.last_error()}")
@@ -272,6 +272,14 @@ def test_persistent_step_matches_eager(anelm, dev):
     state is checked at 1e-4."""
     m = hybrid_model(901, 8, rings=[(0, 5000), (8000, 8192)], lut_std=0.005)
     _persistent_vs_eager(anelm, m, dev, 3, "8 layers")
+
+
+def test_persistent_step_cooperative_launch(anelm, dev):
+    """The cooperative launch (the runtime admits the grid only when every
+    workgroup can be resident) runs the same kernel: 3 advancing steps
+    against the eager path."""
+    m = hybrid_model(908, 4, rings=[(0, 5000)], lut_std=0.005)
+    _persistent_vs_eager(anelm, m, dev, 3, "cooperative", anelm.STEP_COOPERATIVE)
 
 
 def test_persistent_step_rope_table_growth(anelm, dev):
