@@ -14,8 +14,9 @@
 //     columns is permuted identically in A and B, so each lane's weights are
 //     one contiguous 48*NP-byte stretch of its row;
 //   * the wave's X window sits in registers for the whole launch (fp16, as the
-//     LUT6 path takes its activations); weights are double-buffered in
-//     registers one group ahead; each 12-bit field (two indices) dequantises
+//     LUT6 path takes its activations); a group's weights are staged in LDS
+//     one group ahead by coalesced loads (1 KiB per wave instruction) and
+//     taken into registers from there; each 12-bit field (two indices) dequantises
 //     through a 4096-entry pair table T[(i1 << 6) | i0] = (lut[i0], lut[i1])
 //     built per group in LDS (double-buffered);
 //   * the NW partial 32x32 tiles are summed through LDS and written as fp32.
@@ -68,18 +69,41 @@ __device__ __forceinline__ uint32_t pair_off(const uint32_t (&wd)[NWD], int p, u
     return (v & 0x3FFCu) | tb;
 }
 
-// Group g's weights of this lane (buffer loads over the matrix, streaming
-// cache policy).  A group past the last one lies outside the buffer: its
-// loads return zeros without touching memory, so the pipeline's prefetch
-// after a workgroup's last group costs no traffic.
-// The offset is computed in 32 bits (the launch bounds (out_dim + 32 * 1024) *
-// ldw below 2^31) from a laundered lane index: nothing of it is kept live
-// across the group loop, where a spilled address would be reloaded through
-// the vector-memory counter and the reload's wait would drain the prefetch.
+// Group g's 32 weight rows are staged in LDS before each lane takes its own
+// stretch: a lane's operand stretch (48*NP bytes of its row) is 16-byte
+// pieces of 32 different rows, which as direct loads touch 64 partial cache
+// lines per wave instruction.  Staged, every wave instruction reads 1 KiB of
+// consecutive memory.  Row r of the group sits at r * (CH * 16) in the stage,
+// CH = row bytes / 16 + 1: the last 16 bytes of a row are padding (loaded
+// from past the buffer's end, so zeros), which keeps one wave instruction's
+// 64 destination chunks consecutive and puts the operand reads of
+// consecutive rows on different banks.
+template <int NW, int NP>
+struct Stage {
+    static constexpr int RB = NW * 96 * NP;                // row bytes of this column slice
+    static constexpr int CH = RB / 16 + 1;                 // 16-byte chunks per staged row
+    static constexpr int NI = (32 * CH + 63) / 64;         // wave instructions per group
+    static constexpr int kBytes = NI * 1024;
+};
+template <int NW, int NP>
+__device__ __forceinline__ void stage_group(const GemmArgs& a, int g, char* stage, int w, int lane) {
+    using S = Stage<NW, NP>;
+    asm volatile("" : "+v"(lane));   // recomputed per group, not held across the loop
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, (int)((long)a.out_dim * a.ldw), 0x00020000);
+    for (int i = w; i < S::NI; i += NW) {
+        const int q = i * 64 + lane, row = q / S::CH, c = q - row * S::CH;
+        // padding chunks and chunks past the 32 rows read from past the end
+        const int off = (row < 32 && c < S::CH - 1) ? (g * 32 + row) * (int)a.ldw + 16 * c : 0x7ffffff0;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(stage + i * 1024), 16,
+                                                 off, 0, 0, 2);
+    }
+}
+// A workgroup with a single group (the split-K launches) has nothing to
+// overlap the staging with: its lanes load their stretches directly.  The
+// offset is 32-bit (the launch bounds (out_dim + 32 * 1024) * ldw below 2^31).
 template <int NP>
-__device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w,
-                                             int lane) {
-    asm volatile("" : "+v"(lane));
+__device__ __forceinline__ void load_direct(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w, int lane) {
     const int m = lane & 31, hh = lane >> 5;
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, (int)((long)a.out_dim * a.ldw), 0x00020000);
@@ -87,6 +111,22 @@ __device__ __forceinline__ void load_weights(uint32_t (&wd)[12 * NP], const Gemm
 #pragma unroll
     for (int i = 0; i < 3 * NP; i++) {
         const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 2));
+        wd[4 * i] = v.x;
+        wd[4 * i + 1] = v.y;
+        wd[4 * i + 2] = v.z;
+        wd[4 * i + 3] = v.w;
+    }
+}
+// This lane's stretch: row m = lane % 32, bytes w*96*NP + hh*48*NP .. +48*NP.
+template <int NW, int NP>
+__device__ __forceinline__ void read_group(uint32_t (&wd)[12 * NP], const char* stage, int w, int lane) {
+    using S = Stage<NW, NP>;
+    asm volatile("" : "+v"(lane));
+    const int m = lane & 31, hh = lane >> 5;
+    const char* src = stage + m * (S::CH * 16) + w * 96 * NP + hh * 48 * NP;
+#pragma unroll
+    for (int i = 0; i < 3 * NP; i++) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * i);
         wd[4 * i] = v.x;
         wd[4 * i + 1] = v.y;
         wd[4 * i + 2] = v.z;
@@ -220,21 +260,22 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
                                    (_Float16)(hi[t].z * z), (_Float16)(hi[t].w * z)};
         }
     }
-    // Software pipeline, one group ahead: while group g is multiplied from
-    // registers wa (table slot 0), group gn's LUT and weights are in flight
-    // into lr / wb, its table is built into slot 1 after the products, and the
-    // roles swap for the next group.  The LUT load is issued before the
-    // weights, so waiting for it never waits for them; weight loads past the
-    // last group read nothing (out of the buffer's range) and are never used.
+    // Pipeline, one group ahead: group g's staged weights are taken into
+    // registers, then the next group's staging loads go out and run during
+    // g's products; g's pair table (slot j & 1) was built while group g-1
+    // was multiplied, and the next group's table is built after the
+    // products.  The LUT loads are issued before the weights, so the first
+    // table build never waits for them.
     const int stride = gridDim.x;
-    uint32_t wa[12 * NP], wb[12 * NP];
-    load_weights<NP>(wa, a, g, w, lane);
-    stage_luts<nt>(a, lds, 0, tid);
-    lds_barrier();
-    build_table(lds, 0, 0, w, nw, lane);
+    char* stage = lds + kRedOff + NW * 16 * kRedRow * (int)sizeof(float);
+    float* red = reinterpret_cast<float*>(lds + kRedOff);
+    uint32_t wa[12 * NP];
     if (g + stride >= n_groups) {
-        // the only group of this workgroup: no prefetch of a next one
-        float* red = reinterpret_cast<float*>(lds + kRedOff);
+        // the only group of this workgroup
+        load_direct<NP>(wa, a, g, w, lane);
+        stage_luts<nt>(a, lds, 0, tid);
+        lds_barrier();
+        build_table(lds, 0, 0, w, nw, lane);
         lds_barrier();
         float16_t c = float16_t{};
         group_mfma<NP>(c, wa, xb, lds, 0u);
@@ -244,42 +285,36 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
         reduce_store<NW, ACC>(a, g, lds, tid);
         return;
     }
-    load_weights<NP>(wb, a, g + stride, w, lane);
-    float* red = reinterpret_cast<float*>(lds + kRedOff);
-    // j counts the workgroup's groups; LUTs are restaged every kLutSlots groups
-    for (int j = 0;; j += 2) {
-        lds_barrier();                                 // table 0 ready; red free
+    stage_luts<nt>(a, lds, 0, tid);
+    stage_group<NW, NP>(a, g, stage, w, lane);
+    lds_barrier();                                     // LUTs staged
+    build_table(lds, 0, 0, w, nw, lane);
+    for (int j = 0;; j++) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);            // this wave's staging loads of group g landed
+        lds_barrier();                                 // every wave's; table j & 1 ready; red free
+        read_group<NW, NP>(wa, stage, w, lane);
+        lds_barrier();                                 // the stage is free
+        const int gn = g + stride;
+        if (gn < n_groups) stage_group<NW, NP>(a, gn, stage, w, lane);
         {
             float16_t c = float16_t{};
-            group_mfma<NP>(c, wa, xb, lds, 0u);
+            group_mfma<NP>(c, wa, xb, lds, (uint32_t)((j & 1) * kTabBytes));
 #pragma unroll
             for (int e = 0; e < 16; e++) red[w * 16 * kRedRow + red_pos(e, lane)] = c[e];
         }
-        build_table(lds, 1, j + 1, w, nw, lane);      // next group (table 1 is free since the last barrier)
-        lds_barrier();                                 // partial tiles and table 1 complete
-        reduce_store<NW, ACC>(a, g, lds, tid);
-        g += stride;
-        if (g >= n_groups) break;
-        load_weights<NP>(wa, a, g + stride, w, lane);
-        lds_barrier();                                 // table 1 ready; red free
-        {
-            float16_t c = float16_t{};
-            group_mfma<NP>(c, wb, xb, lds, (uint32_t)kTabBytes);
-#pragma unroll
-            for (int e = 0; e < 16; e++) red[w * 16 * kRedRow + red_pos(e, lane)] = c[e];
+        if (gn < n_groups) {
+            if (((j + 1) & (kLutSlots - 1)) == 0) {
+                // restage the next kLutSlots LUTs (every 64 groups of this workgroup)
+                lds_barrier();
+                stage_luts<nt>(a, lds, j + 1, tid);
+                lds_barrier();
+            }
+            build_table(lds, (j + 1) & 1, j + 1, w, nw, lane);
         }
-        if (((j + 2) & (kLutSlots - 1)) == 0) {
-            // restage the next kLutSlots LUTs (every 64 groups of this workgroup)
-            lds_barrier();
-            stage_luts<nt>(a, lds, j + 2, tid);
-            lds_barrier();
-        }
-        build_table(lds, 0, j + 2, w, nw, lane);
-        lds_barrier();
+        lds_barrier();                                 // partial tiles complete
         reduce_store<NW, ACC>(a, g, lds, tid);
-        g += stride;
+        g = gn;
         if (g >= n_groups) break;
-        load_weights<NP>(wb, a, g + stride, w, lane);
     }
 }
 
@@ -336,7 +371,11 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
     // else a grid-stride walk over the groups (prefetching the next one)
     int grid = n_groups;
     if (nsplit == 1 && grid > dev->num_cus) grid = dev->num_cus;
-    const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float);
+    // a workgroup with one group loads its weights directly (no stage)
+    const int stage_bytes = grid == n_groups ? 0
+                            : np == 2       ? (32 * (waves * 192 / 16 + 1) + 63) / 64 * 1024
+                                            : (32 * (waves * 96 / 16 + 1) + 63) / 64 * 1024;
+    const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float) + stage_bytes;
     using K = void (*)(GemmArgs);
 #define ANELM_K2(A) {nullptr, lut6_gemm_kernel<2, 1, A>, lut6_gemm_kernel<2, 2, A>, lut6_gemm_kernel<2, 3, A>,     \
                      lut6_gemm_kernel<2, 4, A>, lut6_gemm_kernel<2, 5, A>, lut6_gemm_kernel<2, 6, A>,              \
@@ -353,10 +392,14 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
     const int acc = accumulate ? 1 : 0;
     const K kp = np == 2 ? k2[acc][waves] : k1[acc][waves];
     if (!kp) return set_error(ANELM_EINVAL, "lut6_gemm: no kernel for %d waves (np %d)", waves, np);
+    // the attribute covers the staged size (the larger of the two per kernel)
     static bool attr_set[2][2][16] = {};
     if (!attr_set[acc][np - 1][waves]) {
+        const int full = (int)((size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float) +
+                               (np == 2 ? (32 * (waves * 192 / 16 + 1) + 63) / 64 * 1024
+                                        : (32 * (waves * 96 / 16 + 1) + 63) / 64 * 1024));
         ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kp), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)lds));
+                                      full));
         attr_set[acc][np - 1][waves] = true;
     }
     hipLaunchKernelGGL(kp, dim3(grid, nsplit), dim3(waves * 64), lds, st, a);
