@@ -23,6 +23,8 @@
 // Reference math: matvec (core/cpu_ops.cpp:77-80) on the dequantised weights.
 #include "anelm_internal.hpp"
 
+#include <algorithm>
+
 namespace anelm {
 namespace {
 
@@ -97,24 +99,6 @@ __device__ __forceinline__ void stage_group(const GemmArgs& a, int g, char* stag
         const int off = (row < 32 && c < S::CH - 1) ? (g * 32 + row) * (int)a.ldw + 16 * c : 0x7ffffff0;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(stage + i * 1024), 16,
                                                  off, 0, 0, 2);
-    }
-}
-// A workgroup with a single group (the split-K launches) has nothing to
-// overlap the staging with: its lanes load their stretches directly.  The
-// offset is 32-bit (the launch bounds (out_dim + 32 * 1024) * ldw below 2^31).
-template <int NP>
-__device__ __forceinline__ void load_direct(uint32_t (&wd)[12 * NP], const GemmArgs& a, int g, int w, int lane) {
-    const int m = lane & 31, hh = lane >> 5;
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, (int)((long)a.out_dim * a.ldw), 0x00020000);
-    const int off = (g * 32 + m) * (int)a.ldw + w * 96 * NP + hh * 48 * NP;
-#pragma unroll
-    for (int i = 0; i < 3 * NP; i++) {
-        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 2));
-        wd[4 * i] = v.x;
-        wd[4 * i + 1] = v.y;
-        wd[4 * i + 2] = v.z;
-        wd[4 * i + 3] = v.w;
     }
 }
 // This lane's stretch: row m = lane % 32, bytes w*96*NP + hh*48*NP .. +48*NP.
@@ -271,12 +255,18 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
     float* red = reinterpret_cast<float*>(lds + kRedOff);
     uint32_t wa[12 * NP];
     if (g + stride >= n_groups) {
-        // the only group of this workgroup
-        load_direct<NP>(wa, a, g, w, lane);
+        // the only group of this workgroup: its stage overlays the partial
+        // tiles, which are written only after the stage has been read; the
+        // LUT loads go first so the table build does not wait for the weights
+        char* stage1 = lds + kRedOff;
         stage_luts<nt>(a, lds, 0, tid);
+        stage_group<NW, NP>(a, g, stage1, w, lane);
         lds_barrier();
         build_table(lds, 0, 0, w, nw, lane);
-        lds_barrier();
+        __builtin_amdgcn_s_waitcnt(0x0F70);            // this wave's staging loads landed
+        lds_barrier();                                 // every wave's; table ready
+        read_group<NW, NP>(wa, stage1, w, lane);
+        lds_barrier();                                 // the stage is read: the partial tiles may overwrite it
         float16_t c = float16_t{};
         group_mfma<NP>(c, wa, xb, lds, 0u);
 #pragma unroll
@@ -367,15 +357,17 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
     GemmArgs a{y, w, lut, x, batch, out_dim, in_dim, ldw, ldx, accumulate,
                (long)in_dim * 3 / 4, (long)in_dim, sy};
     const int n_groups = out_dim / 32;
-    // one group per workgroup once the split already gives 2 units per CU,
-    // else a grid-stride walk over the groups (prefetching the next one)
+    // a grid-stride walk over the groups with about one workgroup per CU in
+    // all: each workgroup loads its window of the inputs once for all its
+    // groups (a split launch has nsplit column slices of the grid)
     int grid = n_groups;
-    if (nsplit == 1 && grid > dev->num_cus) grid = dev->num_cus;
-    // a workgroup with one group loads its weights directly (no stage)
-    const int stage_bytes = grid == n_groups ? 0
-                            : np == 2       ? (32 * (waves * 192 / 16 + 1) + 63) / 64 * 1024
-                                            : (32 * (waves * 96 / 16 + 1) + 63) / 64 * 1024;
-    const size_t lds = (size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float) + stage_bytes;
+    const int per_slice = std::max(1, dev->num_cus / nsplit);
+    if (grid > per_slice) grid = per_slice;
+    // a workgroup with one group overlays its stage on the partial tiles
+    const size_t red_bytes = (size_t)waves * 16 * kRedRow * sizeof(float);
+    const size_t stage_bytes = np == 2 ? (32 * (waves * 192 / 16 + 1) + 63) / 64 * 1024
+                                       : (32 * (waves * 96 / 16 + 1) + 63) / 64 * 1024;
+    const size_t lds = (size_t)kRedOff + (grid == n_groups ? std::max(red_bytes, stage_bytes) : red_bytes + stage_bytes);
     using K = void (*)(GemmArgs);
 #define ANELM_K2(A) {nullptr, lut6_gemm_kernel<2, 1, A>, lut6_gemm_kernel<2, 2, A>, lut6_gemm_kernel<2, 3, A>,     \
                      lut6_gemm_kernel<2, 4, A>, lut6_gemm_kernel<2, 5, A>, lut6_gemm_kernel<2, 6, A>,              \
@@ -395,9 +387,7 @@ int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, 
     // the attribute covers the staged size (the larger of the two per kernel)
     static bool attr_set[2][2][16] = {};
     if (!attr_set[acc][np - 1][waves]) {
-        const int full = (int)((size_t)kRedOff + (size_t)waves * 16 * kRedRow * sizeof(float) +
-                               (np == 2 ? (32 * (waves * 192 / 16 + 1) + 63) / 64 * 1024
-                                        : (32 * (waves * 96 / 16 + 1) + 63) / 64 * 1024));
+        const int full = (int)((size_t)kRedOff + red_bytes + stage_bytes);
         ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kp), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       full));
         attr_set[acc][np - 1][waves] = true;
