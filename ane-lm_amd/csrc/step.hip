@@ -124,8 +124,6 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
                       "hybrid_step: DeltaNet layer %d needs the conv ring (kernel %d, pos %d)", i,
                       dims->conv_kernel, L.conv_pos);
     }
-    ANELM_REQUIRE(!(any_proj && (mode & ANELM_STEP_PERSISTENT)),
-                  "hybrid_step: the persistent step runs core + FFN layers only (no projections)");
     auto* s = new anelm_hybrid_step();
     s->dims = *dims;
     s->layers.assign(layers, layers + n_layers);

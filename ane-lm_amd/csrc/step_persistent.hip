@@ -14,8 +14,10 @@
 // Phase order is the model's dependency chain, per layer L:
 //   core(L) -> barrier -> gate/up(L) -> barrier -> down(L) -> barrier -> core(L+1)
 // where an attention core is two phases, the key splits and the merge of their
-// records, with a barrier between them (the projections around the cores are
-// not part of the step; the chain keeps the order they would impose).
+// records, with a barrier between them (step_kernel: the projections around
+// the cores are not part of the step; the chain keeps the order they would
+// impose).  step_kernel_proj runs complete layers: first projection -> core
+// -> o_proj -> gate/up -> down, a barrier after each.
 //
 // Workgroup = 10 compute waves + 1 control wave.  Compute waves only stream
 // bulk data (weights, KV rows, state) and compute.  The control wave does all
@@ -124,6 +126,20 @@ struct PLayer {
     const uint16_t* lut[3];
 };
 
+// Complete layers (step_kernel_proj): the projections around the core (the
+// layer's q_gate / k / v then point into proj, written by the same launch).
+struct PProj {
+    const float* in_norm_w;
+    const uint8_t* first_w;
+    const uint16_t* first_lut;
+    const uint8_t* o_w;
+    const uint16_t* o_lut;
+    float* proj;
+    float* conv_state;                // DeltaNet [qkv][3] ring
+    const float* conv_w;              // DeltaNet [qkv][4]
+    int conv_pos;                     // ring slot of the step
+};
+
 struct PArgs {
     const PLayer* __restrict__ layers;
     int n_layers;
@@ -141,6 +157,13 @@ struct PArgs {
     unsigned long long* trace;        // [grid][kMaxPhases + 1][kTrEv] (trace build), else null
     const float* rope_tab;            // [rope_rows][2 rot_pairs]: cos then sin of position row
     int rope_rows;
+    // complete layers: first projection (out rows per kind, rows per
+    // workgroup) and o_proj geometry; qkv = DeltaNet conv channels
+    int f_C, f_P, f_RP, f_rows_dn, f_rows_att, f_out_dn, f_out_att;
+    int o_C, o_P, o_RP, o_rows, o_in;
+    int qkv;
+    const PProj* __restrict__ projs;  // [n_layers] (complete layers), else null
+    float* yraw;                      // [o_in] complete layers: a gated DeltaNet core's raw outputs
 };
 
 // Trace events of phase p (p = 3*layer + {0 core, 1 gate/up, 2 down}):
@@ -196,9 +219,11 @@ __device__ __forceinline__ int opaque(int v) {
 #if defined(__HIP_DEVICE_COMPILE__)
 typedef const __attribute__((address_space(4))) PArgs CArgs;
 typedef const __attribute__((address_space(4))) PLayer CLayer;
+typedef const __attribute__((address_space(4))) PProj CProj;
 #else
 typedef const PArgs CArgs;
 typedef const PLayer CLayer;
+typedef const PProj CProj;
 #endif
 __device__ __forceinline__ CArgs* opaque_args(CArgs* p) {
     asm volatile("" : "+s"(p));
@@ -465,13 +490,17 @@ __device__ __forceinline__ void half_sum8(float (&v)[8], int lane) {
 // Compute waves: dot products of the prefetched rows against the staged fp16
 // x pairs; per-half-wave row sums into LDS red[mt][m][hw] (hw = half-wave of
 // the matrix's waves), reduced 8 instructions at a time.
-template <int NI, int NA>
+// ROWLUT: the RP rows of an instruction may straddle a 32-row LUT group (a
+// workgroup row block that does not start on a multiple of RP): each lane
+// takes the table of its own row.
+template <int NI, int NA, bool ROWLUT = false>
 __device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const Buf<8 * NA>& d, const GemvGeo& q,
                                              int n_mat, int wave, int lane, char* lds) {
     if (wave >= n_mat * q.P || q.nrows <= 0) return;
     const int mt = wave / q.P, wl = wave - mt * q.P;
     const int g = 64 * wl + lane;
     const int pos = g % q.C;
+    const int drow = ROWLUT ? g / q.C : 0;   // the lane's row within an instruction's RP rows
     const u32x4* xs = reinterpret_cast<const u32x4*>(lds + kLdsXs);
     const u32x4 x0 = xs[2 * pos], x1 = xs[2 * pos + 1];
     const uint32_t xh[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -488,7 +517,7 @@ __device__ __forceinline__ void gemv_compute(const Buf<3 * NI>& b, const Buf<8 *
                                        d.v[8 * m + 4], d.v[8 * m + 5], d.v[8 * m + 6], d.v[8 * m + 7]};
                 part[j] = pairs_dot(p, xh);
             } else if (m < NI) {
-                const int gi = ((q.R0 + q.RP * m) >> 5) - q.g0;
+                const int gi = min(((q.R0 + q.RP * m + drow) >> 5) - q.g0, 2);   // rows past the block load zeros
                 const uint32_t tb = (uint32_t)(kLdsTab + (mt * 3 + gi) * 16384);
                 part[j] = chunk_dot(lds, tb, b.v[3 * m], b.v[3 * m + 1], b.v[3 * m + 2], xh);
                 __builtin_amdgcn_sched_barrier(0);
@@ -583,16 +612,28 @@ struct AttnStage {
     float k[4], v[4], qw[4], kw[4];
     float cs, sn;
 };
+// COH: q_gate, k and v were written by this launch (the first projection of
+// a complete layer): device-coherent loads.
+template <bool COH = false>
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+    if constexpr (COH) {
+        const f32x4 t = ld4_sc(rsrc(p, 16u), 0);
+        return make_float4(t.x, t.y, t.z, t.w);
+    } else {
+        return *reinterpret_cast<const float4*>(p);
+    }
+}
+template <bool COH = false>
 __device__ __forceinline__ void attn_stage_load(const PArgs& a, const PLayer& L, int lane, AttnStage& r) {
     const int kvh = blockIdx.x / a.splits;
     if (kvh >= a.Hkv) return;
 #pragma unroll
     for (int g = 0; g < kAttnG; g++) {
-        const float4 t = *reinterpret_cast<const float4*>(L.q_gate + (size_t)(kvh * kAttnG + g) * 2 * kAttnD + 4 * lane);
+        const float4 t = ld_f4<COH>(L.q_gate + (size_t)(kvh * kAttnG + g) * 2 * kAttnD + 4 * lane);
         r.q[g][0] = t.x; r.q[g][1] = t.y; r.q[g][2] = t.z; r.q[g][3] = t.w;
     }
-    const float4 k = *reinterpret_cast<const float4*>(L.k + (size_t)kvh * kAttnD + 4 * lane);
-    const float4 v = *reinterpret_cast<const float4*>(L.v + (size_t)kvh * kAttnD + 4 * lane);
+    const float4 k = ld_f4<COH>(L.k + (size_t)kvh * kAttnD + 4 * lane);
+    const float4 v = ld_f4<COH>(L.v + (size_t)kvh * kAttnD + 4 * lane);
     const float4 qw = *reinterpret_cast<const float4*>(L.q_norm_w + 4 * lane);
     const float4 kw = *reinterpret_cast<const float4*>(L.k_norm_w + 4 * lane);
     r.k[0] = k.x; r.k[1] = k.y; r.k[2] = k.z; r.k[3] = k.w;
@@ -1014,6 +1055,7 @@ struct MergeRegs {
     float m, l, gate_in;
     float o[16];
 };
+template <bool COH = false>
 __device__ __forceinline__ void attn_merge_load(const PArgs& a, const PLayer& L, int lane, MergeRegs& r) {
     const int w = blockIdx.x;
     const int kvh = w / kAttnSplits, rr = w - kvh * kAttnSplits;
@@ -1035,8 +1077,13 @@ __device__ __forceinline__ void attn_merge_load(const PArgs& a, const PLayer& L,
     }
     r.m = ml.x;
     r.l = ml.y;
-    if (lane < 16) r.gate_in = L.q_gate[(size_t)(kvh * kAttnG + g) * 2 * kAttnD + kAttnD + 16 * j + lane];
+    if (lane < 16) {
+        const float* gp = L.q_gate + (size_t)(kvh * kAttnG + g) * 2 * kAttnD + kAttnD + 16 * j + lane;
+        r.gate_in = COH ? ldf_sc(gp) : *gp;
+    }
 }
+// COH: the merged output is read by this launch (o_proj): device-coherent store.
+template <bool COH = false>
 __device__ __forceinline__ void attn_merge_fin(const PArgs& a, const PLayer& L, int lane, MergeRegs& r) {
     const int w = blockIdx.x;
     const int kvh = w / kAttnSplits, rr = w - kvh * kAttnSplits;
@@ -1057,7 +1104,101 @@ __device__ __forceinline__ void attn_merge_fin(const PArgs& a, const PLayer& L, 
     if (lane < 16) {
         y = y / Ls;
         y = y / (1.0f + expf(-r.gate_in));
-        L.core_out[(size_t)hq * kAttnD + 16 * j + lane] = y;
+        if constexpr (COH) stf_sc(L.core_out + (size_t)hq * kAttnD + 16 * j + lane, y);
+        else L.core_out[(size_t)hq * kAttnD + 16 * j + lane] = y;
+    }
+}
+
+// ============================================================ complete layers
+// Control wave, after the barrier that follows a DeltaNet layer's first
+// projection: this slab's core inputs from the projection through the conv
+// ring and SiLU (models/llm/qwen3_5.cpp:867-875; conv1d_update,
+// core/cpu_ops.cpp:89-129: y = sum_j ring[(pos + j) % 3] w_j + x w_3), a and
+// b for the gates (:853-860), then the norms and gates of dn_stage_fin.  The
+// ring itself takes the new inputs in the o_proj phase, once every core has
+// read it (dn_ring_update).
+__device__ __forceinline__ float dn_conv_silu(const PProj& L, int ch) {
+    const int pos = L.conv_pos;
+    const int i1 = pos == 2 ? 0 : pos + 1, i2 = pos == 0 ? 2 : pos - 1;
+    const float xn = ldf_sc(L.proj + ch);
+    const float* rs = L.conv_state + (size_t)ch * 3;
+    const float* w = L.conv_w + (size_t)ch * 4;
+    float sum = 0.f;
+    sum += rs[pos] * w[0];
+    sum += rs[i1] * w[1];
+    sum += rs[i2] * w[2];
+    const float y = sum + xn * w[3];
+    return y / (1.0f + expf(-y));
+}
+__device__ void dn_stage_proj(const PArgs& a, const PLayer& L, const PProj& P, int lane, char* lds) {
+    const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
+    if (hd >= a.Hv) return;
+    const int kh = hd / (a.Hv / a.Hk);
+    DnStage r;
+    r.q0 = dn_conv_silu(P, kh * kDnD + lane);
+    r.q1 = dn_conv_silu(P, kh * kDnD + 64 + lane);
+    r.k0 = dn_conv_silu(P, (a.Hk + kh) * kDnD + lane);
+    r.k1 = dn_conv_silu(P, (a.Hk + kh) * kDnD + 64 + lane);
+    r.vj = dn_conv_silu(P, 2 * a.Hk * kDnD + hd * kDnD + kDnCols * c + (lane & (kDnCols - 1)));
+    const float* ab = P.proj + a.qkv + (size_t)a.Hv * kDnD;
+    r.av = ldf_sc(ab + hd);
+    r.b = ldf_sc(ab + a.Hv + hd);
+    r.dt = L.dn_dt_bias[hd];
+    r.A = L.dn_A[hd];
+    dn_stage_fin(a, L, lane, lds, r);
+}
+// Control wave of every workgroup, in the o_proj phase: the conv ring slot
+// of the step takes its new inputs (channels blockIdx.x * 64 + lane + k *
+// grid * 64).
+__device__ __forceinline__ void dn_ring_update(const PArgs& a, const PProj& L, int lane) {
+    for (int ch = blockIdx.x * 64 + lane; ch < a.qkv; ch += gridDim.x * 64)
+        L.conv_state[(size_t)ch * 3 + L.conv_pos] = ldf_sc(L.proj + ch);
+}
+
+// Control wave, o_proj input staging: the core outputs as fp16 pairs in xs.
+// DeltaNet with the gated norm: rmsnorm_gated (core/cpu_ops.cpp:32-38,
+// qwen3_5.cpp:902-908, eps 1e-6) of the raw outputs, the head's sum of
+// squares from its eight slabs; otherwise the outputs as they are.
+__device__ void stage_o(const PArgs& a, const PLayer& L, const PProj& P, bool dn, bool gated, int lane, char* lds) {
+    float* inv = reinterpret_cast<float*>(lds + kLdsMisc + 12288);   // [Hv]
+    if (gated) {
+        for (int hd = lane; hd < a.Hv; hd += 64) {
+            float ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < kDnSlabs; k++) ss += ldf_sc(a.dnss + hd * kDnSlabs + k);
+            inv[hd] = 1.0f / sqrtf(ss / (float)kDnD + 1e-6f);
+        }
+    }
+    // a DeltaNet core's raw outputs (gated) or the merged attention outputs
+    const __amdgpu_buffer_rsrc_t ry = rsrc(dn ? a.yraw : L.core_out, (uint32_t)(a.o_in * 4));
+    const __amdgpu_buffer_rsrc_t rz = rsrc(P.proj + a.qkv, (uint32_t)(a.o_in * 4));
+    u32x2* xs = reinterpret_cast<u32x2*>(lds + kLdsXs);
+    // a gated DeltaNet core's outputs also go to core_out, one slice per
+    // workgroup (they are read after the launch only)
+    const int per = (a.o_in / 4 + (int)gridDim.x - 1) / (int)gridDim.x;
+    for (int e4 = lane; e4 < a.o_in / 4; e4 += 64) {
+        const f32x4 y = ld4_sc(ry, e4 * 16);
+        float o[4] = {y.x, y.y, y.z, y.w};
+        if (gated) {
+            const f32x4 z = ld4_sc(rz, e4 * 16);
+            const float zz[4] = {z.x, z.y, z.z, z.w};
+            const int e = 4 * e4, hd = e / kDnD;
+            const float iv = inv[hd];
+            const float4 w = *reinterpret_cast<const float4*>(L.dn_norm_w + (e % kDnD));
+            const float ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = (o[i] * iv) * ww[i];
+                v = v / (1.0f + expf(-zz[i]));
+                o[i] = v * zz[i];
+            }
+            if (e4 / per == (int)blockIdx.x)
+                *reinterpret_cast<float4*>(L.core_out + (size_t)4 * e4) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+        u32x2 pr;
+        pr.x = pack_h2(o[0], o[1]);
+        pr.y = pack_h2(o[2], o[3]);
+        xs[e4] = pr;
     }
 }
 
@@ -1417,6 +1558,288 @@ __device__ __forceinline__ bool run_layer(CArgs* pa, int l, BC& core_buf, BN& ne
     return true;
 }
 
+// One complete layer (models/llm/qwen3_5.cpp:1287-1354): five phases, each
+// separated from the next by a grid barrier --
+//   first projection: proj = first_w rmsnorm(x, in_norm_w);
+//   core: DeltaNet through the conv ring from proj, or the attention key
+//         splits over q_gate | k | v in proj (then the merge phase);
+//   o_proj: x += o_w core_out (the gated norm of a DeltaNet core applied as
+//         its outputs are staged; the conv ring takes the step's inputs);
+//   gate/up and down: the SwiGLU FFN with its norm and residual.
+// Every GEMV phase's weights and LUTs are requested when the previous phase
+// arrives at its barrier, and its pair tables are built while that barrier
+// resolves; the control wave stages the phase's input after the release.
+// fb / flr carry this layer's first-projection weights (requested by the
+// previous layer's down phase, or at kernel entry), and receive the next
+// layer's.  Returns false on abort.
+template <int KIND, int NIG, int NID, int NIF, int NIO, int NKJ, int JH, int JI, class BC>
+__device__ __forceinline__ bool run_layer_proj(CArgs* pa, int l, BC& core_buf, Buf<3 * NIF>& fb, LutRegs& flr,
+                                               int wave, int lane, char* lds) {
+    CArgs* ap = opaque_args(pa);
+    const PArgs a = *ap;
+    CLayer* layers = (CLayer*)a.layers;
+    const PLayer L = layers[l];
+    const PProj P = ((CProj*)a.projs)[l];
+    int* ctl = ctl_ints(lds);
+    int ln = opaque(lane);
+    const int pb = 5 * l;   // first, core, o_proj, gate/up, down
+    const int pm = 5 * a.n_layers + l / 4;   // attention merge
+    Buf<0> nd;
+    // ------------------------------------------------ first projection
+    const GemvGeo fq = gemv_geo(a.f_C, a.f_P, a.f_RP, KIND == kATT ? a.f_rows_att : a.f_rows_dn,
+                                KIND == kATT ? a.f_out_att : a.f_out_dn);
+    gemv_tables(flr, fq, 1, wave, ln, lds, ctl + 11, fq.P * (l + 1));
+    if (wave == kCtl) {
+        const int okw = l > 0 ? (int)ctl_wait(a, pb - 1, ln) : 1;
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            stage_x_load<JH>(a, ln, lds);
+            stage_w<JH>(a, P.in_norm_w, ln, lds);
+            stage_x_fin<JH>(a, ln, lds);
+        }
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    ln = opaque(lane);
+    gemv_compute<NIF, 0, true>(fb, nd, fq, 1, wave, ln, lds);
+    wg_sync();
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        if (ln < fq.nrows) stf_sc(P.proj + fq.R0 + ln, gemv_row_sum<NIF>(fq, 0, ln, lds));
+        ctl_arrive(a, pb, ln, true);
+    }
+    wg_sync();   // the bulk loads below queue behind the arrival
+    // ------------------------------------------------ core
+    const GemvGeo oq = gemv_geo(a.o_C, a.o_P, a.o_RP, a.o_rows, a.H);
+    Buf<3 * NIO> ob;
+    LutRegs olr;
+    ln = opaque(lane);
+    if constexpr (KIND == kDN) dn_prefetch(core_buf, a, L, wave, ln);
+    else attn_prefetch<NKJ>(core_buf, a, L, wave, ln, lds);
+    {
+        const uint8_t* const OW[2] = {P.o_w, P.o_w};
+        const uint16_t* const OL[2] = {P.o_lut, P.o_lut};
+        gemv_issue<NIO, 0, NIO, true>(ob, olr, oq, OW, OL, 1, wave, ln);
+    }
+    if (wave == kCtl) {
+        const int okw = ctl_wait(a, pb, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            if constexpr (KIND == kDN) {
+                dn_stage_proj(a, L, P, ln, lds);
+            } else {
+                AttnStage as;
+                attn_stage_load<true>(a, L, ln, as);
+                attn_stage_fin(a, L, ln, lds, as);
+            }
+        }
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    ln = opaque(lane);
+    if constexpr (KIND == kATT) {
+        attn_compute<NKJ>(core_buf, a, L, wave, ln, lds, l);
+        vm_drain();   // this thread's part of the split record has been stored
+    } else {
+        const float y = dn_compute(core_buf, a, L, wave, ln, lds, pb + 1);
+        if (wave == kCtl) {
+            // the raw outputs for the o_proj staging (device-coherent); the
+            // gated outputs go to core_out as they are staged
+            const int hd = blockIdx.x / kDnSlabs, c = blockIdx.x % kDnSlabs;
+            if (hd < a.Hv && ln < kDnCols) stf_sc(a.yraw + (size_t)hd * kDnD + kDnCols * c + ln, y);
+        }
+    }
+    wg_sync();
+    ln = opaque(lane);
+    if (wave == kCtl) ctl_arrive(a, pb + 1, ln, KIND == kDN);
+    wg_sync();
+    ln = opaque(lane);
+    // o_proj pair tables while the core's barrier resolves (the core has
+    // left the table region free); an attention layer's merge meanwhile
+    gemv_tables(olr, oq, 1, wave, ln, lds, ctl + 12, oq.P * (l + 1));
+    if constexpr (KIND == kATT) {
+        if (wave == kCtl) {
+            const int okw = ctl_wait(a, pb + 1, ln);
+            if (ln == 0) ctl[0] = okw;
+            if (okw) {
+                MergeRegs mr;
+                attn_merge_load<true>(a, L, ln, mr);
+                attn_merge_fin<true>(a, L, ln, mr);
+                ctl_arrive(a, pm, ln, true);
+            }
+        }
+        wg_sync();
+        if (!ctl[0]) return false;
+    }
+    // ------------------------------------------------ o_proj + residual
+    float x_old = 0.f;
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        const int okw = ctl_wait(a, KIND == kATT ? pm : pb + 1, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            if constexpr (KIND == kDN) dn_ring_update(a, P, ln);
+            stage_o(a, L, P, KIND == kDN, KIND == kDN && (L.dn_flags & ANELM_DN_GATED_NORM) != 0, ln, lds);
+            if (ln < oq.nrows) x_old = ldf_sc(a.x + oq.R0 + ln);
+        }
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    ln = opaque(lane);
+    gemv_compute<NIO, 0>(ob, nd, oq, 1, wave, ln, lds);
+    wg_sync();
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        if (ln < oq.nrows) stf_sc(a.x + oq.R0 + ln, x_old + gemv_row_sum<NIO>(oq, 0, ln, lds));
+        ctl_arrive(a, pb + 2, ln, true);
+    }
+    wg_sync();
+    // ------------------------------------------------ gate/up
+    const GemvGeo gu = gemv_geo(a.gu_C, a.gu_P, a.gu_RP, a.gu_rows, a.I);
+    Buf<3 * NIG> gb;
+    LutRegs glr;
+    ln = opaque(lane);
+    {
+        const uint8_t* const GW[2] = {L.w[0], L.w[1]};
+        const uint16_t* const GLU[2] = {L.lut[0], L.lut[1]};
+        gemv_issue<NIG, 0, NIG, true>(gb, glr, gu, GW, GLU, 2, wave, ln);
+        gemv_tables(glr, gu, 2, wave, ln, lds, ctl + 8, gu.P * (l + 1));
+    }
+    if (wave == kCtl) {
+        const int okw = ctl_wait(a, pb + 2, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            stage_x_load<JH>(a, ln, lds);
+            stage_w<JH>(a, L.ffn_norm_w, ln, lds);
+            stage_x_fin<JH>(a, ln, lds);
+        }
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    ln = opaque(lane);
+    gemv_compute<NIG, 0>(gb, nd, gu, 2, wave, ln, lds);
+    wg_sync();
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        // h = silu(g) * u for this workgroup's rows, published as fp16 pairs
+        float hv = 0.f;
+        if (ln < gu.nrows) {
+            const float g = gemv_row_sum<NIG>(gu, 0, ln, lds);
+            const float u = gemv_row_sum<NIG>(gu, 1, ln, lds);
+            hv = (g / (1.0f + expf(-g))) * u;
+        }
+        const float hn = __shfl_down(hv, 1, 64);
+        if (ln < gu.nrows && (ln & 1) == 0)
+            st_sc(reinterpret_cast<unsigned*>(a.h) + ((gu.R0 + ln) >> 1), pack_h2(hv, hn));
+        ctl_arrive(a, pb + 3, ln, true);
+    }
+    wg_sync();
+    // ------------------------------------------------ down + residual
+    const GemvGeo dg = gemv_geo(a.d_C, a.d_P, a.d_RP, a.d_rows, a.H);
+    Buf<3 * NID> db;
+    LutRegs dlr;
+    ln = opaque(lane);
+    {
+        const uint8_t* const W[2] = {L.w[2], L.w[2]};
+        const uint16_t* const LU[2] = {L.lut[2], L.lut[2]};
+        gemv_issue<NID, 0, NID, true>(db, dlr, dg, W, LU, 1, wave, ln);
+        gemv_tables(dlr, dg, 1, wave, ln, lds, ctl + 10, dg.P * (l + 1));
+    }
+    float xo = 0.f;
+    if (wave == kCtl) {
+        const int okw = ctl_wait(a, pb + 3, ln);
+        if (ln == 0) ctl[0] = okw;
+        if (okw) {
+            stage_h_load<JI>(a, ln, lds);
+            if (ln < dg.nrows) xo = ldf_sc(a.x + dg.R0 + ln);
+            vm_drain();   // h has landed in LDS
+        }
+    }
+    wg_sync();
+    if (!ctl[0]) return false;
+    ln = opaque(lane);
+    gemv_compute<NID, 0>(db, nd, dg, 1, wave, ln, lds);
+    wg_sync();
+    ln = opaque(lane);
+    if (wave == kCtl) {
+        if (ln < dg.nrows) stf_sc(a.x + dg.R0 + ln, xo + gemv_row_sum<NID>(dg, 0, ln, lds));
+        ctl_arrive(a, pb + 4, ln, true);
+    }
+    wg_sync();   // the bulk loads below queue behind the arrival
+    // the next layer's first-projection weights and LUTs
+    ln = opaque(lane);
+    if (l + 1 < a.n_layers) {
+        const bool natt = (l + 2) % 4 == 0;   // layer l + 1 is full attention (qwen3_5.cpp:64-71)
+        const PProj Pn = ((CProj*)a.projs)[l + 1];
+        const GemvGeo fn = gemv_geo(a.f_C, a.f_P, a.f_RP, natt ? a.f_rows_att : a.f_rows_dn,
+                                    natt ? a.f_out_att : a.f_out_dn);
+        const uint8_t* const FW[2] = {Pn.first_w, Pn.first_w};
+        const uint16_t* const FL[2] = {Pn.first_lut, Pn.first_lut};
+        gemv_issue<NIF, 0, NIF, true>(fb, flr, fn, FW, FL, 1, wave, ln);
+    }
+    return true;
+}
+
+// End of a launch: the last workgroup out clears the barrier words of the np
+// phases used (they are zero again for the next launch) and, when advancing,
+// writes the next step's ring descriptors.
+__device__ __forceinline__ void step_finish(const PArgs& a, int tid, int* ctl, int advance, int np, bool proj) {
+    vm_drain();
+    wg_sync();
+    if (tid == 0) ctl[3] = add_sc(a.sync + kFinOff, 1u) == gridDim.x - 1u;
+    wg_sync();
+    if (ctl[3]) {
+        // last workgroup out: every other one has finished all sync accesses
+        // (a timed-out wait stored the abort flag before its workgroup's
+        // drain and arrival here)
+        const bool aborted = ld_sc(a.sync + kAbortOff) != 0u;
+        for (int i = tid; i < np * (2 * kNG + 1); i += kNT) {
+            const int p = i / (2 * kNG + 1), k = i - p * (2 * kNG + 1);
+            if (k < kNG) st_sc(a.sync + kGrpOff + ((long)p * kNG + k) * kPad, 0u);
+            else if (k < 2 * kNG) st_sc(a.sync + kRelOff + ((long)p * kNG + (k - kNG)) * kPad, 0u);
+            else st_sc(a.sync + kRootOff + (long)p * kPad, 0u);
+        }
+        if (tid == 0) {
+            st_sc(a.sync + kFinOff, 0u);
+            st_sc(a.sync + kAbortOff, 0u);
+        }
+        if (advance && !aborted) {
+            // the next step's descriptors: every attention ring and position
+            // moves one token forward (the KVCache bookkeeping of
+            // qwen3_5.cpp:973-983), so consecutive launches need no host
+            // update; the host mirrors the same arithmetic.  An aborted step
+            // does not advance: the next launch redoes its token.
+            PLayer* lw = const_cast<PLayer*>(a.layers);
+            for (int i = tid; i < a.n_layers; i += kNT) {
+                if (lw[i].kind != ANELM_LAYER_ATTENTION) continue;
+                int start = lw[i].ring_start, len = lw[i].ring_len, slot;
+                if (len < a.cap) {
+                    slot = start + len;
+                    if (slot >= a.cap) slot -= a.cap;
+                    len++;
+                } else {
+                    slot = start;
+                    start++;
+                    if (start >= a.cap) start = 0;
+                }
+                const int pos = lw[i].pos + 1;
+                lw[i].ring_start = start;
+                lw[i].ring_len = len;
+                lw[i].slot = slot;
+                lw[i].pos = pos;
+                lw[i].rope = a.rope_tab + (size_t)pos * 2 * a.rot_pairs;
+            }
+            // complete layers: every DeltaNet conv ring moves one slot
+            if (proj) {
+                PProj* pw = const_cast<PProj*>(a.projs);
+                for (int i = tid; i < a.n_layers; i += kNT)
+                    if (lw[i].kind != ANELM_LAYER_ATTENTION) pw[i].conv_pos = pw[i].conv_pos == 2 ? 0 : pw[i].conv_pos + 1;
+            }
+        }
+        vm_drain();
+    }
+}
+
 // NIG / NID: GEMV instructions per wave for gate/up and down; NKJ: key
 // slots per attention lane; JH = H/256, JI = I/512 (fp16 pairs / 4 per load).
 // Layer pattern: groups of 3 DeltaNet layers and 1 full-attention layer
@@ -1483,55 +1906,48 @@ __global__ __launch_bounds__(kNT, 1) void step_kernel(const PArgs* __restrict__ 
     }
     // ------------------------------------------------------------ finish
     trace_stamp(a, kMaxPhases, 1, tid == 0);
-    vm_drain();
-    wg_sync();
-    if (tid == 0) ctl[3] = add_sc(a.sync + kFinOff, 1u) == gridDim.x - 1u;
-    wg_sync();
-    if (ctl[3]) {
-        // last workgroup out: every other one has finished all sync accesses
-        // (a timed-out wait stored the abort flag before its workgroup's
-        // drain and arrival here)
-        const bool aborted = ld_sc(a.sync + kAbortOff) != 0u;
-        const int np = 3 * a.n_layers + a.n_layers / 4;
-        for (int i = tid; i < np * (2 * kNG + 1); i += kNT) {
-            const int p = i / (2 * kNG + 1), k = i - p * (2 * kNG + 1);
-            if (k < kNG) st_sc(a.sync + kGrpOff + ((long)p * kNG + k) * kPad, 0u);
-            else if (k < 2 * kNG) st_sc(a.sync + kRelOff + ((long)p * kNG + (k - kNG)) * kPad, 0u);
-            else st_sc(a.sync + kRootOff + (long)p * kPad, 0u);
-        }
-        if (tid == 0) {
-            st_sc(a.sync + kFinOff, 0u);
-            st_sc(a.sync + kAbortOff, 0u);
-        }
-        if (advance && !aborted) {
-            // the next step's descriptors: every attention ring and position
-            // moves one token forward (the KVCache bookkeeping of
-            // qwen3_5.cpp:973-983), so consecutive launches need no host
-            // update; the host mirrors the same arithmetic.  An aborted step
-            // does not advance: the next launch redoes its token.
-            PLayer* lw = const_cast<PLayer*>(a.layers);
-            for (int i = tid; i < a.n_layers; i += kNT) {
-                if (lw[i].kind != ANELM_LAYER_ATTENTION) continue;
-                int start = lw[i].ring_start, len = lw[i].ring_len, slot;
-                if (len < a.cap) {
-                    slot = start + len;
-                    if (slot >= a.cap) slot -= a.cap;
-                    len++;
-                } else {
-                    slot = start;
-                    start++;
-                    if (start >= a.cap) start = 0;
-                }
-                const int pos = lw[i].pos + 1;
-                lw[i].ring_start = start;
-                lw[i].ring_len = len;
-                lw[i].slot = slot;
-                lw[i].pos = pos;
-                lw[i].rope = a.rope_tab + (size_t)pos * 2 * a.rot_pairs;
-            }
-        }
-        vm_drain();
+    step_finish(a, tid, ctl, advance, 3 * a.n_layers + a.n_layers / 4, false);
+}
+
+// The same step over complete layers (projections around every core): five
+// phases per layer (and an attention merge).  NIF / NIO: first-projection and
+// o_proj instructions per wave.
+template <int NIG, int NID, int NKJ, int JH, int JI, int NIF, int NIO>
+__global__ __launch_bounds__(kNT, 1) void step_kernel_proj(const PArgs* __restrict__ gpa, int advance) {
+    CArgs* pa = (CArgs*)gpa;
+    const PArgs a = *pa;
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave == kCtl) __builtin_amdgcn_s_setprio(3);
+    int* ctl = ctl_ints(lds);
+    Buf<kDnBuf> cdn;
+    Buf<4 * NKJ> cat;
+    Buf<3 * NIF> fb;
+    LutRegs flr;
+    if (tid == 0) {
+        ctl[0] = 1;
+        // table-build counters: gate, up, down, first projection, o_proj
+        ctl[8] = ctl[9] = ctl[10] = ctl[11] = ctl[12] = 0;
     }
+    wg_sync();
+    {
+        // layer 0's first-projection weights (layer 0 is a DeltaNet layer)
+            const PProj P0 = ((CProj*)a.projs)[0];
+        const GemvGeo fq = gemv_geo(a.f_C, a.f_P, a.f_RP, a.f_rows_dn, a.f_out_dn);
+        const uint8_t* const FW[2] = {P0.first_w, P0.first_w};
+        const uint16_t* const FL[2] = {P0.first_lut, P0.first_lut};
+        gemv_issue<NIF, 0, NIF, true>(fb, flr, fq, FW, FL, 1, wave, lane);
+    }
+    const int groups = a.n_layers / 4;
+    for (int gr = 0; gr < groups; gr++) {
+        const int l0 = 4 * gr;
+        if (!run_layer_proj<kDN, NIG, NID, NIF, NIO, NKJ, JH, JI>(pa, l0, cdn, fb, flr, wave, lane, lds)) break;
+        if (!run_layer_proj<kDN, NIG, NID, NIF, NIO, NKJ, JH, JI>(pa, l0 + 1, cdn, fb, flr, wave, lane, lds)) break;
+        if (!run_layer_proj<kDN, NIG, NID, NIF, NIO, NKJ, JH, JI>(pa, l0 + 2, cdn, fb, flr, wave, lane, lds)) break;
+        if (!run_layer_proj<kATT, NIG, NID, NIF, NIO, NKJ, JH, JI>(pa, l0 + 3, cat, fb, flr, wave, lane, lds)) break;
+    }
+    step_finish(a, tid, ctl, advance, 5 * a.n_layers + a.n_layers / 4, true);
 }
 
 }  // namespace pk
@@ -1545,6 +1961,10 @@ struct PersistentStep {
     std::vector<pk::PLayer> host_layers;
     std::vector<int> pos;              // per layer (attention): position of the new token
     std::vector<int> start, len;       // per layer ring state BEFORE the step
+    std::vector<int> conv_pos;         // per DeltaNet layer (complete layers): ring slot of the step
+    bool proj = false;                 // complete layers (step_kernel_proj)
+    std::vector<pk::PProj> host_projs;
+    pk::PProj* d_projs = nullptr;
     int cap = 0, rot = 0;
     float theta = 0.f;
     pk::PLayer* d_layers = nullptr;
@@ -1561,6 +1981,20 @@ namespace {
 template <int NIG, int NID, int NKJ, int JH, int JI>
 void* kernel_ptr() {
     return reinterpret_cast<void*>(&pk::step_kernel<NIG, NID, NKJ, JH, JI>);
+}
+template <int NIG, int NID, int NKJ, int JH, int JI, int NIF, int NIO>
+void* kernel_ptr_proj() {
+    return reinterpret_cast<void*>(&pk::step_kernel_proj<NIG, NID, NKJ, JH, JI, NIF, NIO>);
+}
+
+// Geometry of a LUT6 GEMV with in_dim K run by P waves of one matrix: C
+// chunks per row, RP rows per instruction group (64 P lanes = RP rows).
+bool geo_p(int K, int P, int& C, int& RP) {
+    if (K % 512 != 0) return false;
+    C = K / 16;
+    if ((64 * P) % C != 0) return false;
+    RP = 64 * P / C;
+    return true;
 }
 
 // Geometry of a LUT6 GEMV with in_dim K for the persistent kernel: C chunks
@@ -1598,6 +2032,9 @@ void plan_positions(PersistentStep* s) {
         L.pos = s->pos[i];
         L.rope = s->d_rope + (size_t)s->pos[i] * s->rot;
     }
+    if (s->proj)
+        for (int i = 0; i < n; i++)
+            if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) s->host_projs[i].conv_pos = s->conv_pos[i];
 }
 
 // Largest position a launch may reach: the new token of this step, and with
@@ -1642,8 +2079,14 @@ int resync(PersistentStep* s) {
     if (!s->launched) return ANELM_OK;
     std::vector<pk::PLayer> dl(s->host_layers.size());
     ANELM_HIP(hipMemcpy(dl.data(), s->d_layers, dl.size() * sizeof(pk::PLayer), hipMemcpyDeviceToHost));
+    std::vector<pk::PProj> dp(s->proj ? dl.size() : 0);
+    if (s->proj)
+        ANELM_HIP(hipMemcpy(dp.data(), s->d_projs, dp.size() * sizeof(pk::PProj), hipMemcpyDeviceToHost));
     for (size_t i = 0; i < dl.size(); i++) {
-        if (dl[i].kind != ANELM_LAYER_ATTENTION) continue;
+        if (dl[i].kind != ANELM_LAYER_ATTENTION) {
+            if (s->proj) s->conv_pos[i] = dp[i].conv_pos;
+            continue;
+        }
         s->start[i] = dl[i].ring_start;
         s->len[i] = dl[i].ring_len - 1;
         s->pos[i] = dl[i].pos;
@@ -1665,6 +2108,9 @@ int upload(PersistentStep* s, bool advance) {
     plan_positions(s);
     ANELM_HIP(hipMemcpy(s->d_layers, s->host_layers.data(), s->host_layers.size() * sizeof(pk::PLayer),
                         hipMemcpyHostToDevice));
+    if (s->proj)
+        ANELM_HIP(hipMemcpy(s->d_projs, s->host_projs.data(), s->host_projs.size() * sizeof(pk::PProj),
+                            hipMemcpyHostToDevice));
     ANELM_HIP(hipMemcpy(s->d_args, &s->args, sizeof(pk::PArgs), hipMemcpyHostToDevice));
     return ANELM_OK;
 }
@@ -1674,10 +2120,12 @@ int upload(PersistentStep* s, bool advance) {
 void persistent_destroy(PersistentStep* s) {
     if (!s) return;
     if (s->d_layers) (void)hipFree(s->d_layers);
+    if (s->d_projs) (void)hipFree(s->d_projs);
     if (s->d_args) (void)hipFree(s->d_args);
     if (s->d_rope) (void)hipFree(s->d_rope);
     if (s->args.part) (void)hipFree(s->args.part);
     if (s->args.dnss) (void)hipFree(s->args.dnss);
+    if (s->args.yraw) (void)hipFree(s->args.yraw);
     if (s->args.sync) (void)hipFree(s->args.sync);
     if (s->args.trace) (void)hipFree(s->args.trace);
     delete s;
@@ -1690,22 +2138,40 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     ANELM_REQUIRE(n_layers >= 1 && n_layers <= pk::kMaxLayers, "persistent step: %d layers (max %d)",
                   n_layers, pk::kMaxLayers);
     bool any_attn = false;
+    // complete layers (projections around every core) or core + FFN layers
+    const bool proj = layers[0].first_w != nullptr;
     for (int i = 0; i < n_layers; i++) {
         const anelm_hybrid_layer& L = layers[i];
+        ANELM_REQUIRE((L.first_w != nullptr) == proj,
+                      "persistent step: layer %d -- either every layer has projections or none", i);
         // every pointer the kernel reads or writes unconditionally
         const bool ffn = L.ffn_norm_w && L.gate_w && L.gate_lut && L.up_w && L.up_lut && L.down_w && L.down_lut;
         bool core;
         if (L.kind == ANELM_LAYER_ATTENTION) {
             any_attn = true;
-            core = L.q_gate && L.k && L.v && L.k_cache && L.v_cache && L.q_norm_w && L.k_norm_w && L.core_out;
+            core = (proj || (L.q_gate && L.k && L.v)) && L.k_cache && L.v_cache && L.q_norm_w && L.k_norm_w &&
+                   L.core_out;
+        } else if (proj) {
+            core = L.state && L.dn_A && L.dn_dt_bias && L.core_out && L.conv_state && L.conv_w &&
+                   (!(L.dn_flags & ANELM_DN_GATED_NORM) || L.dn_norm_w);
         } else {
             core = L.state && L.dn_q && L.dn_k && L.dn_v && L.dn_a && L.dn_b && L.dn_A && L.dn_dt_bias &&
                    L.core_out && (!(L.dn_flags & ANELM_DN_GATED_NORM) || (L.dn_z && L.dn_norm_w));
         }
+        if (proj && !(L.in_norm_w && L.first_lut && L.o_w && L.o_lut && L.proj))
+            return set_error(ANELM_ENULL, "persistent step: layer %d lacks a projection pointer (the input norm "
+                             "weight is required here)", i);
         if (!ffn || !core)
             return set_error(ANELM_ENULL, "persistent step: layer %d lacks a %s pointer (q/k norm weights are "
                              "required here)", i, ffn ? "core" : "FFN");
     }
+    ANELM_REQUIRE(!proj || d->conv_kernel == 4, "persistent step: conv kernel %d (4 supported)", d->conv_kernel);
+    ANELM_REQUIRE(!proj || 5 * n_layers + n_layers / 4 <= pk::kMaxPhases,
+                  "persistent step: %d complete layers exceed the barrier words", n_layers);
+#if ANELM_STEP_TRACE
+    // the phase timeline covers the core + FFN step only
+    ANELM_REQUIRE(!proj, "step trace: complete layers are not traced");
+#endif
     // a rotary width of 0 would leave the kernel's RoPE row reads without a
     // table row to read
     ANELM_REQUIRE(!any_attn || (d->rot_dim >= 2 && d->rot_dim % 2 == 0 && d->rot_dim <= pk::kAttnD &&
@@ -1776,7 +2242,34 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     // to 8960 keys; smaller caches leave slots past their split empty.
     void* kp = nullptr;
     const int jh = d->hidden / 256, ji = d->inter / 512;
-    if (nkj <= 7) {
+    // complete layers: first projection over 10 waves, o_proj over 8
+    int fC = 0, fRP = 0, oC = 0, oRP = 0, f_rows_dn = 0, f_rows_att = 0, f_out_dn = 0, f_out_att = 0;
+    int o_in = 0, o_rows = 0, nif = 0, nio = 0, qkv = 0;
+    if (proj) {
+        qkv = 2 * d->lin_k_heads * d->lin_dim + d->lin_v_heads * d->lin_dim;
+        f_out_dn = qkv + d->lin_v_heads * d->lin_dim + 2 * d->lin_v_heads;
+        f_out_att = d->n_heads * 2 * d->head_dim + 2 * d->n_kv_heads * d->head_dim;
+        o_in = n_attn ? d->n_heads * d->head_dim : d->lin_v_heads * d->lin_dim;
+        ANELM_REQUIRE(n_attn == 0 || n_attn == n_layers || d->n_heads * d->head_dim == d->lin_v_heads * d->lin_dim,
+                      "persistent step: o_proj inputs differ between the layer kinds (%d, %d)",
+                      d->n_heads * d->head_dim, d->lin_v_heads * d->lin_dim);
+        ANELM_REQUIRE(geo_p(d->hidden, 10, fC, fRP) && geo_p(o_in, 8, oC, oRP) && fC <= 768 && oC <= 768 &&
+                          o_in * 2 <= 24576 && f_out_dn % 32 == 0 && f_out_att % 32 == 0,
+                      "persistent step: projection geometry (hidden %d, o_proj in %d)", d->hidden, o_in);
+        f_rows_dn = (f_out_dn + nwg - 1) / nwg;
+        f_rows_att = (f_out_att + nwg - 1) / nwg;
+        o_rows = d->hidden / nwg;
+        ANELM_REQUIRE(f_rows_dn <= 64 && f_rows_att <= 64 && o_rows % oRP == 0,
+                      "persistent step: projection rows per workgroup %d / %d / %d", f_rows_dn, f_rows_att, o_rows);
+        nif = (std::max(f_rows_dn, f_rows_att) + fRP - 1) / fRP;
+        nio = o_rows / oRP;
+        if (nkj <= 7) {
+            if (nig == 18 && nid == 10 && jh == 10 && ji == 18 && nif == 13 && nio == 5)
+                kp = kernel_ptr_proj<18, 10, 7, 10, 18, 13, 5>();
+            else if (nig == 14 && nid == 2 && jh == 4 && ji == 7 && nif == 4 && nio == 1)
+                kp = kernel_ptr_proj<14, 2, 7, 4, 7, 4, 1>();
+        }
+    } else if (nkj <= 7) {
         if (nig == 18 && nid == 10 && jh == 10 && ji == 18) kp = kernel_ptr<18, 10, 7, 10, 18>();
         else if (nig == 14 && nid == 2 && jh == 4 && ji == 7) {
 #if ANELM_STEP_TRACE
@@ -1790,8 +2283,8 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
         }
     }
     ANELM_REQUIRE(kp != nullptr,
-                  "persistent step: no kernel for this shape (gate/up %d, down %d instructions, %d key slots)",
-                  nig, nid, nkj);
+                  "persistent step: no kernel for this shape (gate/up %d, down %d, first %d, o_proj %d instructions, "
+                  "%d key slots)", nig, nid, nif, nio, nkj);
 
     auto* s = new PersistentStep();
     s->cap = cap;
@@ -1799,15 +2292,20 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     s->theta = d->theta;
     s->grid = nwg;
     s->kernel = reinterpret_cast<void (*)(const pk::PArgs*, int)>(kp);
+    s->proj = proj;
     s->host_layers.resize(n_layers);
+    s->conv_pos.assign(n_layers, 0);
+    s->host_projs.assign(proj ? n_layers : 0, pk::PProj{});
     s->pos.resize(n_layers);
     s->start.resize(n_layers);
     s->len.resize(n_layers);
     hipError_t e = hipMalloc(&s->d_layers, sizeof(pk::PLayer) * n_layers);
+    if (e == hipSuccess && proj) e = hipMalloc(&s->d_projs, sizeof(pk::PProj) * n_layers);
     if (e == hipSuccess) e = hipMalloc(&s->d_args, sizeof(pk::PArgs));
     const size_t rec = (size_t)pk::kAttnG * pk::kAttnRec;
     if (e == hipSuccess) e = hipMalloc(&s->args.part, sizeof(float) * rec * (n_attn ? d->n_kv_heads * splits : 1));
     if (e == hipSuccess) e = hipMalloc(&s->args.dnss, sizeof(float) * (size_t)nwg);
+    if (e == hipSuccess && proj) e = hipMalloc(&s->args.yraw, sizeof(float) * (size_t)o_in);
     if (e == hipSuccess) e = hipMalloc(&s->args.sync, sizeof(unsigned) * pk::kSyncWords);
     if (e == hipSuccess) e = hipMemset(s->args.sync, 0, sizeof(unsigned) * pk::kSyncWords);
 #if ANELM_STEP_TRACE
@@ -1859,6 +2357,27 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
         L.lut[0] = S.gate_lut;
         L.lut[1] = S.up_lut;
         L.lut[2] = S.down_lut;
+        if (proj) {
+            pk::PProj& P = s->host_projs[i];
+            P.in_norm_w = S.in_norm_w;
+            P.first_w = S.first_w;
+            P.first_lut = S.first_lut;
+            P.o_w = S.o_w;
+            P.o_lut = S.o_lut;
+            P.proj = S.proj;
+            P.conv_state = S.conv_state;
+            P.conv_w = S.conv_w;
+            if (S.kind == ANELM_LAYER_ATTENTION) {
+                // the core's inputs are the projection's rows (qwen3_5.cpp:948-950)
+                L.q_gate = S.proj;
+                L.k = S.proj + (size_t)d->n_heads * 2 * d->head_dim;
+                L.v = L.k + (size_t)d->n_kv_heads * d->head_dim;
+            } else {
+                ANELM_REQUIRE(S.conv_pos >= 0 && S.conv_pos < 3, "persistent step: layer %d conv_pos %d", i,
+                              S.conv_pos);
+                s->conv_pos[i] = S.conv_pos;
+            }
+        }
         s->pos[i] = S.pos;
         s->start[i] = S.cache_start;
         s->len[i] = S.cache_len;
@@ -1888,6 +2407,20 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
     a.scale = 1.0f / sqrtf((float)d->head_dim);
     a.Hk = d->lin_k_heads;
     a.Hv = d->lin_v_heads;
+    a.f_C = fC;
+    a.f_P = 10;
+    a.f_RP = fRP;
+    a.f_rows_dn = f_rows_dn;
+    a.f_rows_att = f_rows_att;
+    a.f_out_dn = f_out_dn;
+    a.f_out_att = f_out_att;
+    a.o_C = oC;
+    a.o_P = 8;
+    a.o_RP = oRP;
+    a.o_rows = o_rows;
+    a.o_in = o_in;
+    a.qkv = qkv;
+    a.projs = s->d_projs;
     const int rc = upload(s, true);
     if (rc) {
         persistent_destroy(s);
@@ -1926,7 +2459,10 @@ int persistent_run(PersistentStep* s, bool advance, bool cooperative, hipStream_
         // host mirror of the launch's own advance (no copy, no wait); after
         // an abort it runs ahead of the device until the next resync
         for (size_t i = 0; i < s->host_layers.size(); i++) {
-            if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) continue;
+            if (s->host_layers[i].kind != ANELM_LAYER_ATTENTION) {
+                if (s->proj) s->conv_pos[i] = s->conv_pos[i] == 2 ? 0 : s->conv_pos[i] + 1;
+                continue;
+            }
             s->start[i] = s->host_layers[i].ring_start;
             s->len[i] = s->host_layers[i].ring_len;
             s->pos[i]++;

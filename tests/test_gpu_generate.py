@@ -183,9 +183,7 @@ def test_complete_layers_4b_shape(anelm, orc, dev):
     -- first projections 2560->12352 / 2560->10240, o_proj 4096->2560, FFN
     2560->9216->2560 -- three decode steps; the hidden state after the layer
     loop against the oracle's."""
-    dims = dict(TINY_LM, hidden=QWEN35_4B["hidden"], inter=QWEN35_4B["inter"], n_heads=16, n_kv_heads=4,
-                lin_k_heads=16, lin_v_heads=32, vocab=256, cap=64)
-    m = tiny_lm(2028, dims=dims)
+    m = tiny_lm(2028, dims=_DIMS_4B)
     ref, gpu = OracleLM(orc, m), StepLM(anelm, m, dev)
     try:
         for pos, tok in enumerate((3, 17, 101)):
@@ -194,6 +192,92 @@ def test_complete_layers_4b_shape(anelm, orc, dev):
             assert_close(to_host(logits_gpu), logits_ref, what=f"4B-shape logits at step {pos}")
     finally:
         gpu.close()
+
+
+_DIMS_4B = dict(TINY_LM, hidden=QWEN35_4B["hidden"], inter=QWEN35_4B["inter"], n_heads=16, n_kv_heads=4,
+                lin_k_heads=16, lin_v_heads=32, vocab=256, cap=64)
+_DIMS_08B = dict(TINY_LM, hidden=1024, inter=3584, n_heads=8, n_kv_heads=2, lin_k_heads=16, lin_v_heads=16)
+
+
+def _persistent_lm(anelm, m, dev):
+    gpu = StepLM.__new__(StepLM)
+    try:
+        StepLM.__init__(gpu, anelm, m, dev, mode=anelm.STEP_PERSISTENT)
+    except Exception as e:   # noqa: BLE001 -- a device without 256 CUs
+        pytest.skip(f"persistent step unsupported here: {e}")
+    return gpu
+
+
+def test_complete_layers_persistent_4b_shape(anelm, orc, dev):
+    """The complete layers as ONE persistent launch per step (first
+    projection, conv ring + DeltaNet core or attention core with its merge,
+    o_proj + residual, FFN: five grid-barrier phases per layer) at the
+    Qwen3.5-4B shape, four layers, three decode steps: the logits against
+    the oracle's Qwen35Model::forward."""
+    m = tiny_lm(2028, dims=_DIMS_4B)
+    ref, gpu = OracleLM(orc, m), _persistent_lm(anelm, m, dev)
+    try:
+        for pos, tok in enumerate((3, 17, 101)):
+            _, logits_ref = ref.step(tok, pos)
+            logits_gpu = gpu.forward(tok)
+            assert_close(to_host(logits_gpu), logits_ref, what=f"persistent 4B-shape logits at step {pos}")
+        st = ctypes.c_int(-1)
+        anelm.call("anelm_hybrid_step_status", gpu.handle, ctypes.byref(st))
+        assert st.value == 0, "a grid barrier timed out"
+    finally:
+        gpu.close()
+
+
+def test_complete_layers_persistent_matches_eager(anelm, dev):
+    """Eight complete layers at the 4B shape, five decode steps (the conv
+    rings cycle past their 3 slots, the KV rings fill): the persistent step's
+    hidden state, caches, conv rings and DeltaNet states against the eager
+    executor's."""
+    m = tiny_lm(2032, dims=dict(_DIMS_4B, layers=8), lut_std=0.005)
+    a = StepLM(anelm, m, dev, mode=anelm.STEP_EAGER)
+    b = _persistent_lm(anelm, m, dev)
+    try:
+        for pos, tok in enumerate((5, 9, 200, 31, 77)):
+            xa = to_host(a.forward(tok))
+            xb = to_host(b.forward(tok))
+            torch.cuda.synchronize()
+            assert_close(xb, xa, what=f"step {pos} logits")
+            for i, (ta, tb) in enumerate(zip(a.keep, b.keep)):
+                if ta.dtype == torch.float16:
+                    assert_close(to_host(tb.float()), to_host(ta.float()), what=f"step {pos} tensor {i}")
+                elif ta.dtype == torch.float32 and ta.numel() < 5_000_000:
+                    assert_close(to_host(tb), to_host(ta), rel=1e-3, max_abs=2e-2, what=f"step {pos} tensor {i}")
+    finally:
+        a.close()
+        b.close()
+
+
+def test_complete_layers_persistent_greedy_08b_shape(anelm, orc, dev):
+    """Greedy decoding through the persistent complete step at the
+    reference's default Qwen3.5-0.8B shape (hidden 1024, inter 3584, 8 q /
+    2 kv heads, 16 DeltaNet heads), four layers: two independent loops, 32
+    tokens, identical (the seed's smallest top-2 gap is checked first)."""
+    m = tiny_lm(2048, dims=_DIMS_08B)
+    ref = OracleLM(orc, m)
+    want, gaps, tok = [], [], 1
+    for pos in range(32):
+        _, logits = ref.step(tok, pos)
+        tok, adj = orc.sample_token(logits, np.array(want, np.int32), 0.0, 1.2, 256, 0.1, 0.5)
+        top2 = np.sort(adj)[-2:]
+        gaps.append(float(top2[1] - top2[0]))
+        want.append(tok)
+    assert min(gaps) > 1e-3, "seeded model has a near-tie: pick another seed"
+    gpu = _persistent_lm(anelm, m, dev)
+    got, tok = [], 1
+    try:
+        for pos in range(32):
+            logits = gpu.forward(tok)
+            rec = to_dev(np.array(got, np.int32), dev) if got else None
+            tok = int(to_host(anelm.ops.sample_token(logits, rec, 0.0, 1.2, 256, 0.1, 0.5))[0])
+            got.append(tok)
+    finally:
+        gpu.close()
+    assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
 
 
 def test_complete_step_graph_replays(anelm, dev):
