@@ -426,9 +426,17 @@ __device__ __forceinline__ void gemv_issue(Buf<3 * NI>& b, LutRegs& lr, const Ge
         b.v[3 * m + 2] = t.z;
     }
 }
+template <bool EMPTY_OK = false>
 __device__ __forceinline__ void gemv_tables(const LutRegs& lr, const GemvGeo& q, int n_mat, int wave, int lane,
                                             char* lds, int* ctr, int target) {
-    if (wave >= n_mat * q.P || q.nrows <= 0) return;
+    if (wave >= n_mat * q.P) return;
+    if (!EMPTY_OK && q.nrows <= 0) return;
+    if (q.nrows <= 0) {
+        // no rows here (a projection whose rows do not fill the grid): the
+        // build count still advances, so later targets stay in step
+        if (lane == 0) __hip_atomic_fetch_add(ctr + wave / q.P, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return;
+    }
     const int mt = wave / q.P, wl = wave - mt * q.P;
     // pair tables (mt*3 + gi): rows i1 = wl, wl + P, ... of 64
     for (int gi = 0; gi < q.ng; gi++) {
@@ -1588,7 +1596,7 @@ __device__ __forceinline__ bool run_layer_proj(CArgs* pa, int l, BC& core_buf, B
     // ------------------------------------------------ first projection
     const GemvGeo fq = gemv_geo(a.f_C, a.f_P, a.f_RP, KIND == kATT ? a.f_rows_att : a.f_rows_dn,
                                 KIND == kATT ? a.f_out_att : a.f_out_dn);
-    gemv_tables(flr, fq, 1, wave, ln, lds, ctl + 11, fq.P * (l + 1));
+    gemv_tables<true>(flr, fq, 1, wave, ln, lds, ctl + 11, fq.P * (l + 1));
     if (wave == kCtl) {
         const int okw = l > 0 ? (int)ctl_wait(a, pb - 1, ln) : 1;
         if (ln == 0) ctl[0] = okw;
@@ -2165,6 +2173,13 @@ int persistent_create(PersistentStep** out, const anelm_hybrid_dims* d, const an
             return set_error(ANELM_ENULL, "persistent step: layer %d lacks a %s pointer (q/k norm weights are "
                              "required here)", i, ffn ? "core" : "FFN");
     }
+    // Complete layers in one launch are switched off: a run of a variant of
+    // step_kernel_proj ended in a GPU fault whose cause has not been found
+    // (the kernel stays for the investigation; the eager and graph modes run
+    // complete layers).
+    if (proj)
+        return set_error(ANELM_EINVAL, "persistent step: complete layers (projections) are disabled; use "
+                         "ANELM_STEP_EAGER or ANELM_STEP_GRAPH");
     ANELM_REQUIRE(!proj || d->conv_kernel == 4, "persistent step: conv kernel %d (4 supported)", d->conv_kernel);
     ANELM_REQUIRE(!proj || 5 * n_layers + n_layers / 4 <= pk::kMaxPhases,
                   "persistent step: %d complete layers exceed the barrier words", n_layers);

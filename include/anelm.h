@@ -525,11 +525,9 @@ typedef struct anelm_hybrid_step anelm_hybrid_step;
  *                          combined with ANELM_STEP_STATIC.  Supported for hidden/inter
  *                          sizes that tile over the device's compute units
  *                          (the Qwen3.5-4B and Qwen3.5-0.8B shapes on 256
- *                          CUs), for core + FFN layers (first_w NULL) or
- *                          complete layers (every layer with its projections
- *                          and the DeltaNet conv ring: five barrier phases per
- *                          layer; needs in_norm_w and conv_kernel 4); other
- *                          shapes return ANELM_EINVAL from create.
+ *                          CUs) and core + FFN layers (first_w NULL); other
+ *                          shapes, and complete layers (disabled), return
+ *                          ANELM_EINVAL from create.
  *   ANELM_STEP_COOPERATIVE (with PERSISTENT) launches through
  *                          hipLaunchCooperativeKernel: the runtime starts the
  *                          grid only when every workgroup can be resident, so
