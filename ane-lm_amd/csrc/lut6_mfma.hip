@@ -170,6 +170,53 @@ __device__ __forceinline__ void stage_luts(const GemmArgs& a, char* lds, int j0,
     }
 }
 
+// The wave's X window (vectors n < 32, columns w*128*NP .. +128*NP) as MFMA B
+// operands: lane (n, hh) takes columns hh*64*NP + 8t + j.  That is a 128*NP-
+// byte stretch of one row per lane, which as direct loads touches 64 partial
+// cache lines per wave instruction; instead each wave instruction loads
+// consecutive 16-byte chunks of whole rows (1 KiB), converts them to fp16
+// into this wave's 4 KiB of LDS (8 rows, RS bytes apart) and each lane takes
+// its stretch from there, 8 rows per round.  Vectors past the batch read
+// zeros (offsets past the buffer).
+template <int NP>
+__device__ __forceinline__ void load_x(half8 (&xb)[8 * NP], const GemmArgs& a, char* scratch, int w, int lane) {
+    constexpr int C4 = 32 * NP;            // float4 chunks in a row of the window
+    constexpr int RS = 256 * NP + 16;      // staged row: 128*NP halves + 16 bytes of bank offset
+    constexpr int PER = 8 * C4 / 64;       // chunks per lane per round of 8 rows
+    static_assert(8 * RS <= 16 * kRedRow * 4, "x staging exceeds the wave's partial-tile area");
+    const uint32_t bytes = (uint32_t)(((long)a.batch - 1) * a.ldx + a.in_dim) * 4u;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, (int)bytes, 0x00020000);
+    const int n = lane & 31, hh = lane >> 5;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        u32x4 v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int q = i * 64 + lane, row = 8 * r + q / C4, c4 = q % C4;
+            const uint32_t off = row < a.batch ? (uint32_t)(((long)row * a.ldx + w * 128 * NP + 4 * c4) * 4) : bytes;
+            v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int q = i * 64 + lane, rl = q / C4, c4 = q % C4;
+            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            // each element copied out before its bit cast (a bit cast of a
+            // vector element expression compiles as element 0)
+            const uint32_t e0 = v[i].x, e1 = v[i].y, e2 = v[i].z, e3 = v[i].w;
+            const half4 hv = {(_Float16)__builtin_bit_cast(float, e0), (_Float16)__builtin_bit_cast(float, e1),
+                              (_Float16)__builtin_bit_cast(float, e2), (_Float16)__builtin_bit_cast(float, e3)};
+            *reinterpret_cast<half4*>(scratch + rl * RS + c4 * 8) = hv;
+        }
+        // the wave's own LDS, accessed in order: no barrier
+        if ((n >> 3) == r) {
+            const char* src = scratch + (n & 7) * RS + hh * 128 * NP;
+#pragma unroll
+            for (int t = 0; t < 8 * NP; t++) xb[t] = *reinterpret_cast<const half8*>(src + 16 * t);
+        }
+    }
+}
+
 // Sums the NW partial tiles of group g and writes Y[n][32g + m] for n < batch.
 // Thread t handles (n = t / 32, m = t % 32): consecutive threads write
 // consecutive rows of one output vector.
@@ -222,28 +269,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
 
     // the wave's X window as MFMA B operands (fp16), zero for vectors >= batch
     half8 xb[8 * NP];
-    {
-        // every lane loads (vectors past the batch read vector 0 and are
-        // zeroed afterwards): no branch, so all loads are in flight at once
-        const int n = lane & 31, hh = lane >> 5;
-        const bool live = n < a.batch;
-        const float* xr = a.x + (size_t)(live ? n : 0) * a.ldx + (size_t)w * 128 * NP + hh * 64 * NP;
-        const float z = live ? 1.0f : 0.0f;
-#pragma unroll
-        for (int h0 = 0; h0 < 8 * NP; h0 += 4 * NP) {   // two halves bound the registers in flight
-            float4 lo[4 * NP], hi[4 * NP];
-#pragma unroll
-            for (int t = 0; t < 4 * NP; t++) {
-                lo[t] = *reinterpret_cast<const float4*>(xr + 8 * (h0 + t));
-                hi[t] = *reinterpret_cast<const float4*>(xr + 8 * (h0 + t) + 4);
-            }
-#pragma unroll
-            for (int t = 0; t < 4 * NP; t++)
-                xb[h0 + t] = half8{(_Float16)(lo[t].x * z), (_Float16)(lo[t].y * z), (_Float16)(lo[t].z * z),
-                                   (_Float16)(lo[t].w * z), (_Float16)(hi[t].x * z), (_Float16)(hi[t].y * z),
-                                   (_Float16)(hi[t].z * z), (_Float16)(hi[t].w * z)};
-        }
-    }
+    char* xs = lds + kRedOff + w * 16 * kRedRow * (int)sizeof(float);   // this wave's partial-tile area
     // Pipeline, one group ahead: group g's staged weights are taken into
     // registers, then the next group's staging loads go out and run during
     // g's products; g's pair table (slot j & 1) was built while group g-1
@@ -260,6 +286,8 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
         // LUT loads go first so the table build does not wait for the weights
         char* stage1 = lds + kRedOff;
         stage_luts<nt>(a, lds, 0, tid);
+        load_x<NP>(xb, a, xs, w, lane);
+        lds_barrier();                                 // every wave is done with its x staging area
         stage_group<NW, NP>(a, g, stage1, w, lane);
         lds_barrier();
         build_table(lds, 0, 0, w, nw, lane);
@@ -277,6 +305,7 @@ __global__ __launch_bounds__(NW * 64) void lut6_gemm_kernel(const GemmArgs a0) {
     }
     stage_luts<nt>(a, lds, 0, tid);
     stage_group<NW, NP>(a, g, stage, w, lane);
+    load_x<NP>(xb, a, xs, w, lane);
     lds_barrier();                                     // LUTs staged
     build_table(lds, 0, 0, w, nw, lane);
     for (int j = 0;; j++) {
