@@ -705,15 +705,38 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
     const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
     const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
     // rows past the split's last key load that key again (masked below): the
-    // loads stay unconditional, so the counted waits stay exact
-    auto load_rows = [&](int c, const KV* base, Raw8<KV> (&r)[KB]) __attribute__((always_inline)) {
+    // loads stay unconditional, so the counted waits stay exact.  A key's K
+    // and V rows sit at the same offset of their caches.  The chunk's page
+    // entries are all read from LDS before any address is formed (one wait),
+    // a power-of-two page size takes shifts instead of divisions, and row
+    // indices stay 32-bit (the host bounds the cache to 2^31 rows).
+    const int ps_shift = (ps & (ps - 1)) == 0 ? __builtin_ctz((unsigned)ps) : -1;
+    const unsigned rows_per_page = (unsigned)(Hkv * ps), head_row = (unsigned)(kvh * ps);
+    auto load_rows = [&](int c, Raw8<KV> (&rk)[KB], Raw8<KV> (&rv)[KB]) __attribute__((always_inline)) {
         c = min(c, nch - 1);   // (past the last chunk: reload it, unused)
+        unsigned kt[KB], page[KB], row[KB];
+#pragma unroll
+        for (int b = 0; b < KB; b++)   // key index inside the sequence
+            kt[b] = (unsigned)(k0 + min(c * CK + b * KPB + w * KPI + sub, nk_all - 1));
+        if (ps_shift >= 0) {
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                page[b] = (unsigned)pg[(int)(kt[b] >> ps_shift) - pfirst];
+                row[b] = kt[b] & (unsigned)(ps - 1);
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                const unsigned pi = kt[b] / (unsigned)ps;
+                page[b] = (unsigned)pg[(int)pi - pfirst];
+                row[b] = kt[b] - pi * (unsigned)ps;
+            }
+        }
 #pragma unroll
         for (int b = 0; b < KB; b++) {
-            const int lt = min(c * CK + b * KPB + w * KPI + sub, nk_all - 1);   // key index inside the split
-            const int kt = k0 + lt;
-            const int page = pg[kt / ps - pfirst], row = kt % ps;
-            r[b] = load_raw(base + (((size_t)page * Hkv + kvh) * ps + row) * D + dl * 8);
+            const size_t off = (size_t)(page[b] * rows_per_page + head_row + row[b]) * D + dl * 8;
+            rk[b] = load_raw(kc + off);
+            rv[b] = load_raw(vc + off);
         }
     };
 
@@ -799,8 +822,7 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
     // each other's load latency)
     for (int c = 0; c < nch; c++) {
         Raw8<KV> rk[KB], rv[KB];
-        load_rows(c, kc, rk);
-        load_rows(c, vc, rv);
+        load_rows(c, rk, rv);
         if (t_new >= 0 && c == t_new / CK) {
             // the new key's row was loaded before (or while) it was stored:
             // take it from the prologue, rounded as stored
@@ -1230,6 +1252,9 @@ extern "C" int anelm_attn_decode_paged(float* out, const float* q, int q_head_st
     ANELM_REQUIRE(n_seqs > 0 && n_seqs <= 65535, "paged: n_seqs %d", n_seqs);
     ANELM_REQUIRE(page_size > 0 && max_pages > 0 && n_pages > 0,
                   "paged: page_size %d max_pages %d n_pages %d", page_size, max_pages, n_pages);
+    ANELM_REQUIRE((long long)n_pages * n_kv_heads * page_size < (1LL << 31),
+                  "paged: %d pages of %d rows x %d kv heads exceed 2^31 cache rows", n_pages, page_size,
+                  n_kv_heads);
     ANELM_REQUIRE(max_seq_len > 0 && max_seq_len <= max_pages * page_size,
                   "paged: max_seq_len %d beyond max_pages*page_size", max_seq_len);
     ANELM_REQUIRE(q_head_stride >= head_dim, "paged: q_head_stride %d < head_dim", q_head_stride);
@@ -1274,6 +1299,9 @@ extern "C" int anelm_attn_decode_paged_step(float* out, const float* q_gate, con
     ANELM_REQUIRE(n_seqs > 0 && n_seqs <= 65535, "paged step: n_seqs %d", n_seqs);
     ANELM_REQUIRE(page_size > 0 && max_pages > 0 && n_pages > 0,
                   "paged step: page_size %d max_pages %d n_pages %d", page_size, max_pages, n_pages);
+    ANELM_REQUIRE((long long)n_pages * n_kv_heads * page_size < (1LL << 31),
+                  "paged step: %d pages of %d rows x %d kv heads exceed 2^31 cache rows", n_pages, page_size,
+                  n_kv_heads);
     ANELM_REQUIRE(max_seq_len > 0 && max_seq_len <= max_pages * page_size,
                   "paged step: max_seq_len %d beyond max_pages*page_size", max_seq_len);
     ANELM_REQUIRE(rot_dim >= 0 && rot_dim % 2 == 0 && rot_dim <= head_dim && rot_dim / 2 <= kMaxRotPairs,
