@@ -11,6 +11,8 @@
 // loads, an arrival counter per kv head), else in a second small kernel.
 #include "anelm_internal.hpp"
 
+#include <type_traits>
+
 #include <algorithm>
 #include <math.h>
 #include <vector>
@@ -113,6 +115,15 @@ template <> __device__ __forceinline__ Raw8<float> make_raw<float>(const float* 
 
 __device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f2h(v); }
 __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
+
+// fp16 pair (lo, hi) and its dot product with another pair, accumulated in fp32
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+    return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+}
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c, false);
+}
 
 // RMSNorm (cpu_ops.cpp:24-30) + RoPE (cpu_ops.cpp:40-63) of one D-vector held
 // in shared memory, in place.  All threads participate.
@@ -618,8 +629,9 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
     constexpr int REC = D + 2;
     static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
 
-    __shared__ float sc[G][CK];
+    __shared__ __attribute__((aligned(16))) float sc_w[kNW][64];   // each wave's softmax weights of a chunk
     __shared__ float red_g[kNW][G];
+    __shared__ float red_m[kNW][G];
     __shared__ float red_o[kNW][G][D];
     __shared__ int pg[KPS + 1];   // page-table entries of the split (any page size)
     // fused step only: q rows and the new key after norm + RoPE, RoPE row
@@ -700,6 +712,16 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
             for (int i = 0; i < 8; i++) qr[g][i] = src[i];
         }
     }
+    // fp16 caches: q as fp16 pairs, so scores are packed fp16 dot products
+    // with fp32 accumulation (fp16 inputs, as the cache itself)
+    constexpr bool kHalf = std::is_same<KV, uint16_t>::value;
+    uint32_t qh[G][4];
+    if constexpr (kHalf) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) qh[g][j] = pack_half2(qr[g][2 * j], qr[g][2 * j + 1]);
+    }
     lds_barrier();
 
     const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
@@ -740,82 +762,123 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
         }
     };
 
-    float m[G], lsum[G], acc[G][8];
+    // Online softmax per wave: a wave keeps its own running maximum per head
+    // and sums over the keys it holds (rows t = b*KPB + w*KPI + sub of each
+    // chunk), so the chunk loop has no workgroup barrier and a wave waiting
+    // on its rows holds up no other; the waves' states are merged once at the
+    // end by log-sum-exp.  After the transpose reduction lane (sub, dl) holds
+    // the score of row b = dl / G for head g = dl % G = lane % G.
+    float m[G], acc[G][8];
+    float lsum = 0.f;   // this lane's share of the sum for its head lane % G
 #pragma unroll
     for (int g = 0; g < G; g++) {
         m[g] = -INFINITY;
-        lsum[g] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
     }
+    float* pw = sc_w[w];
+    const int g_own = dl % G;
     auto chunk = [&](int c, const Raw8<KV> (&rk)[KB], const Raw8<KV> (&rv)[KB]) __attribute__((always_inline)) {
         const int nk = min(CK, nk_all - c * CK);
         // ---- scores: one transpose reduction over the KB rows of each lane
+        float s_own;
         {
             float part[KB * G];
 #pragma unroll
             for (int b = 0; b < KB; b++) {
-                float kf[8];
-                to_f32(rk[b], kf);
+                if constexpr (kHalf) {
+                    const uint32_t kw[4] = {rk[b].a.x, rk[b].a.y, rk[b].a.z, rk[b].a.w};
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float sv = 0.f;
+                    for (int g = 0; g < G; g++) {
+                        float sv = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) sv = fmaf(qr[g][i], kf[i], sv);
-                    part[b * G + g] = sv;
+                        for (int j = 0; j < 4; j++) sv = dot2_acc(qh[g][j], kw[j], sv);
+                        part[b * G + g] = sv;
+                    }
+                } else {
+                    float kf[8];
+                    to_f32(rk[b], kf);
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        float sv = 0.f;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) sv = fmaf(qr[g][i], kf[i], sv);
+                        part[b * G + g] = sv;
+                    }
                 }
             }
             transpose_reduce<LPK, KB * G>(part, dl);
-            const int b = dl / G, g = dl % G;
-            const int t = b * KPB + w * KPI + sub;
-            sc[g][t] = t < nk ? part[0] * p.scale : -INFINITY;
+            const int t = (dl / G) * KPB + w * KPI + sub;
+            s_own = t < nk ? part[0] * p.scale : -INFINITY;
         }
-        lds_barrier();
-        // ---- running maximum per head (one reduction for all G heads)
-        float mc[G];
+        // ---- running maximum per head over the wave's keys (exact XOR
+        // partners keep the lanes of one head together)
+        float mx = s_own;
+#pragma unroll
+        for (int mm = G; mm < 64; mm <<= 1) mx = fmaxf(mx, shfl_xor(mx, mm));
+        float alpha_own = 0.f, m_own = 0.f;
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            float v = -INFINITY;
-            for (int t = tid; t < CK; t += kNT) v = fmaxf(v, sc[g][t]);
-            mc[g] = wave_max(v);
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int g = 0; g < G; g++) red_g[w][g] = mc[g];
-        }
-        lds_barrier();
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float mx = red_g[0][g];
-#pragma unroll
-            for (int ww = 1; ww < kNW; ww++) mx = fmaxf(mx, red_g[ww][g]);
-            const float m_new = fmaxf(m[g], mx);
-            const float alpha = __expf(m[g] - m_new);   // 0 on the first chunk (m = -inf)
-            lsum[g] *= alpha;
+            const float mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), g));
+            const float m_new = fmaxf(m[g], mc);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no valid key yet: weights 0
+            const float alpha = __expf(m[g] - m_use);              // 0 while m is -inf
 #pragma unroll
             for (int i = 0; i < 8; i++) acc[g][i] *= alpha;
             m[g] = m_new;
-            for (int t = tid; t < CK; t += kNT) {
-                const float e = __expf(sc[g][t] - m_new);   // masked keys: exp(-inf) = 0
-                sc[g][t] = e;
-                lsum[g] += e;
+            if (g == g_own) {
+                alpha_own = alpha;
+                m_own = m_use;
             }
         }
-        lds_barrier();
-        // ---- P V
+        const float e = __expf(s_own - m_own);   // masked keys: exp(-inf) = 0
+        lsum = lsum * alpha_own + e;
+        // the weights back in row order through the wave's own LDS (a wave's
+        // LDS accesses execute in order: no barrier)
+        pw[lane] = e;
+        float pv[KB * G];
 #pragma unroll
-        for (int b = 0; b < KB; b++) {
-            const int t = b * KPB + w * KPI + sub;
+        for (int k = 0; k < KB * G / 4; k++) {
+            const float4 v4 = *reinterpret_cast<const float4*>(pw + sub * LPK + 4 * k);
+            pv[4 * k] = v4.x;
+            pv[4 * k + 1] = v4.y;
+            pv[4 * k + 2] = v4.z;
+            pv[4 * k + 3] = v4.w;
+        }
+        // ---- P V (fp16 caches: two key rows per packed dot product, the
+        // weights rounded to fp16 pairs and the rows' values interleaved)
+        constexpr int KP = kHalf ? KB / 2 : 0;
+        if constexpr (kHalf) {
+#pragma unroll
+            for (int j = 0; j < KP; j++) {
+                const uint32_t va[4] = {rv[2 * j].a.x, rv[2 * j].a.y, rv[2 * j].a.z, rv[2 * j].a.w};
+                const uint32_t vb[4] = {rv[2 * j + 1].a.x, rv[2 * j + 1].a.y, rv[2 * j + 1].a.z,
+                                        rv[2 * j + 1].a.w};
+                uint32_t vp[8];   // (row 2j, row 2j+1) of dims 2k and 2k+1
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    vp[2 * k] = __builtin_amdgcn_perm(vb[k], va[k], 0x05040100u);
+                    vp[2 * k + 1] = __builtin_amdgcn_perm(vb[k], va[k], 0x07060302u);
+                }
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const uint32_t pp = pack_half2(pv[(2 * j) * G + g], pv[(2 * j + 1) * G + g]);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc[g][i] = dot2_acc(pp, vp[i], acc[g][i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 2 * KP; b < KB; b++) {
             float vf[8];
             to_f32(rv[b], vf);
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float pgv = sc[g][t];
+                const float pgv = pv[b * G + g];
 #pragma unroll
                 for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pgv, vf[i], acc[g][i]);
             }
         }
-        lds_barrier();   // sc is rewritten by the next chunk
     };
 
     // one chunk's rows in registers at a time (several workgroups per CU hide
@@ -837,13 +900,22 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
         chunk(c, rk, rv);
     }
 
-    // ---- totals: l over the workgroup, O over the lanes sharing dims and the waves
-    float lt[G];
+    // ---- merge the waves: per head M = max of the waves' maxima, each wave
+    // weighed by e^(m_w - M); O summed over the lanes sharing dims first
+    float lw[G];
+    {
+        float l = lsum;
 #pragma unroll
-    for (int g = 0; g < G; g++) lt[g] = wave_sum(lsum[g]);
+        for (int mm = G; mm < 64; mm <<= 1) l += shfl_xor(l, mm);
+#pragma unroll
+        for (int g = 0; g < G; g++) lw[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), g));
+    }
     if (lane == 0) {
 #pragma unroll
-        for (int g = 0; g < G; g++) red_g[w][g] = lt[g];
+        for (int g = 0; g < G; g++) {
+            red_g[w][g] = lw[g];
+            red_m[w][g] = m[g];
+        }
     }
 #pragma unroll
     for (int mm = LPK; mm < 64; mm <<= 1)
@@ -858,19 +930,27 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
             for (int i = 0; i < 8; i++) red_o[w][g][dl * 8 + i] = acc[g][i];
     }
     lds_barrier();
-    float ltot[G];
+    float mtot[G], ltot[G], wsc[G][kNW];
 #pragma unroll
     for (int g = 0; g < G; g++) {
+        float M = red_m[0][g];
+#pragma unroll
+        for (int ww = 1; ww < kNW; ww++) M = fmaxf(M, red_m[ww][g]);
+        const float Mu = M == -INFINITY ? 0.f : M;
+        mtot[g] = M;
         ltot[g] = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < kNW; ww++) ltot[g] += red_g[ww][g];
+        for (int ww = 0; ww < kNW; ww++) {
+            wsc[g][ww] = __expf(red_m[ww][g] - Mu);   // a wave without valid keys: 0
+            ltot[g] += red_g[ww][g] * wsc[g][ww];
+        }
     }
     if (n_splits == 1) {
         for (int e = tid; e < G * D; e += kNT) {
             const int g = e / D, d = e % D;
             float o = 0.f;
 #pragma unroll
-            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d] * wsc[g][ww];
             const int hq = kvh * G + g;
             float yv = o / ltot[g];
             if (p.gate) yv = yv / (1.0f + expf(-q[(size_t)hq * p.q_stride + D + d]));
@@ -883,9 +963,9 @@ __global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
         const int g = e / D, d = e % D;
         float o = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d];
+        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d] * wsc[g][ww];
         rec[(size_t)g * REC + 2 + d] = o;
-        if (d == 0) { rec[(size_t)g * REC] = m[g]; rec[(size_t)g * REC + 1] = ltot[g]; }
+        if (d == 0) { rec[(size_t)g * REC] = mtot[g]; rec[(size_t)g * REC + 1] = ltot[g]; }
     }
 }
 
