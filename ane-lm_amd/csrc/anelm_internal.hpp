@@ -98,6 +98,13 @@ bool lut6_gemm_geometry(int in_dim, int& np, int& waves);
 int lut6_gemm_launch(float* y, const uint8_t* w, long ldw, const uint16_t* lut, const float* x, long ldx, int batch,
                      int out_dim, int in_dim, int accumulate, int nsplit, long sy, hipStream_t st);
 int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st);
+bool lut6_split_sum_norm_fits(int out_dim, int nsplit);
+int lut6_split_sum_norm(float* y, const float* part, long n, int nsplit, int accumulate, int rows, int out_dim,
+                        const float* norm_w, float eps, float* xn, hipStream_t st);
+// Y (+)= W X over a batch (anelm_lut6_gemm), then xn = RMSNorm(Y) * norm_w per
+// row: fused into the sum of the column slices where the GEMM is split.
+int lut6_gemm_norm(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                   int in_dim, int accumulate, const float* norm_w, float eps, float* xn, hipStream_t st);
 
 // y (+)= W x over a LUT6 matrix, x optionally RMS-normalised first (norm_w).
 int lut6_gemv_impl(float* y, const uint8_t* w, const uint16_t* lut, const float* x, const float* norm_w,

@@ -104,7 +104,11 @@ extern "C" int anelm_batch_step_run(anelm_batch_step* s, int advance, void* stre
     const anelm_hybrid_dims& d = s->dims;
     const anelm_batch_seqs& q = s->seqs;
     const int B = q.n_seqs, H = d.hidden, I = d.inter;
-    for (const anelm_batch_layer& L : s->layers) {
+    const int n_layers = (int)s->layers.size();
+    // the final norm for the LM head, folded into the last down projection
+    const float* final_norm = q.lm_w ? q.final_norm_w : nullptr;
+    for (int l = 0; l < n_layers; l++) {
+        const anelm_batch_layer& L = s->layers[l];
         int rc;
         if (L.kind == ANELM_LAYER_ATTENTION) {
             rc = anelm_attn_decode_paged_step(L.core_out, L.q_gate, L.k, L.v, L.k_pages, L.v_pages, L.page_table,
@@ -118,21 +122,27 @@ extern "C" int anelm_batch_step_run(anelm_batch_step* s, int advance, void* stre
                                                d.lin_dim, d.lin_dim, L.dn_flags, stream);
         }
         if (rc) return rc;
-        rc = anelm_rmsnorm(s->xn, s->x, L.ffn_norm_w, H, B, H, H, d.eps, stream);
-        if (rc) return rc;
+        // the FFN norm of layer 0; later layers' come with the previous down
+        // projection (the cores between leave x unchanged)
+        if (l == 0) {
+            rc = anelm_rmsnorm(s->xn, s->x, L.ffn_norm_w, H, B, H, H, d.eps, stream);
+            if (rc) return rc;
+        }
         rc = anelm_lut6_gemm(s->gu, L.gate_up_w, L.gate_up_lut, s->xn, B, 2 * I, H, 0, stream);
         if (rc) return rc;
         rc = anelm_swiglu_rows(s->h, s->gu, B, I, stream);
         if (rc) return rc;
-        rc = anelm_lut6_gemm(s->x, L.down_w, L.down_lut, s->h, B, H, I, 1, stream);
+        const float* next_norm = l + 1 < n_layers ? s->layers[l + 1].ffn_norm_w : final_norm;
+        rc = next_norm ? lut6_gemm_norm(s->x, L.down_w, L.down_lut, s->h, B, H, I, 1, next_norm, d.eps, s->xn,
+                                        as_stream(stream))
+                       : anelm_lut6_gemm(s->x, L.down_w, L.down_lut, s->h, B, H, I, 1, stream);
         if (rc) return rc;
     }
     if (q.lm_w) {
-        const float* xf = s->x;
-        if (q.final_norm_w) {
-            const int rc = anelm_rmsnorm(s->xn, s->x, q.final_norm_w, H, B, H, H, d.eps, stream);
+        const float* xf = final_norm ? s->xn : s->x;
+        if (final_norm && n_layers == 0) {
+            const int rc = anelm_rmsnorm(s->xn, s->x, final_norm, H, B, H, H, d.eps, stream);
             if (rc) return rc;
-            xf = s->xn;
         }
         const int rc = anelm_lut6_topk(q.top_idx, q.top_val, q.lm_w, q.lm_lut, xf, B, q.vocab, H, q.top_k, stream);
         if (rc) return rc;

@@ -800,7 +800,13 @@ int gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int ou
 // accumulating) -- a fixed order, so results do not vary between calls.
 // Shapes that fit no slicing take one GEMV per input.
 int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
-                 int in_dim, int accumulate, hipStream_t st) {
+                 int in_dim, int accumulate, hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
+                 float* xn = nullptr) {
+    // with norm_w: xn = RMSNorm(y) * norm_w per row afterwards
+    auto norm_rows = [&](int b0, int nb) {
+        return anelm_rmsnorm(xn + (size_t)b0 * out_dim, y + (size_t)b0 * out_dim, norm_w, out_dim, nb, out_dim,
+                             out_dim, eps, st);
+    };
     int np = 0, waves = 0;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
     auto fits = [&](int s) {
@@ -813,7 +819,7 @@ int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x
             const int rc = gemv(y + (size_t)b * out_dim, w, lut, x + (size_t)b * in_dim, out_dim, in_dim, accumulate, st);
             if (rc) return rc;
         }
-        return ANELM_OK;
+        return norm_w ? norm_rows(0, batch) : ANELM_OK;
     }
     Device* dev = device();
     if (!dev) return ANELM_EHIP;
@@ -828,7 +834,8 @@ int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x
         float* yb = y + (size_t)b0 * out_dim;
         const float* xb = x + (size_t)b0 * in_dim;
         if (ns == 1) {
-            const int rc = lut6_gemm_launch(yb, w, ldw, lut, xb, in_dim, nb, out_dim, part, accumulate, 1, 0, st);
+            int rc = lut6_gemm_launch(yb, w, ldw, lut, xb, in_dim, nb, out_dim, part, accumulate, 1, 0, st);
+            if (rc == ANELM_OK && norm_w) rc = norm_rows(b0, nb);
             if (rc) return rc;
             continue;
         }
@@ -837,7 +844,13 @@ int batched_gemv(float* y, const uint8_t* w, const uint16_t* lut, const float* x
         if (!parts) return ANELM_ENOMEM;
         int rc = lut6_gemm_launch(parts, w, ldw, lut, xb, in_dim, nb, out_dim, part, 0, ns, n, st);
         if (rc) return rc;
-        rc = lut6_split_sum(yb, parts, n, ns, accumulate, st);
+        if (norm_w && lut6_split_sum_norm_fits(out_dim, ns)) {
+            rc = lut6_split_sum_norm(yb, parts, n, ns, accumulate, nb, out_dim, norm_w, eps,
+                                     xn + (size_t)b0 * out_dim, st);
+        } else {
+            rc = lut6_split_sum(yb, parts, n, ns, accumulate, st);
+            if (rc == ANELM_OK && norm_w) rc = norm_rows(b0, nb);
+        }
         if (rc) return rc;
     }
     return ANELM_OK;
@@ -854,6 +867,18 @@ int lut6_gemv_impl(float* y, const uint8_t* w, const uint16_t* lut, const float*
     int rc = check_shape(out_dim, in_dim);
     if (rc) return rc;
     return gemv(y, w, lut, x, out_dim, in_dim, residual, st, norm_w, eps);
+}
+}  // namespace anelm
+
+namespace anelm {
+int lut6_gemm_norm(float* y, const uint8_t* w, const uint16_t* lut, const float* x, int batch, int out_dim,
+                   int in_dim, int accumulate, const float* norm_w, float eps, float* xn, hipStream_t st) {
+    ANELM_NONNULL(norm_w);
+    ANELM_NONNULL(xn);
+    int rc = check_shape(out_dim, in_dim);
+    if (rc) return rc;
+    ANELM_REQUIRE(batch > 0, "lut6_gemm: batch %d", batch);
+    return batched_gemv(y, w, lut, x, batch, out_dim, in_dim, accumulate, st, norm_w, eps, xn);
 }
 }  // namespace anelm
 

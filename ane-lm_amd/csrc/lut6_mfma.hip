@@ -346,7 +346,61 @@ __global__ __launch_bounds__(256) void split_sum_kernel(float* y, const float* p
     y[i] = s;
 }
 
+// split_sum_kernel for one row per workgroup (rows of out_dim <= 4 * 1024
+// elements, up to 16 column slices), followed by the RMSNorm of the summed row
+// times w into xn (cpu_ops.cpp:24-30): the norm input of the next layer's
+// FFN, one launch fewer.  Each thread issues all of its loads at once (the
+// slices unrolled), then adds them in slice order.
+constexpr int kSumNormThreads = 1024, kSumNormReg = 4, kSumNormSplits = 16;
+__global__ __launch_bounds__(kSumNormThreads) void split_sum_norm_kernel(float* y, const float* part, float* xn,
+                                                                         const float* w, int out_dim, long n,
+                                                                         int nsplit, int accumulate, float eps) {
+    constexpr int NT = kSumNormThreads, R = kSumNormReg, S = kSumNormSplits;
+    __shared__ float red[NT / 64];
+    const size_t r0 = (size_t)blockIdx.x * out_dim;
+    float v[R], wv[R];
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        const int i = threadIdx.x + NT * k;
+        const bool in = i < out_dim;
+        const size_t e = r0 + (in ? i : 0);
+        float ps[S];
+#pragma unroll
+        for (int sp = 0; sp < S; sp++) ps[sp] = sp < nsplit ? part[(long)sp * n + e] : 0.f;
+        float s = accumulate ? y[e] : 0.f;
+#pragma unroll
+        for (int sp = 0; sp < S; sp++)
+            if (sp < nsplit) s += ps[sp];
+        if (in) y[e] = s;
+        v[k] = in ? s : 0.f;
+        wv[k] = in ? w[i] : 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < R; k++) ss += v[k] * v[k];
+    ss = block_sum<NT>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)out_dim + eps);
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        const int i = threadIdx.x + NT * k;
+        if (i < out_dim) xn[r0 + i] = (v[k] * inv) * wv[k];
+    }
+}
+
 }  // namespace
+
+bool lut6_split_sum_norm_fits(int out_dim, int nsplit) {
+    return out_dim <= kSumNormThreads * kSumNormReg && nsplit <= kSumNormSplits;
+}
+int lut6_split_sum_norm(float* y, const float* part, long n, int nsplit, int accumulate, int rows, int out_dim,
+                        const float* norm_w, float eps, float* xn, hipStream_t st) {
+    if (out_dim > kSumNormThreads * kSumNormReg || nsplit > kSumNormSplits)
+        return set_error(ANELM_EINVAL, "split_sum_norm: row of %d elements in %d slices", out_dim, nsplit);
+    hipLaunchKernelGGL(split_sum_norm_kernel, dim3((unsigned)rows), dim3(kSumNormThreads), 0, st, y, part, xn, norm_w,
+                       out_dim, n, nsplit, accumulate, eps);
+    ANELM_LAUNCHED("split_sum_norm_kernel");
+    return ANELM_OK;
+}
 
 int lut6_split_sum(float* y, const float* part, long n, int nsplit, int accumulate, hipStream_t st) {
     hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, part, n, nsplit,
