@@ -744,11 +744,14 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
                 }
             }
         }
-        float q[kAttnG][8];
+        // q as fp16 pairs: scores are packed fp16 dot products (fp16 inputs,
+        // as the cache rows, fp32 accumulation)
+        uint32_t qh[kAttnG][4];
 #pragma unroll
         for (int g = 0; g < kAttnG; g++)
 #pragma unroll
-            for (int i = 0; i < 8; i++) q[g][i] = qs[g * kAttnD + dl * 8 + i];
+            for (int i = 0; i < 4; i++)
+                qh[g][i] = pack_h2(qs[g * kAttnD + dl * 8 + 2 * i], qs[g * kAttnD + dl * 8 + 2 * i + 1]);
 #pragma unroll
         for (int j0 = 0; j0 < NKJ; j0 += 2) {
             float part[8];
@@ -763,17 +766,11 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
                     kr = *reinterpret_cast<const u32x4*>(src);
                 }
                 const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
-                float kf[8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    kf[2 * i] = h16(kw[i], 0);
-                    kf[2 * i + 1] = h16(kw[i], 1);
-                }
 #pragma unroll
                 for (int g = 0; g < kAttnG; g++) {
                     float sdot = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) sdot = fmaf(q[g][i], kf[i], sdot);
+                    for (int i = 0; i < 4; i++) sdot = dot2(qh[g][i], kw[i], sdot);
                     part[jj * kAttnG + g] = sdot;
                 }
             }
@@ -813,8 +810,30 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
         for (int g = 0; g < kAttnG; g++)
 #pragma unroll
             for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
+        // two key rows per packed fp16 dot product: the rows' values
+        // interleaved per dimension, the probabilities rounded to fp16 pairs
+        // (rows past the split's keys weigh 0)
 #pragma unroll
-        for (int j = 0; j < NKJ; j++) {
+        for (int j = 0; j + 1 < NKJ; j += 2) {
+            const int t0 = hw + 20 * j, t1 = t0 + 20;
+            uint32_t vp[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                vp[2 * i] = __builtin_amdgcn_perm(b.v[4 * (j + 1) + i], b.v[4 * j + i], 0x05040100u);
+                vp[2 * i + 1] = __builtin_amdgcn_perm(b.v[4 * (j + 1) + i], b.v[4 * j + i], 0x07060302u);
+            }
+#pragma unroll
+            for (int g = 0; g < kAttnG; g++) {
+                const float p0 = t0 < nk ? sc[g * 160 + t0] : 0.f;
+                const float p1 = t1 < nk ? sc[g * 160 + t1] : 0.f;
+                const uint32_t pp = pack_h2(p0, p1);
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[g][i] = dot2(pp, vp[i], acc[g][i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (NKJ % 2 == 1) {
+            constexpr int j = NKJ - 1;
             const int t = hw + 20 * j;
             if (t < nk) {
                 float vf[8];
@@ -830,7 +849,6 @@ __device__ void attn_compute(Buf<4 * NKJ>& b, const PArgs& a, const PLayer& L, i
                     for (int i = 0; i < 8; i++) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int g = 0; g < kAttnG; g++)
