@@ -273,20 +273,62 @@ __global__ __launch_bounds__(ring_threads<G>()) void attn_decode_kernel(const De
     const bool owner = p.fused && split == n_splits - 1;   // holds the newest key
     const float* qh = p.q + (size_t)kvh * G * p.q_stride;
 
-    // ---- every operand requested at once
+    // ---- every operand requested at once.  With interleaved RoPE pairs (or
+    // none) every lane takes the 8 dims dl*8 .. dl*8+7 of each q row (and of
+    // the new key) itself: the row sums over the LPK lanes that hold it,
+    // the pairs lie inside the lane, so norm and RoPE need no LDS and no
+    // workgroup barrier.  Half-split pairs go through LDS (one thread per dim).
+    const bool lane_rows = !p.fused || p.rope_mode == 0;
+    const bool qnorm = p.fused && p.q_norm_w != nullptr;
     float qv[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) qv[g] = tid < D ? qh[(size_t)g * p.q_stride + tid] : 0.f;
+    float q8[G][8], wq8[8], kn8[8], wk8[8];
     float wq = 1.f, wk = 1.f;
-    if (p.fused && p.q_norm_w != nullptr && tid < D) wq = p.q_norm_w[tid];
     float kn_reg = 0.f, vn_reg = 0.f;
     float vn8[8];
-    if (owner) {
-        if (tid < D) {
+    if (lane_rows) {
+        // 8 consecutive floats per lane: two 16-byte loads where the rows are
+        // 16-byte aligned (the two halves of a lane's 32 bytes share lines)
+        auto load8 = [](const float* src, float (&o)[8], bool al) __attribute__((always_inline)) {
+            if (al) {
+                const float4 lo = reinterpret_cast<const float4*>(src)[0];
+                const float4 hi = reinterpret_cast<const float4*>(src)[1];
+                o[0] = lo.x; o[1] = lo.y; o[2] = lo.z; o[3] = lo.w;
+                o[4] = hi.x; o[5] = hi.y; o[6] = hi.z; o[7] = hi.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] = src[i];
+            }
+        };
+        auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+        const bool qal = al16(qh) && (p.q_stride & 3) == 0;
+#pragma unroll
+        for (int g = 0; g < G; g++) load8(qh + (size_t)g * p.q_stride + dl * 8, q8[g], qal);
+        if (qnorm) {
+            load8(p.q_norm_w + dl * 8, wq8, al16(p.q_norm_w));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) wq8[i] = 1.f;
+        }
+        if (owner) {
+            load8(p.k_new + (size_t)kvh * D + dl * 8, kn8, al16(p.k_new));
+            if (p.k_norm_w != nullptr) {
+                load8(p.k_norm_w + dl * 8, wk8, al16(p.k_norm_w));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) wk8[i] = 1.f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; g++) qv[g] = tid < D ? qh[(size_t)g * p.q_stride + tid] : 0.f;
+        if (qnorm && tid < D) wq = p.q_norm_w[tid];
+        if (owner && tid < D) {
             kn_reg = p.k_new[(size_t)kvh * D + tid];
             vn_reg = p.v_new[(size_t)kvh * D + tid];
             if (p.k_norm_w != nullptr) wk = p.k_norm_w[tid];
         }
+    }
+    if (owner) {
 #pragma unroll
         for (int i = 0; i < 8; i++) vn8[i] = p.v_new[(size_t)kvh * D + dl * 8 + i];   // any alignment
     }
@@ -297,11 +339,11 @@ __global__ __launch_bounds__(ring_threads<G>()) void attn_decode_kernel(const De
         const int e = tid + i * NT, g = e / D, d = e % D;
         gl[i] = (p.gate && finisher && e < G * D) ? qh[(size_t)g * p.q_stride + D + d] : 0.f;
     }
-    if (p.fused && tid < p.rot_pairs) {
-        // cos / sin through pointers into the argument segment: indexing the
-        // by-value arrays directly expands into a select over every entry
-        const float* csp = p.cs;
-        const float* snp = p.sn;
+    // cos / sin through pointers into the argument segment: indexing the
+    // by-value arrays directly expands into a select over every entry
+    const float* csp = p.cs;
+    const float* snp = p.sn;
+    if (!lane_rows && tid < p.rot_pairs) {
         cs_s[tid] = csp[tid];
         sn_s[tid] = snp[tid];
     }
@@ -320,72 +362,141 @@ __global__ __launch_bounds__(ring_threads<G>()) void attn_decode_kernel(const De
         }
     }
 
-    // ---- q rows (and the owner's key row): RMSNorm + RoPE in one reduction round
-    if (tid < D) {
+    float qr[G][8];
+    if (lane_rows) {
+        // ---- RMSNorm (sum over the row's LPK lanes) and interleaved RoPE in registers
+        if (qnorm) {
 #pragma unroll
-        for (int g = 0; g < G; g++) q_s[g][tid] = qv[g];
-        q_s[G][tid] = kn_reg;
-    }
-    const int nrows = owner ? G + 1 : G;
-    if (p.fused) {
-        if (p.q_norm_w != nullptr) {
-            // partial sums in the order of block_sum: per wave, then over the waves
-            float ss[G + 1];
+            for (int g = 0; g < G; g++) {
+                float ss = 0.f;
 #pragma unroll
-            for (int r = 0; r <= G; r++) {
-                const float v = tid < D ? (r < G ? qv[r] : kn_reg) : 0.f;
-                ss[r] = wave_sum(v * v);
+                for (int i = 0; i < 8; i++) ss += q8[g][i] * q8[g][i];
+                ss = wave_sum_from<LPK / 2>(ss);   // the LPK lanes holding the row
+                const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+                for (int i = 0; i < 8; i++) q8[g][i] = (q8[g][i] * inv) * wq8[i];
             }
-            if (lane == 0) {
+        }
+        if (owner && p.k_norm_w != nullptr) {
+            float ss = 0.f;
 #pragma unroll
-                for (int r = 0; r <= G; r++) red_g[w][r] = ss[r];
-            }
-            __syncthreads();
-            if (tid < D) {
+            for (int i = 0; i < 8; i++) ss += kn8[i] * kn8[i];
+            ss = wave_sum_from<LPK / 2>(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
 #pragma unroll
-                for (int r = 0; r <= G; r++) {
-                    float t = 0.f;
+            for (int i = 0; i < 8; i++) kn8[i] = (kn8[i] * inv) * wk8[i];
+        }
+        if (p.fused) {
 #pragma unroll
-                    for (int i = 0; i < NW; i++) t += red_g[i][r];
-                    const float inv = 1.0f / sqrtf(t / (float)D + p.eps);
-                    q_s[r][tid] = (q_s[r][tid] * inv) * (r < G ? wq : wk);
+            for (int m = 0; m < 4; m++) {
+                const int j = dl * 4 + m;   // pair (2j, 2j + 1)
+                if (j < p.rot_pairs) {
+                    const float c = csp[j], sv = snp[j];
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float v0 = q8[g][2 * m], v1 = q8[g][2 * m + 1];
+                        rotate_pair(q8[g][2 * m], q8[g][2 * m + 1], v0, v1, c, sv);
+                    }
+                    if (owner) {
+                        const float v0 = kn8[2 * m], v1 = kn8[2 * m + 1];
+                        rotate_pair(kn8[2 * m], kn8[2 * m + 1], v0, v1, c, sv);
+                    }
                 }
             }
         }
-        __syncthreads();
-        for (int e = tid; e < nrows * p.rot_pairs; e += NT) {
-            const int r = e / p.rot_pairs, j = e - r * p.rot_pairs;
-            const int i0 = p.rope_mode == 0 ? 2 * j : j;
-            const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
-            const float c = cs_s[j], sv = sn_s[j];
-            const float v0 = q_s[r][i0], v1 = q_s[r][i1];
-            rotate_pair(q_s[r][i0], q_s[r][i1], v0, v1, c, sv);
-        }
-    }
-    __syncthreads();
-    if (owner) {
-        KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
-        KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
-        if (tid < D) {
-            store_kv(kw + tid, q_s[G][tid]);
-            store_kv(vw + tid, vn_reg);
-        }
-        // The row loads above ran before the append: the newest key and
-        // value come from the prologue instead, rounded as stored.
+        if (owner) {
+            // the fp16 append of the new key and value (one half-wave writes
+            // the row), and the row as stored for the lane that scores it
+            if (w == 0 && sub == 0) {
+                KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off + dl * 8;
+                KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off + dl * 8;
 #pragma unroll
-        for (int b = 0; b < KB; b++) {
-            if (b * KPB + w * KPI + sub == nk - 1) {
-                rk[b] = make_raw<KV>(&q_s[G][dl * 8]);
-                rv[b] = make_raw<KV>(vn8);
+                for (int i = 0; i < 8; i++) {
+                    store_kv(kw + i, kn8[i]);
+                    store_kv(vw + i, vn8[i]);
+                }
+            }
+            // The row loads above ran before the append: the newest key and
+            // value come from the prologue instead, rounded as stored.
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                if (b * KPB + w * KPI + sub == nk - 1) {
+                    rk[b] = make_raw<KV>(kn8);
+                    rv[b] = make_raw<KV>(vn8);
+                }
             }
         }
-    }
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) qr[g][i] = q8[g][i];
+    } else {
+        // ---- q rows (and the owner's key row): RMSNorm + RoPE in one reduction round
+        if (tid < D) {
+#pragma unroll
+            for (int g = 0; g < G; g++) q_s[g][tid] = qv[g];
+            q_s[G][tid] = kn_reg;
+        }
+        const int nrows = owner ? G + 1 : G;
+        if (p.fused) {
+            if (p.q_norm_w != nullptr) {
+                // partial sums in the order of block_sum: per wave, then over the waves
+                float ss[G + 1];
+#pragma unroll
+                for (int r = 0; r <= G; r++) {
+                    const float v = tid < D ? (r < G ? qv[r] : kn_reg) : 0.f;
+                    ss[r] = wave_sum(v * v);
+                }
+                if (lane == 0) {
+#pragma unroll
+                    for (int r = 0; r <= G; r++) red_g[w][r] = ss[r];
+                }
+                __syncthreads();
+                if (tid < D) {
+#pragma unroll
+                    for (int r = 0; r <= G; r++) {
+                        float t = 0.f;
+#pragma unroll
+                        for (int i = 0; i < NW; i++) t += red_g[i][r];
+                        const float inv = 1.0f / sqrtf(t / (float)D + p.eps);
+                        q_s[r][tid] = (q_s[r][tid] * inv) * (r < G ? wq : wk);
+                    }
+                }
+            }
+            __syncthreads();
+            for (int e = tid; e < nrows * p.rot_pairs; e += NT) {
+                const int r = e / p.rot_pairs, j = e - r * p.rot_pairs;
+                const int i0 = p.rope_mode == 0 ? 2 * j : j;
+                const int i1 = p.rope_mode == 0 ? 2 * j + 1 : j + p.rot_pairs;
+                const float c = cs_s[j], sv = sn_s[j];
+                const float v0 = q_s[r][i0], v1 = q_s[r][i1];
+                rotate_pair(q_s[r][i0], q_s[r][i1], v0, v1, c, sv);
+            }
+        }
+        __syncthreads();
+        if (owner) {
+            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
+            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + (size_t)p.new_slot * tok_stride + head_off;
+            if (tid < D) {
+                store_kv(kw + tid, q_s[G][tid]);
+                store_kv(vw + tid, vn_reg);
+            }
+            // The row loads above ran before the append: the newest key and
+            // value come from the prologue instead, rounded as stored.
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                if (b * KPB + w * KPI + sub == nk - 1) {
+                    rk[b] = make_raw<KV>(&q_s[G][dl * 8]);
+                    rv[b] = make_raw<KV>(vn8);
+                }
+            }
+        }
 
-    float qr[G][8];
 #pragma unroll
-    for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
+            for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
+    }
 
     // ---- scores: one transpose reduction over the KB rows of each lane
     {
