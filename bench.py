@@ -34,10 +34,10 @@ HBM_PEAK_GBPS = 8000.0
 MODE_NAMES = {0: "eager launches", 1: "hip graph replay", 6: "persistent kernel, one launch per step"}
 # HBM bytes per launch of the step kernel from rocprofv3 --pmc runs of this
 # script: fetched = 32 x TCC_EA0_RDREQ_32B + 64 x TCC_EA0_RDREQ_64B + 128 x
-# TCC_EA0_RDREQ_128B (summed over the L2 channels) = 2,131,584,499 B; written =
-# WRITE_SIZE x 1024 = 67,002,470 B.  The same counters read 1,073,768,768 B
+# TCC_EA0_RDREQ_128B (summed over the L2 channels) = 2,139,283,283 B; written =
+# WRITE_SIZE x 1024 = 71,560,499 B.  The same counters read 1,073,768,640 B
 # fetched and 1,073,741,824 B written for a 1 GiB device copy in the same runs.
-TRAFFIC = {"step_kernel": 2198586970}
+TRAFFIC = {"step_kernel": 2210843782}
 
 CFG = dict(hidden=2560, inter=9216, layers=32, n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64,
            theta=1e7, eps=1e-6, lin_k_heads=16, lin_v_heads=32, lin_dim=128, ctx=8192)
