@@ -32,7 +32,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxWaves = 16;
 constexpr int kTabBytes = 4096 * 4;
 constexpr int kLutSlots = 64;                          // LUTs staged per round
 constexpr int kLutOff = 2 * kTabBytes;                 // staged LUTs [kLutSlots][64] u16

@@ -109,13 +109,11 @@ extern "C" int anelm_hybrid_step_create(anelm_hybrid_step** out, const anelm_hyb
                   "hybrid_step: mode %d unknown", mode);
     const bool use_graph = mode == ANELM_STEP_GRAPH;
     ANELM_REQUIRE(!use_graph || stream != nullptr, "hybrid_step: graph capture needs a non-null stream");
-    bool any_proj = false;
     for (int i = 0; i < n_layers; i++) {
         const anelm_hybrid_layer& L = layers[i];
         ANELM_REQUIRE(L.kind == ANELM_LAYER_ATTENTION || L.kind == ANELM_LAYER_DELTANET,
                       "hybrid_step: layer %d kind %d", i, L.kind);
         if (!L.first_w) continue;
-        any_proj = true;
         ANELM_REQUIRE(L.first_lut && L.o_w && L.o_lut && L.proj,
                       "hybrid_step: layer %d has a first projection but no o_proj / proj scratch", i);
         ANELM_REQUIRE(L.kind == ANELM_LAYER_ATTENTION ||
