@@ -67,6 +67,8 @@ struct DecodeParams {
     const float* rope_tab;
     int rope_rows;
     float theta;
+    // paged: the q rows after the prologue kernel, fp16 [seq][Hkv][G][D]
+    const uint16_t* q_prep;
 };
 
 template <typename KV> struct Raw8;
@@ -115,15 +117,6 @@ template <> __device__ __forceinline__ Raw8<float> make_raw<float>(const float* 
 
 __device__ __forceinline__ void store_kv(uint16_t* p, float v) { *p = f2h(v); }
 __device__ __forceinline__ void store_kv(float* p, float v) { *p = v; }
-
-// fp16 pair (lo, hi) and its dot product with another pair, accumulated in fp32
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
-    return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
-}
-__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c, false);
-}
 
 // RMSNorm (cpu_ops.cpp:24-30) + RoPE (cpu_ops.cpp:40-63) of one D-vector held
 // in shared memory, in place.  All threads participate.
@@ -722,361 +715,353 @@ __global__ __launch_bounds__(ring_threads<G>()) void attn_decode_kernel(const De
     }
 }
 
-// Paged decode over many sequences: a workgroup owns kPagedChunks chunks of
-// 256/G keys of one (sequence, kv head) and walks them one after the other
-// (online softmax across chunks: running maximum per head, rescaled sums).
-// The split's page-table entries are read once into LDS.  Fewer, longer
-// splits than the ring path also shrink the partial records 4x.
-constexpr int kPagedChunks = 4;
+// ---- paged decode on the matrix cores (fp16 pages)
+//
+// A workgroup owns kPagedSplit keys of one (sequence, kv head); each of its 4
+// waves walks its own 16-key blocks (block b of the split goes to wave b % 4)
+// with its own online softmax, and the waves merge by log-sum-exp at the end.
+// Per block, with lane l = 16 q + n:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_f16 over D/32 steps: A = K rows (lane
+//                 holds key n, dims 32 s + 8 q .. +8), B = Q^T (lane holds q
+//                 head n < G, the same dims; zero columns for n >= G).  Lane
+//                 (q, n) ends with the scores of head n for keys 4 q .. 4 q + 3.
+//   softmax       per head column: running maximum over the four lanes of the
+//                 column, weights rounded to fp16 -- already the A operand of
+//                 P V (lane (q, n) holds P[head n][keys 4 q .. 4 q + 3]).
+//   O += P V      v_mfma_f32_16x16x16f16 per 16-dim tile t: B = V[keys 4 q ..
+//                 4 q + 3][dim 16 t + n], read from the wave's LDS copy of the
+//                 block's V rows with ds_read_b64_tr_b16 (a 16-lane group whose
+//                 lanes address 4 keys x 16 dims, 8 bytes each, receives the
+//                 4 x 16 block transposed: lane n gets dim n of the 4 keys).
+// The V rows reach LDS by direct global-to-LDS loads (16 bytes per lane:
+// key n, dims 8 (4 i + q) .. +8 of instruction i land at byte (16 (4 i + q) +
+// n) * 16 of the wave's block), the K rows go to registers; both are issued
+// together, K first.  Output rows of heads >= G are computed and dropped.
+constexpr int kPagedSplit = 256;   // keys per workgroup
+constexpr int kPagedBlk = 16;      // keys per wave block
 
-template <typename KV, int D, int G>
-__global__ __launch_bounds__(kNT) void attn_paged_kernel(const DecodeParams p) {
-    constexpr int LPK = D / 8;        // lanes per key row (8 elements each)
-    constexpr int KPI = 64 / LPK;     // key rows per wave instruction
-    constexpr int KPB = kNW * KPI;    // key rows per workgroup instruction
-    constexpr int KB = LPK / G;       // instructions per chunk
-    constexpr int CK = KPB * KB;      // keys per chunk (= 256 / G)
-    constexpr int KPS = CK * kPagedChunks;
-    constexpr int REC = D + 2;
-    static_assert(KB >= 1 && KB * G == LPK, "G must divide D/8");
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
-    __shared__ __attribute__((aligned(16))) float sc_w[kNW][64];   // each wave's softmax weights of a chunk
+// cos / sin of RoPE pair j at position pos: the table row, or past the table
+// the formula of cpu_ops.cpp:51-55
+__device__ __forceinline__ void rope_cs(const DecodeParams& p, int pos, bool in_tab, int j, float& c, float& s) {
+    const int R = p.rot_pairs;
+    if (in_tab) {
+        c = p.rope_tab[(size_t)pos * 2 * R + j];
+        s = p.rope_tab[(size_t)pos * 2 * R + R + j];
+    } else {
+        const float freq = 1.0f / powf(p.theta, (float)(2 * j) / (float)(2 * R));
+        const float angle = (float)pos * freq;
+        c = cosf(angle);
+        s = sinf(angle);
+    }
+}
+
+// Inclusive prefix sum of v over the workgroup's kNT threads through s[kNT]
+// (s[kNT - 1] then holds the total; every thread's s reads are done before
+// the next call writes s).
+__device__ int block_scan_int(int v, int* s) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+    s[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < kNT; off <<= 1) {
+        const int a = tid >= off ? s[tid - off] : 0;
+        __syncthreads();
+        s[tid] += a;
+        __syncthreads();
+    }
+    return s[tid];
+}
+
+// Paged-step prologue, one workgroup per (kv head, sequence): the G q rows
+// normalised and rotated (models/llm/qwen3_5.cpp:952-986 for the sequence:
+// q/k RMSNorm, RoPE at its position -- the table row, or past the table the
+// formula of cpu_ops.cpp:51-55), stored as fp16 for the attention kernel;
+// fused, also the new key (normalised, rotated) and value appended to their
+// pages as fp16.  Unfused: the q rows converted as given.
+template <int D, int G>
+__global__ __launch_bounds__(kNT) void attn_paged_prep_kernel(const DecodeParams p, uint16_t* qh) {
+    __shared__ float q_s[G + 1][D];   // the q rows, then the new key
     __shared__ float red_g[kNW][G];
-    __shared__ float red_m[kNW][G];
-    __shared__ float red_o[kNW][G][D];
-    __shared__ int pg[KPS + 1];   // page-table entries of the split (any page size)
-    // fused step only: q rows and the new key after norm + RoPE, RoPE row
-    __shared__ float q_s[G][D];
-    __shared__ float kn_s[D];
     __shared__ float red[kNW];
     __shared__ float rope_s[2][kMaxRotPairs];
+    const int kvh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
+    const int Hkv = p.n_kv_heads;
+    const float* qk = p.q + ((size_t)seq * Hkv + kvh) * G * p.q_stride;
+    uint16_t* const dst = qh + ((size_t)seq * Hkv + kvh) * G * D;
+    for (int e = tid; e < G * D; e += kNT) q_s[e / D][e % D] = qk[(size_t)(e / D) * p.q_stride + e % D];
+    if (!p.fused) {
+        __syncthreads();
+        for (int e = tid; e < G * D; e += kNT) dst[e] = f2h(q_s[e / D][e % D]);
+        return;
+    }
+    const int cached = p.seq_lens[seq];
+    const bool append = cached >= 0 && cached < p.len;   // the new key is attended (and stored)
+    const int pos = p.positions ? p.positions[seq] : cached;
+    const bool in_tab = p.rope_tab != nullptr && pos >= 0 && pos < p.rope_rows;
+    for (int j = tid; j < p.rot_pairs; j += kNT) rope_cs(p, pos, in_tab, j, rope_s[0][j], rope_s[1][j]);
+    __syncthreads();
+    norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, rope_s[0], rope_s[1]);
+    for (int e = tid; e < G * D; e += kNT) dst[e] = f2h(q_s[e / D][e % D]);
+    if (!append) return;   // (uniform)
+    const size_t nrow = ((size_t)seq * Hkv + kvh) * D;
+    for (int d = tid; d < D; d += kNT) q_s[G][d] = p.k_new[nrow + d];
+    __syncthreads();
+    norm_rope_row<D>(q_s[G], p.k_norm_w, p, red, rope_s[0], rope_s[1]);
+    const int ps = p.page_size;
+    const int page = min(max(p.page_table[(size_t)seq * p.max_pages + cached / ps], 0), p.n_pages - 1);
+    const size_t off = (((size_t)page * Hkv + kvh) * ps + cached % ps) * D;
+    uint16_t* const kw = reinterpret_cast<uint16_t*>(p.k_cache_w) + off;
+    uint16_t* const vw = reinterpret_cast<uint16_t*>(p.v_cache_w) + off;
+    for (int d = tid; d < D; d += kNT) {
+        kw[d] = f2h(q_s[G][d]);
+        vw[d] = f2h(p.v_new[nrow + d]);
+    }
+}
 
-    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+template <int D, int G>
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3))) void attn_paged_mfma_kernel(const DecodeParams p) {
+    constexpr int KS = D / 32;                // QK steps of 32 dims (also V load instructions)
+    constexpr int NTD = D / 16;               // P V tiles of 16 dims
+    constexpr int VB = kPagedBlk * D * 2;     // bytes of a wave's V block
+    constexpr int KPS = kPagedSplit;
+    constexpr int REC = D + 2;
+    static_assert(G <= 8 && KS >= 2, "heads per kv head <= 8, head_dim >= 64");
+    static_assert(G * D * 4 <= VB, "O rows fit in the wave's block");
+    // per wave: the V block; after a run's blocks, the wave's O rows [G][D]
+    __shared__ __attribute__((aligned(16))) char vblk[kNW][VB];
+    __shared__ float red_g[kNW][G];
+    __shared__ float red_m[kNW][G];
+    __shared__ int scan_s[kNT];
+
     const int Hkv = p.n_kv_heads;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
-    const int sub = lane / LPK, dl = lane % LPK;
-    // fused: the sequence's new token is key `cached` and is attended too
-    const int cached = p.seq_lens[seq];
-    const int len = p.fused ? min(cached + 1, p.len) : min(cached, p.len);
-    float* out = p.out + (size_t)seq * Hkv * G * D;
-    if (len <= 0) {   // empty sequence: zeros, as cpu_ops.cpp:152-155
-        if (split == 0)
-            for (int e = tid; e < G * D; e += kNT) out[(size_t)kvh * G * D + e] = 0.f;
-        return;
-    }
-    const int n_splits = (len + KPS - 1) / KPS;
-    if (split >= n_splits) return;   // (uniform: before any barrier)
-    const int k0 = split * KPS, nk_all = min(KPS, len - k0);
-    const int nch = (nk_all + CK - 1) / CK;
-    const float* q = p.q + (size_t)seq * Hkv * G * p.q_stride;
+    const int w = tid >> 6;
+    const int NWG = gridDim.x, wg = blockIdx.x;
+    // keys of sequence s: its cached keys, and (fused) the new one
+    auto seq_len = [&](int s) {
+        const int c = p.seq_lens[s];
+        return p.fused ? min(c + 1, p.len) : min(c, p.len);
+    };
+    auto units_of = [&](int L) { return L > 0 ? Hkv * ((L + KPS - 1) / KPS) : 0; };
 
-    const int ps = p.page_size;
-    const int pfirst = k0 / ps, pcount = (k0 + nk_all - 1) / ps - pfirst + 1;
-    const int32_t* ptab = p.page_table + (size_t)seq * p.max_pages;
-    for (int i = tid; i < pcount; i += kNT) pg[i] = min(max(ptab[pfirst + i], 0), p.n_pages - 1);
-    float qr[G][8];
-    // fused: local index of the new key in this split (-1: another split's)
-    const int t_new = p.fused && cached >= k0 && cached < k0 + nk_all ? cached - k0 : -1;
-    if (p.fused) {
-        // models/llm/qwen3_5.cpp:952-986 for this sequence: q/k RMSNorm, RoPE
-        // at the token's position (the table row, or the same formula as
-        // cpu_ops.cpp:51-55 past the table), fp16 append into the page
-        const int pos = p.positions ? p.positions[seq] : cached;
-        for (int j = tid; j < p.rot_pairs; j += kNT) {
-            if (p.rope_tab != nullptr && pos >= 0 && pos < p.rope_rows) {
-                rope_s[0][j] = p.rope_tab[(size_t)pos * 2 * p.rot_pairs + j];
-                rope_s[1][j] = p.rope_tab[(size_t)pos * 2 * p.rot_pairs + p.rot_pairs + j];
-            } else {
-                const float freq = 1.0f / powf(p.theta, (float)(2 * j) / (float)(2 * p.rot_pairs));
-                const float angle = (float)pos * freq;
-                rope_s[0][j] = cosf(angle);
-                rope_s[1][j] = sinf(angle);
-            }
-        }
-        for (int e = tid; e < G * D; e += kNT) q_s[e / D][e % D] = q[(size_t)(kvh * G + e / D) * p.q_stride + e % D];
+    // ---- this workgroup's units: the (sequence, kv head, split) units in
+    // sequence-major order, U in all, split evenly over the NWG workgroups
+    // (every workgroup scans the lengths; empty sequences get zeros here)
+    int U = 0;
+    for (int c0 = 0; c0 < p.n_seqs; c0 += kNT) {
+        const int s = c0 + tid;
+        block_scan_int(s < p.n_seqs ? units_of(seq_len(s)) : 0, scan_s);
+        U += scan_s[kNT - 1];
+    }
+    for (int s = wg; s < p.n_seqs; s += NWG) {   // empty sequences: zeros, as cpu_ops.cpp:152-155
+        if (seq_len(s) > 0) continue;
+        float* o0 = p.out + (size_t)s * Hkv * G * D;
+        for (int e = tid; e < Hkv * G * D; e += kNT) o0[e] = 0.f;
+    }
+    const int u0 = (int)(((long long)U * wg) / NWG), u1 = (int)(((long long)U * (wg + 1)) / NWG);
+    if (u0 >= u1) return;   // (uniform)
+    // the sequence holding unit u0 and the units before it
+    int seq = 0, ubase = 0;
+    for (int c0 = 0; c0 < p.n_seqs; c0 += kNT) {
+        const int s = c0 + tid;
+        const int us = s < p.n_seqs ? units_of(seq_len(s)) : 0;
+        const int incl = block_scan_int(us, scan_s);   // inclusive, chunk-local
+        const int total = scan_s[kNT - 1];
+        // the thread whose range [ubase + incl - us, ubase + incl) holds u0
+        const int lo = ubase + incl - us;
         __syncthreads();
-        norm_rope_rows<D, G>(q_s, p.q_norm_w, p, red_g, rope_s[0], rope_s[1]);
-        if (t_new >= 0) {
-            const size_t nrow = ((size_t)seq * Hkv + kvh) * D;
-            for (int d = tid; d < D; d += kNT) kn_s[d] = p.k_new[nrow + d];
-            __syncthreads();
-            norm_rope_row<D>(kn_s, p.k_norm_w, p, red, rope_s[0], rope_s[1]);
-            const int page = pg[cached / ps - pfirst], row = cached % ps;
-            const size_t off = (((size_t)page * Hkv + kvh) * ps + row) * D;
-            KV* kw = reinterpret_cast<KV*>(p.k_cache_w) + off;
-            KV* vw = reinterpret_cast<KV*>(p.v_cache_w) + off;
-            for (int d = tid; d < D; d += kNT) {
-                store_kv(kw + d, kn_s[d]);
-                store_kv(vw + d, p.v_new[nrow + d]);
-            }
+        if (s < p.n_seqs && us > 0 && u0 >= lo && u0 < lo + us) scan_s[0] = s, scan_s[1] = lo;
+        __syncthreads();
+        const bool found = u0 < ubase + total;
+        if (found) {
+            seq = scan_s[0];
+            ubase = scan_s[1];
         }
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) qr[g][i] = q_s[g][dl * 8 + i];
-    } else {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float* src = q + (size_t)(kvh * G + g) * p.q_stride + dl * 8;
-#pragma unroll
-            for (int i = 0; i < 8; i++) qr[g][i] = src[i];
-        }
+        __syncthreads();
+        if (found) break;
+        ubase += total;
     }
-    // fp16 caches: q as fp16 pairs, so scores are packed fp16 dot products
-    // with fp32 accumulation (fp16 inputs, as the cache itself)
-    constexpr bool kHalf = std::is_same<KV, uint16_t>::value;
-    uint32_t qh[G][4];
-    if constexpr (kHalf) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) qh[g][j] = pack_half2(qr[g][2 * j], qr[g][2 * j + 1]);
-    }
-    lds_barrier();
 
-    const KV* kc = reinterpret_cast<const KV*>(p.k_cache);
-    const KV* vc = reinterpret_cast<const KV*>(p.v_cache);
-    // rows past the split's last key load that key again (masked below): the
-    // loads stay unconditional, so the counted waits stay exact.  A key's K
-    // and V rows sit at the same offset of their caches.  The chunk's page
-    // entries are all read from LDS before any address is formed (one wait),
-    // a power-of-two page size takes shifts instead of divisions, and row
-    // indices stay 32-bit (the host bounds the cache to 2^31 rows).
-    const int ps_shift = (ps & (ps - 1)) == 0 ? __builtin_ctz((unsigned)ps) : -1;
-    const unsigned rows_per_page = (unsigned)(Hkv * ps), head_row = (unsigned)(kvh * ps);
-    auto load_rows = [&](int c, Raw8<KV> (&rk)[KB], Raw8<KV> (&rv)[KB]) __attribute__((always_inline)) {
-        c = min(c, nch - 1);   // (past the last chunk: reload it, unused)
-        unsigned kt[KB], page[KB], row[KB];
-#pragma unroll
-        for (int b = 0; b < KB; b++)   // key index inside the sequence
-            kt[b] = (unsigned)(k0 + min(c * CK + b * KPB + w * KPI + sub, nk_all - 1));
-        if (ps_shift >= 0) {
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                page[b] = (unsigned)pg[(int)(kt[b] >> ps_shift) - pfirst];
-                row[b] = kt[b] & (unsigned)(ps - 1);
-            }
-        } else {
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                const unsigned pi = kt[b] / (unsigned)ps;
-                page[b] = (unsigned)pg[(int)pi - pfirst];
-                row[b] = kt[b] - pi * (unsigned)ps;
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < KB; b++) {
-            const size_t off = (size_t)(page[b] * rows_per_page + head_row + row[b]) * D + dl * 8;
-            rk[b] = load_raw(kc + off);
-            rv[b] = load_raw(vc + off);
-        }
-    };
+    const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.k_cache);
+    const uint16_t* vc = reinterpret_cast<const uint16_t*>(p.v_cache);
+    const int ps = p.page_size;
+    const unsigned rows_per_page = (unsigned)(Hkv * ps);
+    char* const vb = vblk[w];
 
-    // Online softmax per wave: a wave keeps its own running maximum per head
-    // and sums over the keys it holds (rows t = b*KPB + w*KPI + sub of each
-    // chunk), so the chunk loop has no workgroup barrier and a wave waiting
-    // on its rows holds up no other; the waves' states are merged once at the
-    // end by log-sum-exp.  After the transpose reduction lane (sub, dl) holds
-    // the score of row b = dl / G for head g = dl % G = lane % G.
-    float m[G], acc[G][8];
-    float lsum = 0.f;   // this lane's share of the sum for its head lane % G
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        m[g] = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[g][i] = 0.f;
-    }
-    float* pw = sc_w[w];
-    const int g_own = dl % G;
-    auto chunk = [&](int c, const Raw8<KV> (&rk)[KB], const Raw8<KV> (&rv)[KB]) __attribute__((always_inline)) {
-        const int nk = min(CK, nk_all - c * CK);
-        // ---- scores: one transpose reduction over the KB rows of each lane
-        float s_own;
-        {
-            float part[KB * G];
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                if constexpr (kHalf) {
-                    const uint32_t kw[4] = {rk[b].a.x, rk[b].a.y, rk[b].a.z, rk[b].a.w};
-#pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        float sv = 0.f;
-#pragma unroll
-                        for (int j = 0; j < 4; j++) sv = dot2_acc(qh[g][j], kw[j], sv);
-                        part[b * G + g] = sv;
-                    }
-                } else {
-                    float kf[8];
-                    to_f32(rk[b], kf);
-#pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        float sv = 0.f;
-#pragma unroll
-                        for (int i = 0; i < 8; i++) sv = fmaf(qr[g][i], kf[i], sv);
-                        part[b * G + g] = sv;
-                    }
-                }
-            }
-            transpose_reduce<LPK, KB * G>(part, dl);
-            const int t = (dl / G) * KPB + w * KPI + sub;
-            s_own = t < nk ? part[0] * p.scale : -INFINITY;
+    // ---- runs: the units of one (sequence, kv head) taken together, keys
+    // [s0 KPS, min((s1 + 1) KPS, L)) with one online softmax
+    int u = u0;
+    while (u < u1) {
+        // lane quantities are derived here, per run, not held across runs
+        int lane = tid & 63;
+        asm volatile("" : "+v"(lane));
+        const int q = lane >> 4, n = lane & 15;
+        // transposed reads: lane n of group q addresses key 4 q + n/4, dims
+        // 16 t + 4 (n % 4) .. +4 of tile t
+        const int tr_off = (16 * ((n & 3) >> 1) + 4 * q + (n >> 2)) * 16 + (n & 1) * 8;
+        const int L = seq_len(seq);
+        const int ns = L > 0 ? (L + KPS - 1) / KPS : 0;
+        if (u >= ubase + Hkv * ns) {   // (uniform) next sequence
+            ubase += Hkv * ns;
+            seq++;
+            continue;
         }
-        // ---- running maximum per head over the wave's keys (exact XOR
-        // partners keep the lanes of one head together)
-        float mx = s_own;
+        const int local = u - ubase, kvh = local / ns, s0 = local - kvh * ns;
+        const int s1 = min(ns - 1, s0 + (u1 - u) - 1);
+        u += s1 - s0 + 1;
+        const int k0 = s0 * KPS, kend = min((s1 + 1) * KPS, L), nk_all = kend - k0;
+        const unsigned k_last = (unsigned)(kend - 1);
+        const int nblk = (nk_all + kPagedBlk - 1) / kPagedBlk;
+        const float* qseq = p.q + (size_t)seq * Hkv * G * p.q_stride;
+        const int32_t* ptab = p.page_table + (size_t)seq * p.max_pages;
+        const unsigned head_row = (unsigned)(kvh * ps);
+
+        // q (normalised, rotated, fp16: the prologue kernel's rows) as the B
+        // operand of S^T = K Q^T: lane (q, n) holds head n, dims 32 s + 8 q
+        // .. +8 (zero columns past the G heads)
+        const uint16_t* qrow = p.q_prep + (((size_t)seq * Hkv + kvh) * G + min(n, G - 1)) * D;
+        half8_t qb[KS];
 #pragma unroll
-        for (int mm = G; mm < 64; mm <<= 1) mx = fmaxf(mx, shfl_xor(mx, mm));
-        float alpha_own = 0.f, m_own = 0.f;
+        for (int s = 0; s < KS; s++) {
+            qb[s] = *reinterpret_cast<const half8_t*>(qrow + 32 * s + 8 * q);
+            if (n >= G) qb[s] = half8_t{};
+        }
+
+        // ---- the run's 16-key blocks, block b to wave b % 4; key n of a
+        // block (past the run's last key: that key again, masked) through its
+        // page-table entry, the next block's entry requested a block ahead
+        f32x4_t o[NTD];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), g));
-            const float m_new = fmaxf(m[g], mc);
+        for (int t = 0; t < NTD; t++) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.f;   // head n of this wave
+        auto key_of = [&](int blk) { return min((unsigned)(k0 + blk * kPagedBlk + n), k_last); };
+        auto entry = [&](unsigned kt) { return ptab[kt / (unsigned)ps]; };
+        int pe = entry(key_of(w));
+        for (int blk = w; blk < nblk; blk += kNW) {
+            const unsigned kt = key_of(blk);
+            const unsigned pi = kt / (unsigned)ps;
+            const unsigned page = (unsigned)min(max(pe, 0), p.n_pages - 1);
+            const size_t base = (size_t)(page * rows_per_page + head_row + (kt - pi * (unsigned)ps)) * D;
+            pe = entry(key_of(blk + kNW));
+            half8_t ka[KS];
+#pragma unroll
+            for (int s = 0; s < KS; s++) ka[s] = *reinterpret_cast<const half8_t*>(kc + base + 32 * s + 8 * q);
+            // the V rows straight into the wave's LDS block: key n, dims
+            // 8 (4 i + q) .. +8 at byte (16 (4 i + q) + n) * 16
+#pragma unroll
+            for (int i = 0; i < KS; i++)
+                __builtin_amdgcn_global_load_lds(vc + base + 8 * (4 * i + q), (lds_void_ptr)(vb + i * 1024), 16, 0, 0);
+            f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < KS; s++) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], qb[s], st, 0, 0, 0);
+            // ---- online softmax of head n over keys 4 q + i of the block
+            float sc[4], bm = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = blk * kPagedBlk + 4 * q + i;
+                sc[i] = t < nk_all ? st[i] * p.scale : -INFINITY;
+                bm = fmaxf(bm, sc[i]);
+            }
+            bm = fmaxf(bm, partner<32>(bm));
+            bm = fmaxf(bm, partner<16>(bm));
+            const float m_new = fmaxf(m_run, bm);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no valid key yet: weights 0
-            const float alpha = __expf(m[g] - m_use);              // 0 while m is -inf
+            const float alpha = __expf(m_run - m_use);              // 0 while m_run is -inf
+            half4_t pa;
+            float psum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc[g][i] *= alpha;
-            m[g] = m_new;
-            if (g == g_own) {
-                alpha_own = alpha;
-                m_own = m_use;
+            for (int i = 0; i < 4; i++) {
+                const float e = __expf(sc[i] - m_use);   // masked keys: 0
+                psum += e;
+                pa[i] = (_Float16)e;
             }
-        }
-        const float e = __expf(s_own - m_own);   // masked keys: exp(-inf) = 0
-        lsum = lsum * alpha_own + e;
-        // the weights back in row order through the wave's own LDS (a wave's
-        // LDS accesses execute in order: no barrier)
-        pw[lane] = e;
-        float pv[KB * G];
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            // O row 4 q + i is head 4 q + i: its factor is that column's alpha
+            if (__any(n < G && alpha != 1.f)) {
 #pragma unroll
-        for (int k = 0; k < KB * G / 4; k++) {
-            const float4 v4 = *reinterpret_cast<const float4*>(pw + sub * LPK + 4 * k);
-            pv[4 * k] = v4.x;
-            pv[4 * k + 1] = v4.y;
-            pv[4 * k + 2] = v4.z;
-            pv[4 * k + 3] = v4.w;
-        }
-        // ---- P V (fp16 caches: two key rows per packed dot product, the
-        // weights rounded to fp16 pairs and the rows' values interleaved)
-        constexpr int KP = kHalf ? KB / 2 : 0;
-        if constexpr (kHalf) {
+                for (int i = 0; i < 4; i++) {
+                    const float ai = __shfl(alpha, 4 * q + i, 64);
 #pragma unroll
-            for (int j = 0; j < KP; j++) {
-                const uint32_t va[4] = {rv[2 * j].a.x, rv[2 * j].a.y, rv[2 * j].a.z, rv[2 * j].a.w};
-                const uint32_t vb[4] = {rv[2 * j + 1].a.x, rv[2 * j + 1].a.y, rv[2 * j + 1].a.z,
-                                        rv[2 * j + 1].a.w};
-                uint32_t vp[8];   // (row 2j, row 2j+1) of dims 2k and 2k+1
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    vp[2 * k] = __builtin_amdgcn_perm(vb[k], va[k], 0x05040100u);
-                    vp[2 * k + 1] = __builtin_amdgcn_perm(vb[k], va[k], 0x07060302u);
-                }
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const uint32_t pp = pack_half2(pv[(2 * j) * G + g], pv[(2 * j + 1) * G + g]);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) acc[g][i] = dot2_acc(pp, vp[i], acc[g][i]);
+                    for (int t = 0; t < NTD; t++) o[t][i] *= ai;
                 }
             }
-        }
+            // ---- O += P V, V^T tiles from the block in LDS
 #pragma unroll
-        for (int b = 2 * KP; b < KB; b++) {
-            float vf[8];
-            to_f32(rv[b], vf);
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float pgv = pv[b * G + g];
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc[g][i] = fmaf(pgv, vf[i], acc[g][i]);
+            for (int t = 0; t < NTD; t++) {
+                const s16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_t*)(vb + t * 512 + tr_off));
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, vt), o[t], 0, 0, 0);
             }
         }
-    };
 
-    // one chunk's rows in registers at a time (several workgroups per CU hide
-    // each other's load latency)
-    for (int c = 0; c < nch; c++) {
-        Raw8<KV> rk[KB], rv[KB];
-        load_rows(c, rk, rv);
-        if (t_new >= 0 && c == t_new / CK) {
-            // the new key's row was loaded before (or while) it was stored:
-            // take it from the prologue, rounded as stored
-#pragma unroll
-            for (int b = 0; b < KB; b++) {
-                if (c * CK + b * KPB + w * KPI + sub == t_new) {
-                    rk[b] = make_raw<KV>(kn_s + dl * 8);
-                    rv[b] = make_raw<KV>(p.v_new + ((size_t)seq * Hkv + kvh) * D + dl * 8);
-                }
-            }
+        // ---- merge the waves: per head M = max of the waves' maxima, each
+        // wave weighed by e^(m_w - M); one record for the run's first split
+        // (the rest of its splits marked empty), or the output itself when
+        // the sequence has one split
+        float lt = l_run;
+        lt += partner<32>(lt);
+        lt += partner<16>(lt);
+        if (lane < G) {
+            red_m[w][lane] = m_run;
+            red_g[w][lane] = lt;
         }
-        chunk(c, rk, rv);
-    }
-
-    // ---- merge the waves: per head M = max of the waves' maxima, each wave
-    // weighed by e^(m_w - M); O summed over the lanes sharing dims first
-    float lw[G];
-    {
-        float l = lsum;
+        float* ro = reinterpret_cast<float*>(vb);   // this wave's O rows [G][D]
 #pragma unroll
-        for (int mm = G; mm < 64; mm <<= 1) l += shfl_xor(l, mm);
+        for (int t = 0; t < NTD; t++)
 #pragma unroll
-        for (int g = 0; g < G; g++) lw[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), g));
-    }
-    if (lane == 0) {
+            for (int i = 0; i < 4; i++)
+                if (4 * q + i < G) ro[(4 * q + i) * D + 16 * t + n] = o[t][i];
+        __syncthreads();
+        float mtot[G], ltot[G], wsc[G][kNW];
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            red_g[w][g] = lw[g];
-            red_m[w][g] = m[g];
+            float M = red_m[0][g];
+#pragma unroll
+            for (int ww = 1; ww < kNW; ww++) M = fmaxf(M, red_m[ww][g]);
+            const float Mu = M == -INFINITY ? 0.f : M;
+            mtot[g] = M;
+            ltot[g] = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < kNW; ww++) {
+                wsc[g][ww] = __expf(red_m[ww][g] - Mu);   // a wave without valid keys: 0
+                ltot[g] += red_g[ww][g] * wsc[g][ww];
+            }
         }
-    }
-#pragma unroll
-    for (int mm = LPK; mm < 64; mm <<= 1)
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc[g][i] += shfl_xor(acc[g][i], mm);
-    if (sub == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) red_o[w][g][dl * 8 + i] = acc[g][i];
-    }
-    lds_barrier();
-    float mtot[G], ltot[G], wsc[G][kNW];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float M = red_m[0][g];
-#pragma unroll
-        for (int ww = 1; ww < kNW; ww++) M = fmaxf(M, red_m[ww][g]);
-        const float Mu = M == -INFINITY ? 0.f : M;
-        mtot[g] = M;
-        ltot[g] = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < kNW; ww++) {
-            wsc[g][ww] = __expf(red_m[ww][g] - Mu);   // a wave without valid keys: 0
-            ltot[g] += red_g[ww][g] * wsc[g][ww];
-        }
-    }
-    if (n_splits == 1) {
+        float* const outs = p.out + (size_t)seq * Hkv * G * D;
+        float* const recs = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * G * REC;
         for (int e = tid; e < G * D; e += kNT) {
             const int g = e / D, d = e % D;
-            float o = 0.f;
+            float o2 = 0.f;
 #pragma unroll
-            for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d] * wsc[g][ww];
-            const int hq = kvh * G + g;
-            float yv = o / ltot[g];
-            if (p.gate) yv = yv / (1.0f + expf(-q[(size_t)hq * p.q_stride + D + d]));
-            out[(size_t)hq * D + d] = yv;
+            for (int ww = 0; ww < kNW; ww++) o2 += reinterpret_cast<const float*>(vblk[ww])[e] * wsc[g][ww];
+            if (ns == 1) {
+                const int hq = kvh * G + g;
+                float yv = o2 / ltot[g];
+                if (p.gate) yv = yv / (1.0f + expf(-qseq[(size_t)hq * p.q_stride + D + d]));
+                outs[(size_t)hq * D + d] = yv;
+            } else {
+                float* rec = recs + ((size_t)s0 * G + g) * REC;
+                rec[2 + d] = o2;
+                if (d == 0) {
+                    rec[0] = mtot[g];
+                    rec[1] = ltot[g];
+                }
+            }
         }
-        return;
-    }
-    float* rec = p.part + (((size_t)seq * Hkv + kvh) * p.max_splits + split) * G * REC;
-    for (int e = tid; e < G * D; e += kNT) {
-        const int g = e / D, d = e % D;
-        float o = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < kNW; ww++) o += red_o[ww][g][d] * wsc[g][ww];
-        rec[(size_t)g * REC + 2 + d] = o;
-        if (d == 0) { rec[(size_t)g * REC] = mtot[g]; rec[(size_t)g * REC + 1] = ltot[g]; }
+        // the run's other splits: empty records (l = 0: the merge skips them)
+        for (int e = tid; e < (s1 - s0) * G; e += kNT) {
+            float* rec = recs + ((size_t)(s0 + 1 + e / G) * G + e % G) * REC;
+            rec[0] = -INFINITY;
+            rec[1] = 0.f;
+        }
+        __syncthreads();   // (LDS reused by the next run)
     }
 }
 
@@ -1118,14 +1103,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p)
         }
         L += block_sum<256>(lpart, red);   // (its barriers also publish f)
         int s = grp;
-        for (; s + 12 < cn; s += 16) {
-            const float o0 = base[(size_t)(c0 + s) * rs + 2 + d];
-            const float o1 = base[(size_t)(c0 + s + 4) * rs + 2 + d];
-            const float o2 = base[(size_t)(c0 + s + 8) * rs + 2 + d];
-            const float o3 = base[(size_t)(c0 + s + 12) * rs + 2 + d];
-            O += f[s] * o0 + f[s + 4] * o1 + f[s + 8] * o2 + f[s + 12] * o3;
-        }
-        for (; s < cn; s += 4) O += f[s] * base[(size_t)(c0 + s) * rs + 2 + d];
+        // (an empty record, l = 0, weighs 0 and its o is never read)
+        auto term = [&](int si) {
+            return f[si] != 0.f ? f[si] * base[(size_t)(c0 + si) * rs + 2 + d] : 0.f;
+        };
+        for (; s + 12 < cn; s += 16) O += term(s) + term(s + 4) + term(s + 8) + term(s + 12);
+        for (; s < cn; s += 4) O += term(s);
         __syncthreads();
     }
     osum[grp][dq] = O;
@@ -1141,8 +1124,29 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p)
 template <typename KV, int D, int G>
 int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
     if (p.paged) {
-        hipLaunchKernelGGL((attn_paged_kernel<KV, D, G>), grid, dim3(kNT), 0, st, p);
-        ANELM_LAUNCHED("attn_paged_kernel");
+        if constexpr (!std::is_same<KV, uint16_t>::value || D < 64) {
+            return set_error(ANELM_EINVAL, "paged decode: fp16 pages of head_dim >= 64 only");
+        } else {
+            // as many workgroups as are resident at once, each with an even
+            // share of the units (the kernel divides them)
+            static int per_cu = 0;
+            if (per_cu == 0) {
+                int nb = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, attn_paged_mfma_kernel<D, G>, kNT, 0) !=
+                        hipSuccess ||
+                    nb < 1)
+                    nb = 1;
+                per_cu = nb;
+            }
+            Device* dev = device();
+            if (dev == nullptr) return ANELM_EHIP;
+            hipLaunchKernelGGL((attn_paged_prep_kernel<D, G>), dim3(p.n_kv_heads, p.n_seqs), dim3(kNT), 0, st, p,
+                               const_cast<uint16_t*>(p.q_prep));
+            ANELM_LAUNCHED("attn_paged_prep_kernel");
+            const dim3 pgrid(std::max(1, per_cu * dev->num_cus));
+            hipLaunchKernelGGL((attn_paged_mfma_kernel<D, G>), pgrid, dim3(kNT), 0, st, p);
+            ANELM_LAUNCHED("attn_paged_mfma_kernel");
+        }
     } else {
         hipLaunchKernelGGL((attn_decode_kernel<KV, D, G>), grid, dim3(ring_threads<G>()), 0, st, p);
         ANELM_LAUNCHED("attn_decode_kernel");
@@ -1179,7 +1183,7 @@ int launch_kv(DecodeParams& p, int D, int G, dim3 grid, hipStream_t st) {
 // Bytes of split partials one decode call needs (0 when one split suffices).
 size_t part_bytes(int n_heads, int n_kv_heads, int D, int n_seqs, int max_len, bool paged) {
     const int G = n_heads / n_kv_heads;
-    const int kps = (256 / G) * (paged ? kPagedChunks : 1);
+    const int kps = paged ? kPagedSplit : 256 / G;
     const int max_splits = (max_len + kps - 1) / kps;
     if (max_splits <= 1) return 0;
     return (size_t)n_seqs * n_kv_heads * max_splits * G * (D + 2) * sizeof(float);
@@ -1187,15 +1191,15 @@ size_t part_bytes(int n_heads, int n_kv_heads, int D, int n_seqs, int max_len, b
 
 // Sets the split layout and partials buffer for one decode call, then
 // launches.  A split is 256/G keys (ring mode: every lane of the workgroup
-// then loads all of its K and V rows at once) or kPagedChunks such chunks
-// (paged mode).  `max_len` bounds every sequence's key count; `n_seqs`
+// then loads all of its K and V rows at once) or kPagedSplit keys (paged
+// mode, 16-key blocks per wave).  `max_len` bounds every sequence's key count; `n_seqs`
 // sequences (1 in ring mode).  The partials go to `part` (part_cap bytes)
 // when it is given, else to the library workspace.
 int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, int max_len,
                hipStream_t st, float* part = nullptr, size_t part_cap = 0) {
     const int Hkv = p.n_kv_heads;
     const int G = n_heads / Hkv;
-    const int kps = (256 / G) * (p.paged ? kPagedChunks : 1);
+    const int kps = p.paged ? kPagedSplit : 256 / G;
     const int max_splits = (max_len + kps - 1) / kps;
     p.kps = kps;
     p.max_splits = max_splits;
@@ -1209,7 +1213,14 @@ int run_decode(DecodeParams& p, int kv_dtype, int n_heads, int D, int n_seqs, in
     const bool merge_inline = !p.paged && max_splits >= 2 && max_splits <= kInlineMaxSplits &&
                               Hkv * n_seqs <= kArrivalWords;
     p.arrivals = nullptr;
-    if (need > 0 && part != nullptr) {
+    if (p.paged) {
+        // records, then the q rows of the paged prologue (fp16)
+        const size_t rec_bytes = (need + 255) & ~(size_t)255;
+        char* ws = static_cast<char*>(workspace(rec_bytes + (size_t)n_seqs * n_heads * D * 2, st));
+        if (!ws) return ANELM_ENOMEM;
+        p.part = need > 0 ? reinterpret_cast<float*>(ws) : nullptr;
+        p.q_prep = reinterpret_cast<const uint16_t*>(ws + rec_bytes);
+    } else if (need > 0 && part != nullptr) {
         // a caller's buffer holds the records from its start and, in its last
         // kArrivalBytes (zero when the caller hands it over), the counters
         if (need + (merge_inline ? kArrivalBytes : 0) > part_cap)

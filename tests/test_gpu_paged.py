@@ -90,3 +90,14 @@ def test_paged_step_shapes(anelm, orc, dev, Hq, Hkv, D, P, mode, norms, gate):
     c = paged_case(1210 + P, lens=[0, 3, 64, 200, 1100, 2049], Hkv=Hkv, D=D, P=P)
     _run_and_check(anelm, orc, dev, c, Hq, Hkv, D, D // 4, table_rows=4096, rope_mode=mode, norms=norms,
                    gate=gate, label=f"{Hq}q/{Hkv}kv D{D} P{P}")
+
+
+@pytest.mark.parametrize("mode,rot", [(1, 20), (0, 20), (1, 64), (0, 6)])
+def test_paged_step_partial_rotary(anelm, orc, dev, mode, rot):
+    """Rotary dims that do not fill whole lanes: half-split pairs whose halves
+    straddle lanes (rot_dim 20: the LDS prologue), interleaved pairs ending
+    inside a lane (rot_dim 20, 6), and half-split halves of whole lanes
+    (rot_dim 64 of D 128)."""
+    c = paged_case(1230 + rot + mode, lens=[0, 5, 130, 700, 1500], Hkv=2, D=128, P=16)
+    _run_and_check(anelm, orc, dev, c, 8, 2, 128, rot, table_rows=4096, rope_mode=mode,
+                   label=f"mode {mode} rot {rot}")
