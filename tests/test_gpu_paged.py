@@ -101,3 +101,16 @@ def test_paged_step_partial_rotary(anelm, orc, dev, mode, rot):
     c = paged_case(1230 + rot + mode, lens=[0, 5, 130, 700, 1500], Hkv=2, D=128, P=16)
     _run_and_check(anelm, orc, dev, c, 8, 2, 128, rot, table_rows=4096, rope_mode=mode,
                    label=f"mode {mode} rot {rot}")
+
+
+@pytest.mark.parametrize("n_seqs", [2049])
+def test_paged_step_many_sequences(anelm, orc, dev, n_seqs):
+    """2049 sequences x 8 kv heads (16,392 (sequence, kv head) pairs over the
+    resident workgroups' unit shares): most lengths are under 40 keys, every
+    97th sequence has 600 (three 256-key splits merged from their records)."""
+    rng = np.random.default_rng(1250)
+    lens = rng.integers(0, 40, n_seqs)
+    lens[::97] = 600
+    c = paged_case(1250, lens=lens, Hkv=8, D=64, P=16)
+    seqs = sorted(set(range(0, n_seqs, 97)) | set(range(1, 40)) | {n_seqs - 1})
+    _run_and_check(anelm, orc, dev, c, 16, 8, 64, 16, table_rows=1024, seqs=seqs, label="merge kernel")
