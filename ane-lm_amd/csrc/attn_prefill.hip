@@ -11,7 +11,7 @@
 // softmax statistics therefore need one cross-half exchange only, the output
 // rescale is a per-lane scalar, and P^T is already in the B-operand layout of
 // the second product O^T += V^T P^T (the contraction order over keys is
-// permuted identically in both operands).  K and V^T tiles of 32 keys are
+// permuted identically in both operands).  K and V tiles of 32 keys are
 // staged in LDS once per workgroup and shared by all waves (the query heads of
 // one KV head and several row blocks).
 #include "anelm_internal.hpp"
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
 //
 // * Blocks of 64 query rows; a workgroup's 8 waves are 4 query heads x 2 row
 //   halves of 32 rows, and all of them consume ONE stream of 32-key tiles, so
-//   each K / V^T byte staged in LDS feeds 256 query rows.
+//   each K / V byte staged in LDS feeds 256 query rows.
 // * Balance: a unit is a KV head and a pair of blocks (a, nb-1-a) (or the
 //   middle block when nb is odd).  Its causal key tiles, a's then b's, are cut
 //   into two equal halves taken by two workgroups.  The block whose tiles are
@@ -182,12 +182,14 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
 //   partial (m, l, unnormalised O) with device-coherent stores, a relaxed
 //   device-scope counter tells the second which it is, and the second combines
 //   and writes the rows (and re-zeroes the counter for the next call).
-// * Stream: K tiles (32 keys x 256) and V^T tiles (256 dims x 32 keys, from the
-//   V^T copy made by vt_kernel) go straight to LDS with buffer loads (1 KiB per
-//   wave instruction) into a ring of 4 buffers, 3 tiles ahead of use.  K rows c
-//   and c+16 share a 1040-byte chunk (16 bytes of padding per chunk) so the
-//   MFMA operand reads are conflict-free with immediate offsets; V^T 16-byte
-//   granules are XOR-swizzled.
+// * Stream: K and V tiles (32 keys x 256) go straight to LDS with buffer loads
+//   (1 KiB per wave instruction: rows c and c+16 of a tile share a chunk) into
+//   a ring of 4 buffers, 3 tiles ahead of use.  K chunks are 1040 bytes (16 of
+//   padding) so the MFMA operand reads are conflict-free with immediate
+//   offsets; V chunks are 1088 bytes, so the four key rows a 16-lane group
+//   reads with ds_read_b64_tr_b16 (4 keys x 16 dims, delivered transposed:
+//   lane n gets dim n of the 4 keys) fall on distinct banks.  That transposing
+//   read builds the V^T operand of O^T += V^T P^T from the V rows as stored.
 // * Scores S^T = K Q^T (v_mfma_f32_32x32x16_f16).  The A-operand lane i reads
 //   key row pi(i) (bits 2 and 3 of i swapped): lane (r, h) of the accumulator
 //   then holds the scores of query row r for keys 8h..8h+7 and 16+8h..16+8h+7,
@@ -197,7 +199,8 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
 //   128-register output rescale is rare.
 constexpr int kGKeys = 32;                       // keys per tile
 constexpr int kGKBytes = 16 * 1040;              // K tile: chunk c = rows c, c + 16
-constexpr int kGTile = kGKBytes + 16384;         // + V^T tile (256 x 32 fp16)
+constexpr int kGVChunk = 1088;                   // V tile chunk: rows c, c + 16 + 64 bytes of bank offset
+constexpr int kGTile = kGKBytes + 16 * kGVChunk; // + V tile (32 x 256 fp16)
 constexpr int kGBuf = 4;                         // ring of tile buffers
 constexpr int kGLds = kGBuf * kGTile + 64;       // + the merge flag
 constexpr int kGSlotFloats = 8 * 128 * 64 + 8 * 128;   // partial: O (8 waves x 128 x 64 lanes), m, l
@@ -205,29 +208,6 @@ constexpr int kGNT = 512;
 constexpr int kSc1 = 16;                         // buffer cache policy: device-scope coherent
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-// V^T copy: vt[(kvh * D + d) * S_pad + key] (zero past S).
-__global__ __launch_bounds__(256) void vt_kernel(_Float16* vt, const _Float16* v, int S, int S_pad, int Hkv) {
-    constexpr int D = 256;
-    __shared__ __attribute__((aligned(16))) _Float16 tile[kGKeys][D + 8];
-    const int j0 = blockIdx.x * kGKeys, kvh = blockIdx.y, tid = threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k, key = c / (D / 8), g = c % (D / 8);
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (j0 + key < S) val = *reinterpret_cast<const uint4*>(v + ((size_t)(j0 + key) * Hkv + kvh) * D + 8 * g);
-        *reinterpret_cast<uint4*>(&tile[key][8 * g]) = val;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k, d = c / 4, g = c % 4;
-        _Float16 e[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) e[i] = tile[8 * g + i][d];
-        *reinterpret_cast<uint4*>(vt + ((size_t)kvh * D + d) * S_pad + j0 + 8 * g) = *reinterpret_cast<const uint4*>(e);
-    }
-}
 
 __device__ __forceinline__ int key_perm(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
@@ -241,8 +221,8 @@ __device__ __forceinline__ int block_tiles(int blk, int S, int qoff) {
 // (r, h) is multiplied by sigmoid(gate[r * gtok + h * ghead + d]).
 template <bool OUT16>
 __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Float16* q, const _Float16* k,
-                                                           const _Float16* vt, float* part, uint32_t* ctr, int S,
-                                                           int L, int L_pad, int qoff, int Hq, int Hkv,
+                                                           const _Float16* v, float* part, uint32_t* ctr, int S,
+                                                           int L, int qoff, int Hq, int Hkv,
                                                            const float* gate, int gtok, int ghead) {
     constexpr int D = 256, KS = D / 16, DB = D / 32;
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -278,10 +258,10 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(k), 0, (int)min((size_t)L * Hkv * D * 2, (size_t)0x7fffffff), 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(vt), 0, (int)min((size_t)Hkv * D * L_pad * 2, (size_t)0x7fffffff), 0x00020000);
+        const_cast<_Float16*>(v), 0, (int)min((size_t)L * Hkv * D * 2, (size_t)0x7fffffff), 0x00020000);
     const float sl2 = (1.0f / 16.0f) * 1.4426950408889634f;   // 1/sqrt(256) * log2(e)
     auto key_tile = [&](int i) { return i < n0 ? t00 + i : t01 + (i - n0); };
-    // stream tile i -> buffer i % 4; wave w loads K chunks 2w, 2w+1 and V^T pieces 2w, 2w+1
+    // stream tile i -> buffer i % 4; wave w loads K and V chunks 2w, 2w+1
     auto issue = [&](int i) {
         char* base = lds + (i % kGBuf) * kGTile;
         const int j0 = key_tile(i) * kGKeys;
@@ -296,10 +276,10 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
         }
 #pragma unroll
         for (int x = 0; x < 2; x++) {
-            const int p = (2 * w + x) * 64 + ln, d = p >> 2, gs = p & 3, g = gs ^ ((d >> 2) & 3);
-            const int off = (((kvh * D + d) * L_pad) + j0 + 8 * g) * 2;
+            const int c = 2 * w + x, row = c + 16 * (ln >> 5), key = j0 + row;
+            const int off = key < L ? ((key * Hkv + kvh) * D + 8 * (ln & 31)) * 2 : 0x7fffffff;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void*)(base + kGKBytes + (2 * w + x) * 1024), 16, off, 0, 0, 0);
+                rv, (__attribute__((address_space(3))) void*)(base + kGKBytes + c * kGVChunk), 16, off, 0, 0, 0);
         }
     };
     for (int i = 0; i < 3 && i < ntot; i++) issue(i);
@@ -378,17 +358,29 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                 l += pe;
                 pf[e / 8][e % 8] = (_Float16)pe;
             }
-            // ---- O^T += V^T P^T
+            // ---- O^T += V^T P^T.  The A operand of lane (m, h2) for keys
+            // 16u + 8 h2 .. +8 and dim 32 db + m comes from two transposing
+            // reads: 16-lane group i (m = 16 (i & 1) + n, h2 = i >> 1) has
+            // its lane n address key 16u + 8 (i >> 1) + 4r + n / 4, dims
+            // 32 db + 16 (i & 1) + 4 (n % 4) .. +4 of the V rows (key t at
+            // chunk t % 16, half t / 16).
             {
-                const int rr = ln & 31, h2 = ln >> 5;
-                const char* vb0 = base + kGKBytes + rr * 64 + ((h2 ^ ((rr >> 2) & 3)) << 4);
-                const char* vb1 = base + kGKBytes + rr * 64 + (((2 + h2) ^ ((rr >> 2) & 3)) << 4);
+                const int gi = ln >> 4, nn = ln & 15;
+                const char* vbase = base + kGKBytes + (8 * (gi >> 1) + (nn >> 2)) * kGVChunk +
+                                    (16 * (gi & 1) + 4 * (nn & 3)) * 2;
+                typedef short s16x4 __attribute__((ext_vector_type(4)));
+                auto vtr = [&](int off) __attribute__((always_inline)) {
+                    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(vbase + off));
+                };
 #pragma unroll
                 for (int db = 0; db < DB; db++) {
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(vb0 + 2048 * db),
-                                                                   pf[0], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(vb1 + 2048 * db),
-                                                                   pf[1], o[db], 0, 0, 0);
+#pragma unroll
+                    for (int u = 0; u < 2; u++) {
+                        const s16x4 lo = vtr(u * 512 + 64 * db), hi = vtr(4 * kGVChunk + u * 512 + 64 * db);
+                        const half8 av = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pf[u], o[db], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -432,7 +424,10 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
             const float M = fmaxf(m, m1);
             a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
             a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
-            inv = 1.0f / (l * a0 + l1 * a1);
+            {
+#pragma clang fp contract(off)
+                inv = 1.0f / (l * a0 + l1 * a1);
+            }
         } else {
             inv = 1.0f / l;
         }
@@ -448,10 +443,18 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                     if (have_other)
                         ov = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                                             rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
-                    float v0 = (o[db][4 * g4] * a0 + ov.x * a1) * inv;
-                    float v1 = (o[db][4 * g4 + 1] * a0 + ov.y * a1) * inv;
-                    float v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
-                    float v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
+                    float v0, v1, v2, v3;
+                    {
+                        // Either workgroup of a split block may be the one that
+                        // merges: products rounded separately keep the sum
+                        // symmetric in the two partials, so a row's bits do not
+                        // depend on which finished second.
+#pragma clang fp contract(off)
+                        v0 = (o[db][4 * g4] * a0 + ov.x * a1) * inv;
+                        v1 = (o[db][4 * g4 + 1] * a0 + ov.y * a1) * inv;
+                        v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
+                        v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
+                    }
                     if (gate) {
                         const float* gr = gate + (size_t)erow * gtok + (size_t)h * ghead + dd;
                         v0 = v0 / (1.0f + expf(-gr[0]));
@@ -475,21 +478,13 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
 int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const void* v, int S, int L, int qoff,
                       int Hq, int Hkv, const float* gate, int gtok, int ghead, hipStream_t st) {
     constexpr int D = 256;
-    const int L_pad = (L + kGKeys - 1) / kGKeys * kGKeys;
-    ANELM_REQUIRE((size_t)L * Hkv * D * 2 < 0x7fffffffu && (size_t)Hkv * D * L_pad * 2 < 0x7fffffffu,
-                  "prefill: %d keys exceed the 2 GiB buffer range", L);
+    ANELM_REQUIRE((size_t)L * Hkv * D * 2 < 0x7fffffffu, "prefill: %d keys exceed the 2 GiB buffer range", L);
     const int nb = (S + 63) / 64, upk = nb / 2 + (nb & 1), units = Hkv * upk;
-    const size_t vt_bytes = ((size_t)Hkv * D * L_pad * 2 + 255) & ~(size_t)255;
     const size_t part_bytes = (size_t)2 * units * kGSlotFloats * sizeof(float);
-    char* ws = static_cast<char*>(workspace(vt_bytes + part_bytes, st));
-    if (!ws) return ANELM_ENOMEM;
+    float* part = static_cast<float*>(workspace(part_bytes, st));
+    if (!part) return ANELM_ENOMEM;
     uint32_t* ctr = counters(units, kCtrPrefill, st);   // zeroed; each call leaves them zeroed
     if (!ctr) return ANELM_ERANGE;
-    _Float16* vt = reinterpret_cast<_Float16*>(ws);
-    float* part = reinterpret_cast<float*>(ws + vt_bytes);
-    hipLaunchKernelGGL(vt_kernel, dim3(L_pad / kGKeys, Hkv), dim3(256), 0, st, vt, static_cast<const _Float16*>(v), L,
-                       L_pad, Hkv);
-    ANELM_LAUNCHED("vt_kernel");
     static bool attr_set = false;
     if (!attr_set) {
         ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_g4_kernel<true>),
@@ -500,13 +495,14 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     }
     const _Float16* qh = static_cast<const _Float16*>(q);
     const _Float16* kh = static_cast<const _Float16*>(k);
+    const _Float16* vh = static_cast<const _Float16*>(v);
     const dim3 grid(2 * units);
     if (out16)
-        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, L,
-                           L_pad, qoff, Hq, Hkv, gate, gtok, ghead);
+        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vh, part, ctr, S, L,
+                           qoff, Hq, Hkv, gate, gtok, ghead);
     else
-        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vt, part, ctr, S, L,
-                           L_pad, qoff, Hq, Hkv, gate, gtok, ghead);
+        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vh, part, ctr, S, L,
+                           qoff, Hq, Hkv, gate, gtok, ghead);
     ANELM_LAUNCHED("prefill_g4_kernel");
     return ANELM_OK;
 }
