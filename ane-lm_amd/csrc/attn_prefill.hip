@@ -392,30 +392,47 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
         __amdgpu_buffer_rsrc_t rot = __builtin_amdgcn_make_buffer_rsrc(part, 0, 0, 0x00020000);
         bool have_other = false;
         if (split && blk == blk_b) {
-            // partial of the split block: publish, then the second finisher merges
-            const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-                part + (size_t)(unit * 2 + half_id) * kGSlotFloats, 0, kGSlotFloats * 4, 0x00020000);
-#pragma unroll
-            for (int db = 0; db < DB; db++)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    const float4 v4 = make_float4(o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]);
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v4), rm,
-                                                           (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1);
-                }
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m), rm, (8 * 128 * 64 + w * 128 + ln) * 4,
-                                                  0, kSc1);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l), rm,
-                                                  (8 * 128 * 64 + w * 128 + 64 + ln) * 4, 0, kSc1);
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's partial is stored
-            __syncthreads();
+            // The split block's two workgroups arrive on the unit's counter
+            // (0 -> 1 -> 2, one more when the first one's partial is out).
+            // The first to arrive publishes its partial and leaves; the
+            // second waits until that partial is stored (the first is
+            // resident, and nothing stands between its arrival and its
+            // stores), merges it with its own registers and re-zeroes the
+            // counter.  One partial per split block is written and read.
             uint32_t* flag = reinterpret_cast<uint32_t*>(lds + kGBuf * kGTile);
             if (tid == 0) flag[0] = __hip_atomic_fetch_add(&ctr[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
-            if (flag[0] == 0) break;   // the other workgroup finishes this block (its segment is the last)
-            if (tid == 0) __hip_atomic_store(&ctr[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            rot = __builtin_amdgcn_make_buffer_rsrc(part + (size_t)(unit * 2 + (half_id ^ 1)) * kGSlotFloats, 0,
-                                                    kGSlotFloats * 4, 0x00020000);
+            const uint32_t arrived = flag[0];
+            rot = __builtin_amdgcn_make_buffer_rsrc(part + (size_t)unit * kGSlotFloats, 0, kGSlotFloats * 4, 0x00020000);
+            if (arrived == 0) {
+#pragma unroll
+                for (int db = 0; db < DB; db++)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const float4 v4 =
+                            make_float4(o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v4), rot,
+                                                               (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1);
+                    }
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m), rot,
+                                                      (8 * 128 * 64 + w * 128 + ln) * 4, 0, kSc1);
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l), rot,
+                                                      (8 * 128 * 64 + w * 128 + 64 + ln) * 4, 0, kSc1);
+                __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's part of the partial is stored
+                __syncthreads();
+                if (tid == 0) __hip_atomic_fetch_add(&ctr[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;   // the other workgroup finishes this block (its segment is the last)
+            }
+            if (tid == 0) {
+                // bounded: the first workgroup only has its stores left
+                uint32_t c = arrived + 1;
+                for (int it = 0; c != 3 && it < (1 << 22); it++) {
+                    __builtin_amdgcn_s_sleep(2);
+                    c = __hip_atomic_load(&ctr[unit], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __hip_atomic_store(&ctr[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
             have_other = true;
             const float m1 = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rot, (8 * 128 * 64 + w * 128 + ln) * 4, 0, kSc1));
@@ -480,7 +497,7 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     constexpr int D = 256;
     ANELM_REQUIRE((size_t)L * Hkv * D * 2 < 0x7fffffffu, "prefill: %d keys exceed the 2 GiB buffer range", L);
     const int nb = (S + 63) / 64, upk = nb / 2 + (nb & 1), units = Hkv * upk;
-    const size_t part_bytes = (size_t)2 * units * kGSlotFloats * sizeof(float);
+    const size_t part_bytes = (size_t)units * kGSlotFloats * sizeof(float);
     float* part = static_cast<float*>(workspace(part_bytes, st));
     if (!part) return ANELM_ENOMEM;
     uint32_t* ctr = counters(units, kCtrPrefill, st);   // zeroed; each call leaves them zeroed
