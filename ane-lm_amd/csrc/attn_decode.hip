@@ -1067,15 +1067,21 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3))) void a
 
 // Log-sum-exp merge of the split partials of one (sequence, q head) for 64
 // output dims per workgroup: M = max m_s, L = sum l_s e^(m_s-M),
-// O = sum o_s e^(m_s-M), out = O / L, then the sigmoid gate.  The 256
-// threads first turn all m_s into weights e^(m_s-M) in LDS, then four groups
-// of 64 threads sum interleaved quarters of the splits.
-constexpr int kCombineChunk = 1024;   // splits weighed per LDS pass
-
-template <int D, int G>
+// O = sum o_s e^(m_s-M), out = O / L, then the sigmoid gate.  Splits are
+// taken kCombineRound at a time, and every load of a round is issued before
+// any of its arithmetic: thread t reads m and l of split t of the round, and
+// the four groups of 64 threads read the o values of interleaved quarters of
+// the round's splits (kCombineRound / 4 each, all in flight together).  The
+// round's maximum and weights then go through LDS; a later round rescales the
+// running sums when the maximum grows.  R splits per round (<= the 256
+// threads): 128 for the ring's records, whose o values are requested with
+// m and l; 64 for paged records, most of which are empty (one record per
+// workgroup run): their o values are requested once the weights are known,
+// only for the records that carry weight.
+template <int D, int G, int R, bool PAGED>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p) {
-    constexpr int REC = D + 2;
-    __shared__ float f[kCombineChunk];
+    constexpr int REC = D + 2, NQ = R / 4;
+    __shared__ float f[R];
     __shared__ float red[4];
     __shared__ float osum[4][64];
     const int tid = threadIdx.x, dq = tid & 63, grp = tid >> 6;
@@ -1088,28 +1094,44 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams p)
     if (n <= 1) return;   // written directly by the split kernel (or zeros)
     const size_t rs = (size_t)G * REC;   // record stride between splits
     const float* base = p.part + ((size_t)seq * Hkv + kvh) * p.max_splits * rs + (size_t)g * REC;
-    float M = -INFINITY;
-    for (int s = tid; s < n; s += 256) M = fmaxf(M, base[(size_t)s * rs]);
-    M = block_max<256>(M, red);
-    float L = 0.f, O = 0.f;
-    for (int c0 = 0; c0 < n; c0 += kCombineChunk) {
-        const int cn = min(kCombineChunk, n - c0);
-        float lpart = 0.f;
-        for (int s = tid; s < cn; s += 256) {
-            const float* r = base + (size_t)(c0 + s) * rs;
-            const float w = __expf(r[0] - M);
-            f[s] = w;
-            lpart += r[1] * w;
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    for (int c0 = 0; c0 < n; c0 += R) {
+        const int cn = min(R, n - c0);
+        float mv = -INFINITY, lv = 0.f;
+        if (tid < cn) {
+            const float* r = base + (size_t)(c0 + tid) * rs;
+            mv = r[0];
+            lv = r[1];
         }
-        L += block_sum<256>(lpart, red);   // (its barriers also publish f)
-        int s = grp;
-        // (an empty record, l = 0, weighs 0 and its o is never read)
-        auto term = [&](int si) {
-            return f[si] != 0.f ? f[si] * base[(size_t)(c0 + si) * rs + 2 + d] : 0.f;
-        };
-        for (; s + 12 < cn; s += 16) O += term(s) + term(s + 4) + term(s + 8) + term(s + 12);
-        for (; s < cn; s += 4) O += term(s);
-        __syncthreads();
+        float ov[NQ];
+        if constexpr (!PAGED) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                const int sj = grp + 4 * j;
+                ov[j] = sj < cn ? base[(size_t)(c0 + sj) * rs + 2 + d] : 0.f;
+            }
+        }
+        const float Mn = fmaxf(M, block_max<256>(mv, red));
+        // (an empty record, m = -inf and l = 0, weighs 0 and its o is not used)
+        const float wv = mv != -INFINITY ? __expf(mv - Mn) : 0.f;
+        const float sc = M != -INFINITY ? __expf(M - Mn) : 0.f;
+        if (tid < R) f[tid] = wv;
+        L = L * sc + block_sum<256>(tid < cn ? lv * wv : 0.f, red);   // (its barriers also publish f)
+        O *= sc;
+        if constexpr (PAGED) {
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                const int sj = grp + 4 * j;
+                ov[j] = sj < cn && f[sj] != 0.f ? base[(size_t)(c0 + sj) * rs + 2 + d] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            const int sj = grp + 4 * j;
+            if (sj < cn && f[sj] != 0.f) O += f[sj] * ov[j];
+        }
+        M = Mn;
+        __syncthreads();   // f is rewritten by the next round
     }
     osum[grp][dq] = O;
     __syncthreads();
@@ -1153,7 +1175,10 @@ int launch_g(DecodeParams& p, dim3 grid, hipStream_t st) {
     }
     if (p.max_splits > 1 && p.arrivals == nullptr) {
         dim3 cgrid(D / 64, grid.y * G, grid.z);
-        hipLaunchKernelGGL((attn_combine_kernel<D, G>), cgrid, dim3(256), 0, st, p);
+        if (p.paged)
+            hipLaunchKernelGGL((attn_combine_kernel<D, G, 64, true>), cgrid, dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((attn_combine_kernel<D, G, 128, false>), cgrid, dim3(256), 0, st, p);
         ANELM_LAUNCHED("attn_combine_kernel");
     }
     return ANELM_OK;
