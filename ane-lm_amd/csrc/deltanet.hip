@@ -109,22 +109,8 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
             vs[tid] = conv_silu(p, cv, vx);
             p.conv_state[(size_t)cv * (p.conv_k - 1) + p.conv_pos] = vx;   // this workgroup is its only reader
         }
-        // every ring read of this workgroup has returned (its values are in
-        // registers): count this workgroup as done with the key head; the last
-        // one stores the new q/k inputs into the ring
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t n = __hip_atomic_fetch_add(p.readers_done + kh, 1u, __ATOMIC_ACQ_REL,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-            last_reader = n == (uint32_t)p.readers - 1u;
-            if (last_reader) __hip_atomic_store(p.readers_done + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (last_reader && tid < kDK) {
-            const int sl = p.conv_k - 1;
-            p.conv_state[(size_t)(kh * kDK + tid) * sl + p.conv_pos] = qx;
-            p.conv_state[(size_t)(p.Hk * kDK + kh * kDK + tid) * sl + p.conv_pos] = kx;
-        }
+        // the key head's q/k ring slots take their new inputs at the end of
+        // the kernel, off the path of the recurrence
     } else if (tid < kDK) {
         qv = p.q[(size_t)kh * kDK + tid];
         kv = p.k[(size_t)kh * kDK + tid];
@@ -188,6 +174,26 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(const DnParams p) {
             float o = (yj * inv) * p.norm_w[j];
             o = o / (1.0f + expf(-zi));
             p.y[(size_t)h * kDV + j] = o * zi;
+        }
+    }
+    if constexpr (CONV) {
+        // Every ring read of this workgroup returned long ago (the values fed
+        // the recurrence): count the workgroup as done with its key head; the
+        // last of the head's readers stores the new q/k inputs into the ring
+        // and re-zeroes the counter.  No data of this workgroup is published
+        // through the counter, so it is relaxed.
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t n = __hip_atomic_fetch_add(p.readers_done + kh, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+            last_reader = n == (uint32_t)p.readers - 1u;
+            if (last_reader) __hip_atomic_store(p.readers_done + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last_reader && tid < kDK) {
+            const int sl = p.conv_k - 1;
+            p.conv_state[(size_t)(kh * kDK + tid) * sl + p.conv_pos] = qx;
+            p.conv_state[(size_t)(p.Hk * kDK + kh * kDK + tid) * sl + p.conv_pos] = kx;
         }
     }
 }
