@@ -18,7 +18,7 @@ _P = ctypes.c_void_p
 
 
 class DeviceBatch:
-    def __init__(self, anelm, m, dev, lm=None, top_k=4, final_norm=None):
+    def __init__(self, anelm, m, dev, lm=None, top_k=4, final_norm=None, rope_rows=4096):
         d = m.dims
         B = len(m.lens)
         self.keep = []
@@ -50,13 +50,13 @@ class DeviceBatch:
             self.outs.append(t["core_out"])
         self.x = to_dev(m.x, dev)
         self.lens = to_dev(m.lens, dev)
-        self.rope = anelm.ops.rope_table(d["rot_dim"], 4096, d["theta"], dev)
+        self.rope = anelm.ops.rope_table(d["rot_dim"], rope_rows, d["theta"], dev)
         self.seqs = anelm.BatchSeqs()
         q = self.seqs
         q.n_seqs, q.seq_lens, q.positions = B, ptr(self.lens), None
         q.page_size, q.n_pages, q.max_pages = self.page_size, self.n_pages, max_pages
         q.max_seq_len = max_pages * self.page_size
-        q.rope_table, q.rope_rows = ptr(self.rope), 4096
+        q.rope_table, q.rope_rows = ptr(self.rope), rope_rows
         if lm is not None:
             self.lm = (to_dev(lm[0], dev), to_dev(lm[1], dev))
             self.fn = to_dev(final_norm, dev)
@@ -118,6 +118,36 @@ def test_batch_step_32_sequences_matches_oracle(anelm, orc, dev):
                     assert np.array_equal(idx[s], oi), f"step {step} seq {s} top indices"
                     exact_rows += 1
         assert exact_rows >= 60, f"only {exact_rows} of 64 rows were separated enough to compare indices"
+    finally:
+        anelm.call("anelm_batch_step_destroy", h)
+
+
+def test_batch_step_full_lengths_matches_oracle(anelm, orc, dev):
+    """The batched step at the full lengths of the 32-sequence workload:
+    lengths U[256, 16384] (sum ~266k keys) over shuffled 16-token pages, so
+    the paged attention layer runs its multi-run workgroups and the split
+    merge over up to 64 records per (sequence, kv head); 4 layers, one
+    advancing step, every core output and the hidden states against the
+    oracle per sequence."""
+    m = batch_model(1320, 4, 32, lo=256, hi=16384, lut_std=0.005)
+    rows = int(m.lens.max()) + 8
+    db = DeviceBatch(anelm, m, dev, rope_rows=rows)
+    h = _P()
+    rc = anelm.status("anelm_batch_step_create", ctypes.byref(h), ctypes.byref(db.dims), db.layers,
+                      len(m.layers), ctypes.byref(db.seqs), _P(db.x.data_ptr()))
+    assert rc == 0, anelm.last_error()
+    try:
+        print(f"batch step: 32 sequences, sum of lengths {int(m.lens.sum())}, 4 layers", flush=True)
+        anelm.call("anelm_batch_step_run", h, 1, _P(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        ob = OracleBatch(orc, m, steps=1)
+        outs = ob.step()
+        for i, L in enumerate(m.layers):
+            got = to_host(db.outs[i])
+            for s in range(32):
+                assert_close(got[s], outs[i][s], what=f"layer {i} seq {s} core output (len {int(m.lens[s])})")
+        assert_close(to_host(db.x), ob.x, what="hidden states")
+        assert np.array_equal(to_host(db.lens), m.lens + 1), "seq_lens not advanced"
     finally:
         anelm.call("anelm_batch_step_destroy", h)
 
