@@ -327,6 +327,14 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                 for (int ks = 0; ks < KS; ks++)
                     sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + 32 * ks), qf[ks], sc,
                                                                 0, 0, 0);
+                // K fragment ks + 1 is read while the product of fragment ks runs
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int ks = 0; ks < KS - 2; ks++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             }
             // ---- online softmax; element e holds key j0 + (e < 8 ? 8 h + e : 16 + 8 h + e - 8)
             if (j0 + 31 > qoff + row0) {
