@@ -377,18 +377,32 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                 const char* vbase = base + kGKBytes + (8 * (gi >> 1) + (nn >> 2)) * kGVChunk +
                                     (16 * (gi & 1) + 4 * (nn & 3)) * 2;
                 typedef short s16x4 __attribute__((ext_vector_type(4)));
-                auto vtr = [&](int off) __attribute__((always_inline)) {
-                    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(vbase + off));
-                };
+                static_assert(4 * kGVChunk == 4352, "offset of the second read");
+                const uint32_t va = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)vbase);
+                // product k = 2 db + u; the reads of product k + 1 are issued
+                // before product k (each asm statement waits only for the
+                // older pair, which it passes through to the product)
+                s16x4 lo[2], hi[2];
+                asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %2 offset:4352"
+                             : "=&v"(lo[0]), "=&v"(hi[0])
+                             : "v"(va)
+                             : "memory");
 #pragma unroll
-                for (int db = 0; db < DB; db++) {
-#pragma unroll
-                    for (int u = 0; u < 2; u++) {
-                        const s16x4 lo = vtr(u * 512 + 64 * db), hi = vtr(4 * kGVChunk + u * 512 + 64 * db);
-                        const half8 av = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pf[u], o[db], 0, 0, 0);
+                for (int kk = 0; kk < 2 * DB; kk++) {
+                    const int db = kk >> 1, u = kk & 1, c = kk & 1, n = c ^ 1;
+                    if (kk + 1 < 2 * DB) {
+                        const int u1 = (kk + 1) & 1, db1 = (kk + 1) >> 1;
+                        asm volatile(
+                            "ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %4 offset:4352\n\ts_waitcnt lgkmcnt(2)"
+                            : "=&v"(lo[n]), "=&v"(hi[n]), "+v"(lo[c]), "+v"(hi[c])
+                            : "v"(va + (uint32_t)(u1 * 512 + 64 * db1))
+                            : "memory");
+                    } else {
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo[c]), "+v"(hi[c]) : : "memory");
                     }
+                    const half8 av =
+                        __builtin_bit_cast(half8, __builtin_shufflevector(lo[c], hi[c], 0, 1, 2, 3, 4, 5, 6, 7));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pf[u], o[db], 0, 0, 0);
                 }
             }
         }
