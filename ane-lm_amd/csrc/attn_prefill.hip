@@ -178,10 +178,12 @@ __global__ __launch_bounds__(HB * RB * 64) void prefill_kernel(void* out, const 
 // * Balance: a unit is a KV head and a pair of blocks (a, nb-1-a) (or the
 //   middle block when nb is odd).  Its causal key tiles, a's then b's, are cut
 //   into two equal halves taken by two workgroups.  The block whose tiles are
-//   split is merged by whichever of the two finishes second: both write their
-//   partial (m, l, unnormalised O) with device-coherent stores, a relaxed
-//   device-scope counter tells the second which it is, and the second combines
-//   and writes the rows (and re-zeroes the counter for the next call).
+//   split is merged by whichever of the two finishes second: a relaxed
+//   device-scope counter orders their arrivals, the first writes its partial
+//   (m, l, unnormalised O) with device-coherent stores and counts again once
+//   they are out, the second waits for that count, combines the partial with
+//   its registers, writes the rows and re-zeroes the counter for the next
+//   call.
 // * Stream: K and V tiles (32 keys x 256) go straight to LDS with buffer loads
 //   (1 KiB per wave instruction: rows c and c+16 of a tile share a chunk) into
 //   a ring of 4 buffers, 3 tiles ahead of use.  K chunks are 1040 bytes (16 of
