@@ -321,6 +321,47 @@ def measure_cores(anelm, torch, dev, seed=11):
     res["deltanet_prefill_4096"] = r
     del pq, pk, pv, pa, pb
 
+    # prompt prefill through the layer cores over their state, 4096 tokens
+    # (generate.cpp:55-85 runs the decode core once per prompt token): full
+    # attention from the first projection's q_gate / k / v (q/k RMSNorm, RoPE
+    # at each position, fp16 append into an empty 8192-key ring, the causal
+    # MFMA core, the sigmoid gate) ...
+    qg = randn(S, 16, 512)
+    kx, vx = randn(S, 4, 256), randn(S, 4, 256)
+    qnw, knw = 1 + randn(256, std=0.02), 1 + randn(256, std=0.02)
+    kc = torch.zeros(8192, 4, 256, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    tab = anelm.ops.rope_table(64, S, 1e7, dev)
+    ring = anelm.ops.KVRing(8192)
+
+    def attn_layer():
+        ring.start.value, ring.len.value = 0, 0
+        anelm.ops.full_attn_prefill(qg, kx, vx, kc, vc, qnw, knw, ring, 16, 4, 256, 64, 0, rope_table=tab,
+                                    rope_rows=S)
+    us = _gpu_us(torch, attn_layer, 10)
+    tf = flops / (us * 1e-6) / 1e12
+    res["prompt_prefill_attention_layer_4096"] = {
+        "us": round(us, 2), "TFLOPs": round(tf, 1), "frac_mfma": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+        "composition": "q/k RMSNorm, RoPE per position, fp16 ring append, causal MFMA core, sigmoid gate"}
+    del qg, kx, vx, kc, vc
+    # ... and Gated DeltaNet from its projection rows (conv ring + SiLU over
+    # the prompt, l2 norm, gates, the chunked recurrence, rmsnorm_gated)
+    qkv = 2 * Hk * 128 + Hv * 128
+    proj = randn(S, qkv + Hv * 128 + 2 * Hv)
+    conv_w, conv_st = randn(qkv, 4, std=0.5), randn(qkv, 3, std=0.5)
+    nw = 1 + randn(128, std=0.02)
+    st = randn(Hv, 128, 128, std=0.1)
+    pos = ctypes.c_int(0)
+
+    def dn_layer():
+        pos.value = 0
+        anelm.ops.deltanet_prefill_from_proj(st, conv_st, pos, proj, conv_w, pA, pdt, nw, Hk, 1 | 4)
+    us = _gpu_us(torch, dn_layer, 10)
+    res["prompt_prefill_deltanet_layer_4096"] = {
+        "us": round(us, 2),
+        "composition": "conv1d ring + SiLU, l2 norm, gates, chunked recurrence, rmsnorm_gated with z"}
+    del proj, st
+
     # 32-sequence batched decode, per layer: paged attention over ragged
     # lengths U[256, 16384] (16-token pages, shuffled page table) ...
     rng = np.random.default_rng(seed)
