@@ -152,19 +152,32 @@ struct ConvArgs {
 // current input times the last tap, as cpu_ops.cpp:89-129 evaluates it),
 // SiLU (cpu_ops.cpp:6-13), written to q, k or v.  Channels past C: z, a, b
 // copied to contiguous arrays.
+constexpr int kConvBatch = 16;   // tokens whose inputs one thread requests at once
+
 template <int K>
 __global__ __launch_bounds__(256) void dn_conv_prefill_kernel(ConvArgs p) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     const int extra = p.nz + 2 * p.nab;
     if (c >= p.C + extra) return;
     const int t0 = blockIdx.y * p.tpb, t1 = min(p.S, t0 + p.tpb);
+    // the inputs of kConvBatch tokens are requested together before any of
+    // them is used (the stores below may alias the rows for the compiler, so
+    // it would otherwise wait for each token's load in turn)
+    constexpr int NB = kConvBatch;
     if (c >= p.C) {
         const int cc = c - p.C;
-        for (int t = t0; t < t1; t++) {
-            const float x = p.proj[(size_t)t * p.pd + c];
-            if (cc < p.nz) p.z[(size_t)t * p.nz + cc] = x;
-            else if (cc < p.nz + p.nab) p.a[(size_t)t * p.nab + cc - p.nz] = x;
-            else p.b[(size_t)t * p.nab + cc - p.nz - p.nab] = x;
+        for (int tb = t0; tb < t1; tb += NB) {
+            float xs[NB];
+#pragma unroll
+            for (int u = 0; u < NB; u++) xs[u] = tb + u < t1 ? p.proj[(size_t)(tb + u) * p.pd + c] : 0.f;
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                const int t = tb + u;
+                if (t >= t1) break;
+                if (cc < p.nz) p.z[(size_t)t * p.nz + cc] = xs[u];
+                else if (cc < p.nz + p.nab) p.a[(size_t)t * p.nab + cc - p.nz] = xs[u];
+                else p.b[(size_t)t * p.nab + cc - p.nz - p.nab] = xs[u];
+            }
         }
         return;
     }
@@ -187,19 +200,27 @@ __global__ __launch_bounds__(256) void dn_conv_prefill_kernel(ConvArgs p) {
     float wl[K];
 #pragma unroll
     for (int j = 0; j < K; j++) wl[j] = w[j];
-    for (int t = t0; t < t1; t++) {
-        const float x = p.proj[(size_t)t * p.pd + c];
-        float sum = 0.0f;
+    for (int tb = t0; tb < t1; tb += NB) {
+        float xs[NB];
 #pragma unroll
-        for (int j = 0; j < sl; j++) sum += hist[j] * wl[j];
-        float yv = sum + x * wl[sl];
-        yv = yv / (expf(-yv) + 1.0f);
+        for (int u = 0; u < NB; u++) xs[u] = tb + u < t1 ? p.proj[(size_t)(tb + u) * p.pd + c] : 0.f;
 #pragma unroll
-        for (int j = 0; j + 1 < sl; j++) hist[j] = hist[j + 1];
-        hist[sl - 1] = x;
-        if (c < p.nqk) p.q[(size_t)t * p.nqk + c] = yv;
-        else if (c < 2 * p.nqk) p.k[(size_t)t * p.nqk + c - p.nqk] = yv;
-        else p.v[(size_t)t * (p.C - 2 * p.nqk) + c - 2 * p.nqk] = yv;
+        for (int u = 0; u < NB; u++) {
+            const int t = tb + u;
+            if (t >= t1) break;
+            const float x = xs[u];
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < sl; j++) sum += hist[j] * wl[j];
+            float yv = sum + x * wl[sl];
+            yv = yv / (expf(-yv) + 1.0f);
+#pragma unroll
+            for (int j = 0; j + 1 < sl; j++) hist[j] = hist[j + 1];
+            hist[sl - 1] = x;
+            if (c < p.nqk) p.q[(size_t)t * p.nqk + c] = yv;
+            else if (c < 2 * p.nqk) p.k[(size_t)t * p.nqk + c - p.nqk] = yv;
+            else p.v[(size_t)t * (p.C - 2 * p.nqk) + c - 2 * p.nqk] = yv;
+        }
     }
 }
 
