@@ -64,6 +64,37 @@ __global__ __launch_bounds__(kNT) void rmsnorm_gated_kernel(float* out, const fl
     }
 }
 
+// The same for rows of at most 64 * PER elements: one wave per row, four
+// rows per workgroup, the row held in registers and its sum of squares
+// reduced inside the wave (no workgroup barrier).
+template <int PER>
+__global__ __launch_bounds__(kNT) void rmsnorm_gated_rows_kernel(float* out, const float* x, const float* z,
+                                                                 const float* w, int dim, int n_rows) {
+    const int row = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= n_rows) return;   // the whole wave leaves together
+    const size_t off = (size_t)row * dim;
+    float xv[PER], zv[PER];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int i = lane + 64 * e;
+        xv[e] = i < dim ? x[off + i] : 0.f;
+        zv[e] = i < dim ? z[off + i] : 0.f;
+        ss += xv[e] * xv[e];
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + 1e-6f);
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int i = lane + 64 * e;
+        if (i < dim) {
+            float o = (xv[e] * inv) * w[i];
+            o = o / (1.0f + expf(-zv[e]));
+            out[off + i] = o * zv[e];
+        }
+    }
+}
+
 // core/cpu_ops.cpp:82-87
 __global__ __launch_bounds__(kNT) void l2norm_kernel(float* x, int dim) {
     __shared__ float red[kNT / 64];
@@ -225,9 +256,18 @@ int anelm_rmsnorm_gated(float* out, const float* x, const float* z, const float*
     ANELM_NONNULL(weight);
     ANELM_REQUIRE(dim > 0 && n_rows >= 0, "rmsnorm_gated: dim %d rows %d", dim, n_rows);
     if (n_rows == 0) return ANELM_OK;
-    hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(n_rows), dim3(kNT), 0, as_stream(stream), out, x,
-                       z, weight, dim);
-    ANELM_LAUNCHED("rmsnorm_gated_kernel");
+    hipStream_t st = as_stream(stream);
+    const dim3 rgrid((unsigned)((n_rows + kNT / 64 - 1) / (kNT / 64)));
+    if (dim <= 128) {
+        hipLaunchKernelGGL(rmsnorm_gated_rows_kernel<2>, rgrid, dim3(kNT), 0, st, out, x, z, weight, dim, n_rows);
+        ANELM_LAUNCHED("rmsnorm_gated_rows_kernel");
+    } else if (dim <= 256) {
+        hipLaunchKernelGGL(rmsnorm_gated_rows_kernel<4>, rgrid, dim3(kNT), 0, st, out, x, z, weight, dim, n_rows);
+        ANELM_LAUNCHED("rmsnorm_gated_rows_kernel");
+    } else {
+        hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(n_rows), dim3(kNT), 0, st, out, x, z, weight, dim);
+        ANELM_LAUNCHED("rmsnorm_gated_kernel");
+    }
     return ANELM_OK;
 }
 
