@@ -473,17 +473,41 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
             inv = 1.0f / l;
         }
         if (erow < S) {
-            // o[db][e] = output dim 32 db + 8 (e / 4) + 4 h + e % 4 of row erow
+            // o[db][e] = output dim 32 db + 8 (e / 4) + 4 h + e % 4 of row erow.
+            // The other partial's values and the gate logits of column block
+            // db + 1 are requested before the stores of block db: issued after
+            // them, each request would wait for those stores (the output may
+            // alias them as far as the compiler knows).
+            const float* grow = gate != nullptr ? gate + (size_t)erow * gtok + (size_t)h * ghead : nullptr;
+            auto fetch = [&](int db, float4 (&ov)[4], float4 (&gv)[4]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int dd = 32 * db + 8 * g4 + 4 * eh;
+                    ov[g4] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    gv[g4] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (have_other)
+                        ov[g4] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
+                    if (gate)   // (rows of any stride: four dword loads)
+                        gv[g4] = make_float4(grow[dd], grow[dd + 1], grow[dd + 2], grow[dd + 3]);
+                }
+            };
+            float4 ovn[4], gvn[4];
+            fetch(0, ovn, gvn);
 #pragma unroll
             for (int db = 0; db < DB; db++) {
+                float4 ovc[4], gvc[4];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    ovc[g4] = ovn[g4];
+                    gvc[g4] = gvn[g4];
+                }
+                if (db + 1 < DB) fetch(db + 1, ovn, gvn);
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
                     const int dd = 32 * db + 8 * g4 + 4 * eh;
                     const size_t off = ((size_t)erow * Hq + h) * D + dd;
-                    float4 ov = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (have_other)
-                        ov = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                            rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
+                    const float4 ov = ovc[g4];
                     float v0, v1, v2, v3;
                     {
                         // Either workgroup of a split block may be the one that
@@ -497,11 +521,11 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                         v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
                     }
                     if (gate) {
-                        const float* gr = gate + (size_t)erow * gtok + (size_t)h * ghead + dd;
-                        v0 = v0 / (1.0f + expf(-gr[0]));
-                        v1 = v1 / (1.0f + expf(-gr[1]));
-                        v2 = v2 / (1.0f + expf(-gr[2]));
-                        v3 = v3 / (1.0f + expf(-gr[3]));
+                        const float4 gl = gvc[g4];
+                        v0 = v0 / (1.0f + expf(-gl.x));
+                        v1 = v1 / (1.0f + expf(-gl.y));
+                        v2 = v2 / (1.0f + expf(-gl.z));
+                        v3 = v3 / (1.0f + expf(-gl.w));
                     }
                     if (OUT16) {
                         half4 hv = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
