@@ -44,17 +44,22 @@ struct PrepArgs {
     float theta, eps;
 };
 
-// One wave per (token, row): rows 0..Hq-1 are the token's q heads, the rest
-// its kv heads (with the value row converted alongside).  The norm and the
-// rotation are the decode core's (models/llm/qwen3_5.cpp:952-971): (x * inv)
-// * w with inv = 1 / sqrtf(ss / D + eps), pairs rotated without contraction.
+// One wave per (token, row), four rows of one token per workgroup (the
+// token's RoPE row is loaded once for them): rows 0..Hq-1 are the token's q
+// heads, the rest its kv heads (with the value row converted alongside).  The
+// norm and the rotation are the decode core's (models/llm/qwen3_5.cpp:952-971):
+// (x * inv) * w with inv = 1 / sqrtf(ss / D + eps), pairs rotated without
+// contraction.
+constexpr int kPrepRowsPerWg = 4;
 template <int D>
-__global__ __launch_bounds__(64) void prefill_prep_kernel(PrepArgs a) {
-    __shared__ float row[D];
+__global__ __launch_bounds__(64 * kPrepRowsPerWg) void prefill_prep_kernel(PrepArgs a) {
+    __shared__ float rows[kPrepRowsPerWg][D];
     __shared__ float cs[128], sn[128];
-    const int t = blockIdx.x, y = blockIdx.y, lane = threadIdx.x;
+    const int t = blockIdx.x, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int y = blockIdx.y * kPrepRowsPerWg + wv;
+    const bool live = y < a.Hq + a.Hkv;   // (a wave past the last row still meets the barriers)
     const int pos = a.pos0 + t;
-    for (int j = lane; j < a.rot_pairs; j += 64) {
+    for (int j = threadIdx.x; j < a.rot_pairs; j += 64 * kPrepRowsPerWg) {
         if (a.rope_tab != nullptr && pos < a.rope_rows) {
             cs[j] = a.rope_tab[(size_t)pos * 2 * a.rot_pairs + j];
             sn[j] = a.rope_tab[(size_t)pos * 2 * a.rot_pairs + a.rot_pairs + j];
@@ -68,39 +73,49 @@ __global__ __launch_bounds__(64) void prefill_prep_kernel(PrepArgs a) {
     }
     const bool isq = y < a.Hq;
     const int kvh = y - a.Hq;
-    const float* src = isq ? a.q_gate + t * a.qs + (long)y * 2 * D : a.k + t * a.ks + (long)kvh * D;
-    const float* w = isq ? a.q_norm_w : a.k_norm_w;
+    float* row = rows[wv];
     constexpr int E = D / 64;
-    float x[E];
+    float x[E], vv[E];
+    if (live) {
+        const float* src = isq ? a.q_gate + t * a.qs + (long)y * 2 * D : a.k + t * a.ks + (long)kvh * D;
+        const float* w = isq ? a.q_norm_w : a.k_norm_w;
 #pragma unroll
-    for (int e = 0; e < E; e++) x[e] = src[lane + 64 * e];
-    if (w != nullptr) {
-        float ss = 0.f;
+        for (int e = 0; e < E; e++) x[e] = src[lane + 64 * e];
+        if (!isq) {
+            const float* vs = a.v + t * a.ks + (long)kvh * D;
 #pragma unroll
-        for (int e = 0; e < E; e++) ss += x[e] * x[e];
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+            for (int e = 0; e < E; e++) vv[e] = vs[lane + 64 * e];
+        }
+        if (w != nullptr) {
+            float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; e++) x[e] = (x[e] * inv) * w[lane + 64 * e];
+            for (int e = 0; e < E; e++) ss += x[e] * x[e];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+            for (int e = 0; e < E; e++) x[e] = (x[e] * inv) * w[lane + 64 * e];
+        }
+#pragma unroll
+        for (int e = 0; e < E; e++) row[lane + 64 * e] = x[e];
     }
-#pragma unroll
-    for (int e = 0; e < E; e++) row[lane + 64 * e] = x[e];
     __syncthreads();
-    for (int j = lane; j < a.rot_pairs; j += 64) {
-        const int i0 = a.rope_mode == 0 ? 2 * j : j;
-        const int i1 = a.rope_mode == 0 ? 2 * j + 1 : j + a.rot_pairs;
-        const float v0 = row[i0], v1 = row[i1];
-        rotate_pair(row[i0], row[i1], v0, v1, cs[j], sn[j]);
+    if (live) {
+        for (int j = lane; j < a.rot_pairs; j += 64) {
+            const int i0 = a.rope_mode == 0 ? 2 * j : j;
+            const int i1 = a.rope_mode == 0 ? 2 * j + 1 : j + a.rot_pairs;
+            const float v0 = row[i0], v1 = row[i1];
+            rotate_pair(row[i0], row[i1], v0, v1, cs[j], sn[j]);
+        }
     }
     __syncthreads();
+    if (!live) return;
     uint16_t* dst = isq ? a.qh + ((size_t)t * a.Hq + y) * D : a.kall + ((size_t)(a.len0 + t) * a.Hkv + kvh) * D;
 #pragma unroll
     for (int e = 0; e < E; e++) dst[lane + 64 * e] = f2h(row[lane + 64 * e]);
     if (!isq) {
-        const float* vs = a.v + t * a.ks + (long)kvh * D;
         uint16_t* vd = a.vall + ((size_t)(a.len0 + t) * a.Hkv + kvh) * D;
 #pragma unroll
-        for (int e = 0; e < E; e++) vd[lane + 64 * e] = f2h(vs[lane + 64 * e]);
+        for (int e = 0; e < E; e++) vd[lane + 64 * e] = f2h(vv[e]);
     }
 }
 
@@ -293,9 +308,9 @@ extern "C" int anelm_full_attn_prefill(float* out, const float* q_gate, const fl
     }
     PrepArgs a{q_gate, k, v, qs, ks, q_norm_w, k_norm_w, rope_table, rope_table ? rope_rows : 0, qh, kall, vall,
                S, n_heads, n_kv_heads, len0, pos0, rot_dim / 2, rope_mode, theta, eps};
-    const dim3 pg(S, n_heads + n_kv_heads);
-    if (D == 256) hipLaunchKernelGGL(prefill_prep_kernel<256>, pg, dim3(64), 0, st, a);
-    else hipLaunchKernelGGL(prefill_prep_kernel<128>, pg, dim3(64), 0, st, a);
+    const dim3 pg(S, (n_heads + n_kv_heads + kPrepRowsPerWg - 1) / kPrepRowsPerWg);
+    if (D == 256) hipLaunchKernelGGL(prefill_prep_kernel<256>, pg, dim3(64 * kPrepRowsPerWg), 0, st, a);
+    else hipLaunchKernelGGL(prefill_prep_kernel<128>, pg, dim3(64 * kPrepRowsPerWg), 0, st, a);
     ANELM_LAUNCHED("prefill_prep_kernel");
     // rows whose ring overflowed inside the prompt see the last `cap` keys
     const int win = L > cap ? cap : 0;
