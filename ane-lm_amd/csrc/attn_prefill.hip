@@ -221,7 +221,7 @@ __device__ __forceinline__ int block_tiles(int blk, int S, int qoff) {
 // Query row r is key qoff + r of the L keys (the keys before qoff are a
 // cached prefix) and attends keys 0 .. qoff + r.  With gate, output row
 // (r, h) is multiplied by sigmoid(gate[r * gtok + h * ghead + d]).
-template <bool OUT16>
+template <bool OUT16, bool GATE>
 __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Float16* q, const _Float16* k,
                                                            const _Float16* v, float* part, uint32_t* ctr, int S,
                                                            int L, int qoff, int Hq, int Hkv,
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
             // db + 1 are requested before the stores of block db: issued after
             // them, each request would wait for those stores (the output may
             // alias them as far as the compiler knows).
-            const float* grow = gate != nullptr ? gate + (size_t)erow * gtok + (size_t)h * ghead : nullptr;
+            const float* grow = GATE ? gate + (size_t)erow * gtok + (size_t)h * ghead : nullptr;
             auto fetch = [&](int db, float4 (&ov)[4], float4 (&gv)[4]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                     if (have_other)
                         ov[g4] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                                                 rot, (((w * DB + db) * 4 + g4) * 256 + ln * 4) * 4, 0, kSc1));
-                    if (gate)   // (rows of any stride: four dword loads)
+                    if constexpr (GATE)   // (rows of any stride: four dword loads)
                         gv[g4] = make_float4(grow[dd], grow[dd + 1], grow[dd + 2], grow[dd + 3]);
                 }
             };
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(kGNT) void prefill_g4_kernel(void* out, const _Floa
                         v2 = (o[db][4 * g4 + 2] * a0 + ov.z * a1) * inv;
                         v3 = (o[db][4 * g4 + 3] * a0 + ov.w * a1) * inv;
                     }
-                    if (gate) {
+                    if constexpr (GATE) {
                         const float4 gl = gvc[g4];
                         v0 = v0 / (1.0f + expf(-gl.x));
                         v1 = v1 / (1.0f + expf(-gl.y));
@@ -550,24 +550,26 @@ int launch_prefill_g4(void* out, bool out16, const void* q, const void* k, const
     if (!part) return ANELM_ENOMEM;
     uint32_t* ctr = counters(units, kCtrPrefill, st);   // zeroed; each call leaves them zeroed
     if (!ctr) return ANELM_ERANGE;
+    // the gated launches (prompt prefill through the layer core) are their own
+    // instantiation: the bare core carries no gate code
+    using K = void (*)(void*, const _Float16*, const _Float16*, const _Float16*, float*, uint32_t*, int, int, int,
+                       int, int, const float*, int, int);
+    static const K kern[2][2] = {{prefill_g4_kernel<false, false>, prefill_g4_kernel<false, true>},
+                                 {prefill_g4_kernel<true, false>, prefill_g4_kernel<true, true>}};
     static bool attr_set = false;
     if (!attr_set) {
-        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_g4_kernel<true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGLds));
-        ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_g4_kernel<false>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kGLds));
+        for (int o = 0; o < 2; o++)
+            for (int g = 0; g < 2; g++)
+                ANELM_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern[o][g]),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, kGLds));
         attr_set = true;
     }
     const _Float16* qh = static_cast<const _Float16*>(q);
     const _Float16* kh = static_cast<const _Float16*>(k);
     const _Float16* vh = static_cast<const _Float16*>(v);
     const dim3 grid(2 * units);
-    if (out16)
-        hipLaunchKernelGGL(prefill_g4_kernel<true>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vh, part, ctr, S, L,
-                           qoff, Hq, Hkv, gate, gtok, ghead);
-    else
-        hipLaunchKernelGGL(prefill_g4_kernel<false>, grid, dim3(kGNT), kGLds, st, out, qh, kh, vh, part, ctr, S, L,
-                           qoff, Hq, Hkv, gate, gtok, ghead);
+    hipLaunchKernelGGL(kern[out16 ? 1 : 0][gate != nullptr ? 1 : 0], grid, dim3(kGNT), kGLds, st, out, qh, kh, vh,
+                       part, ctr, S, L, qoff, Hq, Hkv, gate, gtok, ghead);
     ANELM_LAUNCHED("prefill_g4_kernel");
     return ANELM_OK;
 }
