@@ -95,6 +95,24 @@ __global__ __launch_bounds__(kNT) void rmsnorm_gated_rows_kernel(float* out, con
     }
 }
 
+// The 128-element rows of a DeltaNet head (8-byte aligned): lane l holds
+// elements 2l, 2l + 1, one 8-byte load per operand.
+__global__ __launch_bounds__(kNT) void rmsnorm_gated_rows128_kernel(float* out, const float* x, const float* z,
+                                                                    const float* w, int n_rows) {
+    const int row = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= n_rows) return;   // the whole wave leaves together
+    const size_t off = (size_t)row * 128 + 2 * lane;
+    const float2 xv = *reinterpret_cast<const float2*>(x + off);
+    const float2 zv = *reinterpret_cast<const float2*>(z + off);
+    const float2 wv = *reinterpret_cast<const float2*>(w + 2 * lane);
+    const float ss = wave_sum(xv.x * xv.x + xv.y * xv.y);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+    float o0 = (xv.x * inv) * wv.x, o1 = (xv.y * inv) * wv.y;
+    o0 = o0 / (1.0f + expf(-zv.x));
+    o1 = o1 / (1.0f + expf(-zv.y));
+    *reinterpret_cast<float2*>(out + off) = make_float2(o0 * zv.x, o1 * zv.y);
+}
+
 // core/cpu_ops.cpp:82-87
 __global__ __launch_bounds__(kNT) void l2norm_kernel(float* x, int dim) {
     __shared__ float red[kNT / 64];
@@ -258,7 +276,12 @@ int anelm_rmsnorm_gated(float* out, const float* x, const float* z, const float*
     if (n_rows == 0) return ANELM_OK;
     hipStream_t st = as_stream(stream);
     const dim3 rgrid((unsigned)((n_rows + kNT / 64 - 1) / (kNT / 64)));
-    if (dim <= 128) {
+    const bool al8 = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(x) |
+                       reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(weight)) & 7) == 0;
+    if (dim == 128 && al8) {
+        hipLaunchKernelGGL(rmsnorm_gated_rows128_kernel, rgrid, dim3(kNT), 0, st, out, x, z, weight, n_rows);
+        ANELM_LAUNCHED("rmsnorm_gated_rows128_kernel");
+    } else if (dim <= 128) {
         hipLaunchKernelGGL(rmsnorm_gated_rows_kernel<2>, rgrid, dim3(kNT), 0, st, out, x, z, weight, dim, n_rows);
         ANELM_LAUNCHED("rmsnorm_gated_rows_kernel");
     } else if (dim <= 256) {
